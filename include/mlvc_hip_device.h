@@ -1,0 +1,137 @@
+/*
+ * Thin device C ABI of the MI355X (gfx950) backend: memory, streams,
+ * events, hipGraph capture and the hand-written HIP kernels of the FP16
+ * conv-graph path.
+ *
+ * Plain C, POD arguments, opaque handles; the C++20 host never includes a
+ * HIP header. This is the counterpart of the reference driver backend's
+ * device boundary: the Driver-API wrapper (backends/driver_cubin/src/
+ * driver.cpp:10-490, include/mlvc/driver_cubin/driver.hpp:145-190, handles
+ * isolated in include/mlvc/driver_cubin/abi.hpp:1-34) and its
+ * `extern "C" __global__` kernels launched by cuLaunchKernel
+ * (driver.cpp:420-434). Each kernel entry point names the reference kernel
+ * whose role it takes.
+ *
+ * All tensors are FP16 (raw binary16), channel-first NCHW, N = 1..n.
+ * Every function returns 0 on success and -1 on failure; the message is
+ * available from mlvc_hip_last_error() on the calling thread.
+ */
+#ifndef MLVC_HIP_DEVICE_H
+#define MLVC_HIP_DEVICE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct mlvc_hip_stream_s* mlvc_hip_stream;  /* hipStream_t */
+typedef struct mlvc_hip_event_s* mlvc_hip_event;    /* hipEvent_t */
+typedef struct mlvc_hip_graph_s* mlvc_hip_graph;    /* hipGraphExec_t */
+
+const char* mlvc_hip_last_error(void);
+
+/* ---- device, memory, streams (driver.cpp:10-140 DriverState/buffers) ---- */
+int mlvc_hip_device_count(int* count);
+int mlvc_hip_set_device(int device);
+int mlvc_hip_device_name(int device, char* buf, size_t len);
+int mlvc_hip_malloc(void** ptr, size_t bytes);
+int mlvc_hip_free(void* ptr);
+int mlvc_hip_host_alloc(void** ptr, size_t bytes); /* pinned */
+int mlvc_hip_host_free(void* ptr);
+int mlvc_hip_memcpy_h2d(void* dst, const void* src, size_t bytes, mlvc_hip_stream s);
+int mlvc_hip_memcpy_d2h(void* dst, const void* src, size_t bytes, mlvc_hip_stream s);
+int mlvc_hip_memcpy_d2d(void* dst, const void* src, size_t bytes, mlvc_hip_stream s);
+int mlvc_hip_stream_create(mlvc_hip_stream* s);
+int mlvc_hip_stream_destroy(mlvc_hip_stream s);
+int mlvc_hip_stream_synchronize(mlvc_hip_stream s);
+int mlvc_hip_event_create(mlvc_hip_event* e);
+int mlvc_hip_event_destroy(mlvc_hip_event e);
+int mlvc_hip_event_record(mlvc_hip_event e, mlvc_hip_stream s);
+int mlvc_hip_event_synchronize(mlvc_hip_event e);
+int mlvc_hip_event_elapsed_ms(mlvc_hip_event start, mlvc_hip_event stop, float* ms);
+
+/* ---- hipGraph capture/replay (driver.cpp:452-489 begin_capture/
+ *      end_capture/launch_graph; cuda_graph_executor.cpp:38-52) ---- */
+int mlvc_hip_capture_begin(mlvc_hip_stream s);
+int mlvc_hip_capture_end(mlvc_hip_stream s, mlvc_hip_graph* graph);
+int mlvc_hip_graph_launch(mlvc_hip_graph graph, mlvc_hip_stream s);
+int mlvc_hip_graph_destroy(mlvc_hip_graph graph);
+
+/* ---- convolution (groups == 1): MFMA implicit GEMM ----
+ * Replaces the reference's 1x1 GEMM kernels (pointwise_conv.cu:116-338,
+ * cutlass.cu:116-143), implicit-GEMM KxK convs (spatial_conv.cu:1-293,
+ * cutlass.cu:145-161 with its layout.cu:1-48 NCHW<->NHWC transposes) and
+ * the generic fallback (generic_conv.cu:1-82). Semantics follow
+ * backends/cpu: y = fp16(bias + sum x*w) with FP32 accumulation, then the
+ * epilogue on the rounded value (kernels_scalar.cpp:160-195).
+ *
+ * Fusions (all optional):
+ *   in_s2d_block > 1 : the conv input is SPACE_TO_DEPTH(block) of `x`, read
+ *                      through the CRD index map (x is [n, ic/b^2, ih*b, iw*b]);
+ *   x2 != NULL       : the conv input is the channel CONCAT of `x`
+ *                      (channels [0, ic_split)) and `x2` (the rest);
+ *   epilogue         : LeakyReLU(alpha) or residual ADD of `residual`;
+ *   out_d2s_block > 1: the output is written through DEPTH_TO_SPACE(block)
+ *                      (CRD), y is [n, oc/b^2, oh*b, ow*b].
+ */
+enum { MLVC_EPI_NONE = 0, MLVC_EPI_LEAKY_RELU = 1, MLVC_EPI_RESIDUAL_ADD = 2 };
+
+typedef struct mlvc_hip_conv_desc {
+    int n, ic, ih, iw;                 /* conv input geometry (after fusion maps) */
+    int oc, oh, ow;                    /* conv output geometry (before d2s) */
+    int kh, kw, stride_h, stride_w, pad_h, pad_w;
+    const void* x;
+    const void* x2;
+    int ic_split;
+    int in_s2d_block;
+    const void* packed_w;              /* from mlvc_hip_conv_pack */
+    const float* bias;                 /* fp32 widening of the fp16 bias, length mlvc_hip_conv_bias_len */
+    int epilogue;
+    float alpha;
+    const void* residual;              /* [n, oc, oh, ow] */
+    void* y;
+    int out_d2s_block;
+    int variant;                       /* tile configuration; set by mlvc_hip_conv_plan */
+} mlvc_hip_conv_desc;
+
+/* Chooses the kernel variant for the geometry (sets desc->variant). */
+int mlvc_hip_conv_plan(mlvc_hip_conv_desc* desc);
+const char* mlvc_hip_conv_variant_name(int variant);
+size_t mlvc_hip_conv_packed_bytes(const mlvc_hip_conv_desc* desc);
+size_t mlvc_hip_conv_bias_len(const mlvc_hip_conv_desc* desc);
+/* Host-side repack of OIHW fp16 weights into the variant's MFMA fragment
+ * order (reference role: pack_conv_weights_f16p16x1bias,
+ * kernels_scalar.cpp:14-56, and mlvc_oihw_to_krsc_fp16, layout.cu). */
+int mlvc_hip_conv_pack(const mlvc_hip_conv_desc* desc, const uint16_t* w_oihw, void* dst_host);
+int mlvc_hip_conv_launch(const mlvc_hip_conv_desc* desc, mlvc_hip_stream s);
+
+/* ---- depthwise KxK (groups == C == OC) ----
+ * Replaces mlvc_depthwise_conv_fp16{,_pair,_quad} (depthwise_conv.cu:1-173);
+ * semantics of backends/cpu avx2_depthwise3x3_s1p1 (kernels_x86_avx2.cpp:
+ * 237-302): FP32 accumulator seeded with the bias, taps in (ky,kx) order,
+ * out-of-range taps skipped. `w` is [c, 1, kh, kw] fp16, `bias` fp32 [c]. */
+int mlvc_hip_depthwise(const void* x, const uint16_t* w, const float* bias, void* y, int n, int c,
+                       int ih, int iw, int oh, int ow, int kh, int kw, int stride_h, int stride_w,
+                       int pad_h, int pad_w, mlvc_hip_stream s);
+
+/* ---- pixel layout, CRD (tensor_ops.cu:62-116, mode 1) ----
+ * DEPTH_TO_SPACE: in [n, c*b*b, h, w] -> out [n, c, h*b, w*b].
+ * SPACE_TO_DEPTH: in [n, c, h, w] -> out [n, c*b*b, h/b, w/b]. */
+int mlvc_hip_depth_to_space(const void* x, void* y, int n, int in_c, int h, int w, int block, mlvc_hip_stream s);
+int mlvc_hip_space_to_depth(const void* x, void* y, int n, int in_c, int h, int w, int block, mlvc_hip_stream s);
+
+/* ---- elementwise (elementwise.cu:1-80): y = fp16(op(fp32 inputs)) ---- */
+int mlvc_hip_leaky_relu(const void* x, void* y, size_t count, float alpha, mlvc_hip_stream s);
+int mlvc_hip_add(const void* a, const void* b, void* y, size_t count, mlvc_hip_stream s);
+/* Channel concat of two NCHW tensors (tensor_ops.cu concat copy, axis 1). */
+int mlvc_hip_concat_channels(const void* a, int ca, const void* b, int cb, void* y, int n, size_t hw,
+                             mlvc_hip_stream s);
+/* Zero fill by kernel (safe inside captured graphs). */
+int mlvc_hip_zero(void* y, size_t bytes, mlvc_hip_stream s);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

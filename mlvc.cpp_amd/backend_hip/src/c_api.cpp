@@ -1,0 +1,245 @@
+// C ABI over mlvc::InferenceBackend (include/mlvc_hip_backend.h).
+// Exceptions become -1 plus a per-thread message, as in the reference's
+// codec/src/c_api.cpp:71-88.
+
+#include "hip_backend.hpp"
+#include "mlvc/runtime/graph_builder.hpp"
+#include "mlvc_hip_backend.h"
+
+#include <cstring>
+#include <filesystem>
+#include <stdexcept>
+#include <string>
+
+struct mlvc_backend {
+    std::unique_ptr<mlvc::InferenceBackend> impl;
+    std::string name;
+    std::string model_dir;
+};
+
+namespace {
+
+thread_local std::string g_error;
+
+template <typename F>
+int guard(F&& fn)
+{
+    try {
+        fn();
+        return 0;
+    } catch (const std::exception& e) {
+        g_error = e.what();
+        return -1;
+    }
+}
+
+mlvc::hip_backend::HipBackend& hip(mlvc_backend* b)
+{
+    auto* h = dynamic_cast<mlvc::hip_backend::HipBackend*>(b->impl.get());
+    if (!h) throw std::runtime_error("not a hip backend: " + b->name);
+    return *h;
+}
+
+std::vector<std::vector<std::int64_t>> shapes(mlvc_backend* b, bool outputs)
+{
+    return hip(b).io_shapes(outputs);
+}
+
+void copy_str(const std::string& s, char* buf, std::size_t len)
+{
+    if (!buf || len == 0) return;
+    const std::size_t n = std::min(len - 1, s.size());
+    std::memcpy(buf, s.data(), n);
+    buf[n] = '\0';
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* mlvc_backend_last_error(void) { return g_error.c_str(); }
+
+int mlvc_backend_create(const char* backend_name, const char* model_dir, int device_id, int num_threads, mlvc_backend** out)
+{
+    return guard([&] {
+        mlvc::BackendOptions o;
+        o.backend_name = backend_name ? backend_name : "";
+        o.model_dir = model_dir ? model_dir : "";
+        o.device_id = device_id;
+        o.num_threads = num_threads;
+        auto b = std::make_unique<mlvc_backend>();
+        b->impl = mlvc::create_backend(o);
+        b->name = std::string(b->impl->name());
+        b->model_dir = o.model_dir;
+        *out = b.release();
+    });
+}
+
+void mlvc_backend_destroy(mlvc_backend* backend) { delete backend; }
+
+const char* mlvc_backend_name(const mlvc_backend* backend) { return backend->name.c_str(); }
+
+int mlvc_backend_load(mlvc_backend* backend, const char* model_name, const int64_t* bindings, int n_bindings)
+{
+    return guard([&] {
+        // StateTensorBinding carries the bound tensor's shape; take it from
+        // the graph's own input descriptor.
+        mlvc::ModelExecutionConfig cfg;
+        if (n_bindings > 0) {
+            const auto g = mlvc::aot::load_aot_graph(std::filesystem::path(backend->model_dir), model_name);
+            for (int i = 0; i < n_bindings; ++i) {
+                mlvc::StateTensorBinding b;
+                b.input_index = static_cast<std::size_t>(bindings[2 * i]);
+                b.output_index = static_cast<std::size_t>(bindings[2 * i + 1]);
+                if (b.input_index >= g.descriptor.inputs.size())
+                    throw std::runtime_error("state binding index out of range");
+                b.shape = g.descriptor.tensors[g.descriptor.inputs[b.input_index]].shape;
+                cfg.state_bindings.push_back(b);
+            }
+        }
+        backend->impl->load(model_name, cfg);
+    });
+}
+
+int mlvc_backend_io_count(mlvc_backend* backend, int is_output, int* count)
+{
+    return guard([&] { *count = static_cast<int>(shapes(backend, is_output != 0).size()); });
+}
+
+int mlvc_backend_io_shape(mlvc_backend* backend, int is_output, int index, int64_t* shape4, int* rank)
+{
+    return guard([&] {
+        const auto s = shapes(backend, is_output != 0).at(static_cast<std::size_t>(index));
+        *rank = static_cast<int>(s.size());
+        for (std::size_t i = 0; i < s.size() && i < 4; ++i) shape4[i] = s[i];
+    });
+}
+
+int mlvc_backend_run(mlvc_backend* backend, const uint16_t* const* inputs, uint16_t* const* outputs)
+{
+    return guard([&] {
+        const auto ins = shapes(backend, false);
+        std::vector<mlvc::Tensor> ts;
+        for (std::size_t i = 0; i < ins.size(); ++i) {
+            mlvc::Tensor t;
+            t.shape = ins[i];
+            std::size_t n = 1;
+            for (auto d : t.shape) n *= static_cast<std::size_t>(d);
+            t.data = std::vector<mlvc::Float16Storage>(inputs[i], inputs[i] + n);
+            ts.push_back(std::move(t));
+        }
+        const auto outs = backend->impl->run(ts);
+        for (std::size_t i = 0; i < outs.size(); ++i) std::memcpy(outputs[i], outs[i].raw_data(), outs[i].byte_size());
+    });
+}
+
+int mlvc_backend_reset_state(mlvc_backend* backend)
+{
+    return guard([&] { backend->impl->reset_state(); });
+}
+
+int mlvc_backend_available(char* buf, size_t len)
+{
+    return guard([&] {
+        std::string s;
+        for (const auto& n : mlvc::available_backends()) s += (s.empty() ? "" : ",") + n;
+        copy_str(s, buf, len);
+    });
+}
+
+int mlvc_hip_backend_upload_inputs(mlvc_backend* backend, const uint16_t* const* inputs)
+{
+    return guard([&] {
+        const std::size_t n = shapes(backend, false).size();
+        hip(backend).upload_inputs(std::vector<const std::uint16_t*>(inputs, inputs + n));
+    });
+}
+
+int mlvc_hip_backend_time_frames(mlvc_backend* backend, int frames, float* ms)
+{
+    return guard([&] { *ms = hip(backend).time_frames(frames); });
+}
+
+int mlvc_hip_backend_download_outputs(mlvc_backend* backend, uint16_t* const* outputs)
+{
+    return guard([&] {
+        const std::size_t n = shapes(backend, true).size();
+        hip(backend).download_outputs(std::vector<std::uint16_t*>(outputs, outputs + n));
+    });
+}
+
+int mlvc_hip_backend_launch_count(mlvc_backend* backend, int* count)
+{
+    return guard([&] { *count = static_cast<int>(hip(backend).launch_count()); });
+}
+
+int mlvc_hip_backend_launch_info(mlvc_backend* backend, int index, char* name, size_t name_len, char* kind, size_t kind_len,
+                                 double* flops, double* bytes)
+{
+    return guard([&] {
+        const auto info = hip(backend).launch_info(static_cast<std::size_t>(index));
+        copy_str(info.name, name, name_len);
+        copy_str(info.kind, kind, kind_len);
+        *flops = info.flops;
+        *bytes = info.bytes;
+    });
+}
+
+int mlvc_hip_backend_time_launch(mlvc_backend* backend, int index, int reps, float* ms_per_launch)
+{
+    return guard([&] { *ms_per_launch = hip(backend).time_launch(static_cast<std::size_t>(index), reps); });
+}
+
+int mlvc_aot_inspect(const char* model_dir, const char* model_name, int* nodes, int* tensors, uint64_t* arena_bytes,
+                     uint64_t* weights_bytes)
+{
+    return guard([&] {
+        const auto g = mlvc::aot::load_aot_graph(std::filesystem::path(model_dir), model_name);
+        *nodes = static_cast<int>(g.descriptor.nodes.size());
+        *tensors = static_cast<int>(g.descriptor.tensors.size()) - 1;
+        *arena_bytes = g.descriptor.arena_bytes;
+        *weights_bytes = g.descriptor.weights_bytes;
+    });
+}
+
+int mlvc_synth_configs(char* buf, size_t len)
+{
+    return guard([&] {
+        std::string s;
+        for (const auto& n : mlvc::synth::synthetic_configs()) s += (s.empty() ? "" : ",") + n;
+        copy_str(s, buf, len);
+    });
+}
+
+int mlvc_synth_write(const char* config, const char* out_dir, uint64_t seed)
+{
+    return guard([&] {
+        mlvc::synth::SyntheticModel info;
+        const auto g = mlvc::synth::build_synthetic(config, seed, &info);
+        g.write_directory(out_dir, info.model_name, std::string("synthetic/") + config);
+    });
+}
+
+int mlvc_synth_input(const char* config, int index, int frame, uint64_t seed, uint16_t* dst, size_t count)
+{
+    return guard([&] {
+        const auto v = mlvc::synth::synthetic_input(config, static_cast<std::size_t>(index), frame, seed);
+        if (v.size() != count) throw std::runtime_error("synthetic input size mismatch");
+        std::memcpy(dst, v.data(), count * 2);
+    });
+}
+
+int mlvc_synth_bindings(const char* config, int64_t* pairs, int max_pairs, int* n_pairs, int* frames)
+{
+    return guard([&] {
+        const auto info = mlvc::synth::synthetic_info(config);
+        *n_pairs = static_cast<int>(info.state_bindings.size());
+        *frames = info.frames;
+        for (int i = 0; i < *n_pairs && i < max_pairs; ++i) {
+            pairs[2 * i] = static_cast<int64_t>(info.state_bindings[static_cast<std::size_t>(i)].input_index);
+            pairs[2 * i + 1] = static_cast<int64_t>(info.state_bindings[static_cast<std::size_t>(i)].output_index);
+        }
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,784 @@
+// "hip" backend: graph lowering, fusion, memory planning and hipGraph replay.
+//
+// Behavioural references (nothing of the CUDA code is reused):
+//   * lifecycle and run() checks: backends/cpu/src/execution_plan.cpp:1623-
+//     1675 and backends/driver_cubin/src/cuda_graph_executor.cpp:90-154;
+//   * conv classification (groups == 1 vs depthwise, error on other
+//     grouped convs): execution_plan.cpp:410-462;
+//   * conv epilogue fusion rule (LeakyReLU / same-shape non-initializer ADD
+//     after a conv whose output has one consumer and is not a graph output):
+//     fusion_matcher.cpp:352-411;
+//   * state bindings (feature_out(t) -> ref_in(t+1), zeroed by reset_state):
+//     backend.hpp:34-46, execution_plan.cpp:349-369/806-816/1033-1042. The
+//     driver backend aliases the state output onto its input and therefore
+//     requires the final node to produce it (graph_validator.cpp:11-46);
+//     this backend instead keeps two state buffers and captures one
+//     hipGraph per parity, so the state output may be produced anywhere;
+//   * one graph replay per frame: cuda_graph_executor.cpp:38-52.
+// MI355X-specific lowering on top of the reference rules: SPACE_TO_DEPTH and
+// channel CONCAT feeding a conv are folded into the conv's input staging,
+// DEPTH_TO_SPACE consuming a conv is folded into its store, and device
+// memory is re-planned over the fused launch schedule.
+
+#include "hip_backend.hpp"
+
+#include "mlvc/core/half.hpp"
+#include "mlvc_hip_device.h"
+
+#include <algorithm>
+#include <cstring>
+#include <map>
+#include <set>
+#include <stdexcept>
+
+namespace mlvc::hip_backend {
+namespace {
+
+using aot::Op;
+using aot::TensorId;
+
+[[noreturn]] void fail(const std::string& what) { throw std::runtime_error("hip: " + what); }
+
+void hip_check(int rc, const char* what)
+{
+    if (rc != 0) fail(std::string(what) + ": " + mlvc_hip_last_error());
+}
+
+std::size_t elem_count(const std::vector<std::int64_t>& s)
+{
+    std::size_t n = 1;
+    for (auto d : s) n *= static_cast<std::size_t>(d);
+    return n;
+}
+
+struct DeviceMem {
+    void* ptr = nullptr;
+    DeviceMem() = default;
+    explicit DeviceMem(std::size_t bytes) { hip_check(mlvc_hip_malloc(&ptr, bytes), "device allocation"); }
+    DeviceMem(const DeviceMem&) = delete;
+    DeviceMem& operator=(const DeviceMem&) = delete;
+    DeviceMem(DeviceMem&& o) noexcept : ptr(o.ptr) { o.ptr = nullptr; }
+    DeviceMem& operator=(DeviceMem&& o) noexcept
+    {
+        std::swap(ptr, o.ptr);
+        return *this;
+    }
+    ~DeviceMem()
+    {
+        if (ptr) mlvc_hip_free(ptr);
+    }
+};
+
+struct HostMem {
+    void* ptr = nullptr;
+    HostMem() = default;
+    explicit HostMem(std::size_t bytes) { hip_check(mlvc_hip_host_alloc(&ptr, bytes), "pinned allocation"); }
+    HostMem(const HostMem&) = delete;
+    HostMem& operator=(const HostMem&) = delete;
+    HostMem(HostMem&& o) noexcept : ptr(o.ptr) { o.ptr = nullptr; }
+    HostMem& operator=(HostMem&& o) noexcept
+    {
+        std::swap(ptr, o.ptr);
+        return *this;
+    }
+    ~HostMem()
+    {
+        if (ptr) mlvc_hip_host_free(ptr);
+    }
+};
+
+struct Launch {
+    enum Kind { kConv, kDepthwise, kLeaky, kAdd, kD2S, kS2D, kConcat } kind = kConv;
+    std::string name, kind_name;
+    TensorId x = 0, x2 = 0, res = 0, y = 0;  // tensors read (x, x2, res) and written (y)
+    mlvc_hip_conv_desc conv{};
+    DeviceMem packed, bias;
+    int n = 0, c = 0, ih = 0, iw = 0, oh = 0, ow = 0, kh = 0, kw = 0, sh = 1, sw = 1, ph = 0, pw = 0;
+    int block = 0, ca = 0, cb = 0;
+    std::size_t count = 0, hw = 0;
+    float alpha = 0.0F;
+    double flops = 0.0, bytes = 0.0;
+};
+
+}  // namespace
+
+class Plan {
+public:
+    Plan(const BackendOptions& options, const std::string& model, const ModelExecutionConfig& config)
+        : device_(options.device_id)
+    {
+        int count = 0;
+        hip_check(mlvc_hip_device_count(&count), "device query");
+        if (count <= device_) fail("HIP device " + std::to_string(device_) + " is not available");
+        hip_check(mlvc_hip_set_device(device_), "set device");
+        const auto assets = resolve_model_asset_reader(options.model_dir, options.asset_reader);
+        graph_ = aot::load_aot_graph(*assets, model);
+        hip_check(mlvc_hip_stream_create(&stream_), "stream creation");
+        hip_check(mlvc_hip_event_create(&ev0_), "event creation");
+        hip_check(mlvc_hip_event_create(&ev1_), "event creation");
+        bind_state(config);
+        lower();
+        plan_memory();
+        allocate_io();
+        upload_parameters();
+        capture();
+        initialized_ = bindings_.empty();
+    }
+
+    ~Plan()
+    {
+        for (auto g : graphs_) mlvc_hip_graph_destroy(g);
+        mlvc_hip_event_destroy(ev0_);
+        mlvc_hip_event_destroy(ev1_);
+        mlvc_hip_stream_destroy(stream_);
+    }
+
+    std::vector<std::vector<std::int64_t>> io_shapes(bool outputs) const
+    {
+        std::vector<std::vector<std::int64_t>> s;
+        for (TensorId id : outputs ? ext_out_ : ext_in_) s.push_back(desc(id).shape);
+        return s;
+    }
+
+    void reset_state()
+    {
+        select();
+        for (auto& b : bindings_)
+            for (auto& buf : b.buf) hip_check(mlvc_hip_zero(buf.ptr, b.bytes, stream_), "state reset");
+        hip_check(mlvc_hip_stream_synchronize(stream_), "stream sync");
+        parity_ = 0;
+        initialized_ = true;
+    }
+
+    std::vector<Tensor> run(const std::vector<Tensor>& inputs)
+    {
+        if (!initialized_) fail("reset_state() must be called before run()");
+        if (inputs.size() != ext_in_.size()) fail("graph input count mismatch");
+        select();
+        for (std::size_t i = 0; i < inputs.size(); ++i) {
+            const Tensor& t = inputs[i];
+            t.validate();
+            const auto& d = desc(ext_in_[i]);
+            if (t.shape != d.shape || t.data_type() != TensorDataType::kFloat16 || t.byte_size() != aot::tensor_bytes(d))
+                fail("graph input shape, dtype, or byte size mismatch");
+            std::memcpy(in_stage_[i].ptr, t.raw_data(), t.byte_size());
+            hip_check(mlvc_hip_memcpy_h2d(input_buf_.at(ext_in_[i]).ptr, in_stage_[i].ptr, t.byte_size(), stream_), "input upload");
+        }
+        hip_check(mlvc_hip_graph_launch(graphs_[static_cast<std::size_t>(parity_)], stream_), "graph launch");
+        enqueue_downloads();
+        hip_check(mlvc_hip_stream_synchronize(stream_), "stream sync");
+        std::vector<Tensor> out;
+        for (std::size_t i = 0; i < ext_out_.size(); ++i) {
+            const auto& d = desc(ext_out_[i]);
+            Tensor t;
+            t.name = d.name;
+            t.shape = d.shape;
+            std::vector<Float16Storage> v(elem_count(d.shape));
+            std::memcpy(v.data(), out_stage_[i].ptr, v.size() * 2);
+            t.data = std::move(v);
+            out.push_back(std::move(t));
+        }
+        advance();
+        return out;
+    }
+
+    void upload_inputs(const std::vector<const std::uint16_t*>& inputs)
+    {
+        if (inputs.size() != ext_in_.size()) fail("graph input count mismatch");
+        select();
+        for (std::size_t i = 0; i < inputs.size(); ++i)
+            hip_check(mlvc_hip_memcpy_h2d(input_buf_.at(ext_in_[i]).ptr, inputs[i], aot::tensor_bytes(desc(ext_in_[i])), stream_),
+                      "input upload");
+        hip_check(mlvc_hip_stream_synchronize(stream_), "stream sync");
+    }
+
+    float time_frames(int frames)
+    {
+        if (!initialized_) fail("reset_state() must be called before running frames");
+        select();
+        hip_check(mlvc_hip_event_record(ev0_, stream_), "event record");
+        for (int f = 0; f < frames; ++f) {
+            hip_check(mlvc_hip_graph_launch(graphs_[static_cast<std::size_t>(parity_)], stream_), "graph launch");
+            advance();
+        }
+        hip_check(mlvc_hip_event_record(ev1_, stream_), "event record");
+        hip_check(mlvc_hip_event_synchronize(ev1_), "event sync");
+        float ms = 0.0F;
+        hip_check(mlvc_hip_event_elapsed_ms(ev0_, ev1_, &ms), "event timing");
+        return ms;
+    }
+
+    void download_outputs(const std::vector<std::uint16_t*>& outputs)
+    {
+        if (outputs.size() != ext_out_.size()) fail("graph output count mismatch");
+        select();
+        // Outputs of the last frame were produced with the previous parity.
+        const int produced = bindings_.empty() ? 0 : parity_ ^ 1;
+        for (std::size_t i = 0; i < outputs.size(); ++i)
+            hip_check(mlvc_hip_memcpy_d2h(outputs[i], ptr(ext_out_[i], produced), aot::tensor_bytes(desc(ext_out_[i])), stream_),
+                      "output download");
+        hip_check(mlvc_hip_stream_synchronize(stream_), "stream sync");
+    }
+
+    std::size_t launch_count() const { return launches_.size(); }
+
+    LaunchInfo launch_info(std::size_t i) const
+    {
+        const Launch& l = *launches_.at(i);
+        return {l.name, l.kind_name, l.flops, l.bytes};
+    }
+
+    float time_launch(std::size_t i, int reps)
+    {
+        select();
+        Launch& l = *launches_.at(i);
+        enqueue_one(l, 0);
+        hip_check(mlvc_hip_event_record(ev0_, stream_), "event record");
+        for (int r = 0; r < reps; ++r) enqueue_one(l, 0);
+        hip_check(mlvc_hip_event_record(ev1_, stream_), "event record");
+        hip_check(mlvc_hip_event_synchronize(ev1_), "event sync");
+        float ms = 0.0F;
+        hip_check(mlvc_hip_event_elapsed_ms(ev0_, ev1_, &ms), "event timing");
+        return ms / static_cast<float>(std::max(1, reps));
+    }
+
+private:
+    struct Binding {
+        TensorId in = 0, out = 0;
+        std::size_t bytes = 0;
+        DeviceMem buf[2];
+    };
+
+    const aot::TensorDescriptor& desc(TensorId id) const { return graph_.descriptor.tensors.at(id); }
+    const std::vector<aot::Node>& nodes() const { return graph_.descriptor.nodes; }
+    bool is_weight(TensorId id) const { return std::holds_alternative<aot::WeightLocation>(desc(id).storage); }
+
+    void select() { hip_check(mlvc_hip_set_device(device_), "set device"); }
+
+    void advance()
+    {
+        if (!bindings_.empty()) parity_ ^= 1;
+    }
+
+    void bind_state(const ModelExecutionConfig& config)
+    {
+        const auto& g = graph_.descriptor;
+        std::set<TensorId> seen_in, seen_out;
+        for (const StateTensorBinding& b : config.state_bindings) {
+            if (b.input_index >= g.inputs.size() || b.output_index >= g.outputs.size())
+                fail("state binding index out of range");
+            const TensorId in = g.inputs[b.input_index], out = g.outputs[b.output_index];
+            if (!seen_in.insert(in).second || !seen_out.insert(out).second) fail("duplicate state tensor binding");
+            if (desc(in).dtype != desc(out).dtype || desc(in).shape != desc(out).shape ||
+                desc(in).dtype != aot::DataType::FP16 || b.data_type != TensorDataType::kFloat16 || b.shape != desc(in).shape)
+                fail("state binding shape or dtype mismatch");
+            Binding nb;
+            nb.in = in;
+            nb.out = out;
+            nb.bytes = aot::tensor_bytes(desc(in));
+            bindings_.push_back(std::move(nb));
+            state_in_[in] = bindings_.size() - 1;
+            state_out_[out] = bindings_.size() - 1;
+        }
+        for (TensorId id : g.inputs) {
+            if (desc(id).dtype != aot::DataType::FP16) fail("only FP16 graph inputs are on this path");
+            if (!state_in_.count(id)) ext_in_.push_back(id);
+        }
+        for (TensorId id : g.outputs) {
+            if (desc(id).dtype != aot::DataType::FP16) fail("only FP16 graph outputs are on this path");
+            if (!state_out_.count(id)) ext_out_.push_back(id);
+        }
+    }
+
+    // ---------------------------------------------------------- lowering
+    void lower()
+    {
+        const auto& g = graph_.descriptor;
+        const auto& ns = nodes();
+        std::map<TensorId, int> consumers;
+        std::map<TensorId, std::size_t> producer, first_consumer;
+        for (const aot::Node& n : ns) {
+            for (TensorId id : n.inputs)
+                if (id) {
+                    if (!consumers[id]++) first_consumer[id] = n.index;
+                }
+            producer[n.outputs[0]] = n.index;
+        }
+        std::set<TensorId> outputs(g.outputs.begin(), g.outputs.end());
+        auto internal_single = [&](TensorId id) { return !outputs.count(id) && consumers[id] == 1; };
+        auto fp16_4d = [&](TensorId id) { return desc(id).dtype == aot::DataType::FP16 && desc(id).shape.size() == 4; };
+        auto is_std_conv = [&](const aot::Node& n) {
+            return n.op == Op::CONV && n.conv().groups == 1 && fp16_4d(n.inputs[0]) && fp16_4d(n.outputs[0]) &&
+                   is_weight(n.inputs[1]) && desc(n.inputs[1]).dtype == aot::DataType::FP16;
+        };
+        // Producers folded into the input staging of their only consumer conv.
+        std::vector<bool> folded(ns.size(), false);
+        for (const aot::Node& n : ns) {
+            const TensorId out = n.outputs[0];
+            if ((n.op != Op::SPACE_TO_DEPTH && n.op != Op::CONCAT) || !internal_single(out)) continue;
+            const aot::Node& c = ns[first_consumer[out]];
+            if (!is_std_conv(c) || c.inputs[0] != out || !fp16_4d(n.inputs[0])) continue;
+            if (n.op == Op::CONCAT) {
+                const int axis = n.axis() < 0 ? n.axis() + 4 : n.axis();
+                if (axis != 1 || n.inputs.size() != 2 || !fp16_4d(n.inputs[1]) || is_weight(n.inputs[0]) || is_weight(n.inputs[1]))
+                    continue;
+            } else if (is_weight(n.inputs[0])) {
+                continue;
+            }
+            folded[n.index] = true;
+        }
+
+        std::vector<bool> done(ns.size(), false);
+        for (const aot::Node& n : ns) {
+            if (done[n.index] || folded[n.index]) continue;
+            done[n.index] = true;
+            auto L = std::make_unique<Launch>();
+            switch (n.op) {
+            case Op::CONV:
+                if (n.conv().groups == 1) {
+                    lower_conv(*L, n, producer, folded, done, internal_single, first_consumer);
+                } else {
+                    lower_depthwise(*L, n);
+                }
+                break;
+            case Op::LEAKY_RELU:
+                require_fp16_activation(n.inputs[0]);
+                L->kind = Launch::kLeaky;
+                L->kind_name = "leaky_relu";
+                L->x = n.inputs[0];
+                L->y = n.outputs[0];
+                L->count = elem_count(desc(L->y).shape);
+                L->alpha = n.alpha();
+                L->bytes = 4.0 * static_cast<double>(L->count);
+                break;
+            case Op::ADD:
+                require_fp16_activation(n.inputs[0]);
+                require_fp16_activation(n.inputs[1]);
+                if (desc(n.inputs[0]).shape != desc(n.outputs[0]).shape || desc(n.inputs[1]).shape != desc(n.outputs[0]).shape)
+                    fail("broadcast ADD is outside the conv-graph path");
+                L->kind = Launch::kAdd;
+                L->kind_name = "add";
+                L->x = n.inputs[0];
+                L->x2 = n.inputs[1];
+                L->y = n.outputs[0];
+                L->count = elem_count(desc(L->y).shape);
+                L->bytes = 6.0 * static_cast<double>(L->count);
+                break;
+            case Op::DEPTH_TO_SPACE:
+            case Op::SPACE_TO_DEPTH: {
+                require_fp16_activation(n.inputs[0]);
+                const auto& s = desc(n.inputs[0]).shape;
+                if (s.size() != 4) fail("pixel shuffle needs a 4-D tensor");
+                L->kind = n.op == Op::DEPTH_TO_SPACE ? Launch::kD2S : Launch::kS2D;
+                L->kind_name = n.op == Op::DEPTH_TO_SPACE ? "depth_to_space" : "space_to_depth";
+                L->x = n.inputs[0];
+                L->y = n.outputs[0];
+                L->n = static_cast<int>(s[0]);
+                L->c = static_cast<int>(s[1]);
+                L->ih = static_cast<int>(s[2]);
+                L->iw = static_cast<int>(s[3]);
+                L->block = n.block_size();
+                L->bytes = 4.0 * static_cast<double>(elem_count(s));
+                break;
+            }
+            case Op::CONCAT: {
+                const int axis = n.axis() < 0 ? n.axis() + 4 : n.axis();
+                if (axis != 1 || n.inputs.size() != 2) fail("only two-input channel CONCAT is on this path");
+                require_fp16_activation(n.inputs[0]);
+                require_fp16_activation(n.inputs[1]);
+                const auto& a = desc(n.inputs[0]).shape;
+                const auto& b = desc(n.inputs[1]).shape;
+                L->kind = Launch::kConcat;
+                L->kind_name = "concat";
+                L->x = n.inputs[0];
+                L->x2 = n.inputs[1];
+                L->y = n.outputs[0];
+                L->n = static_cast<int>(a[0]);
+                L->ca = static_cast<int>(a[1]);
+                L->cb = static_cast<int>(b[1]);
+                L->hw = static_cast<std::size_t>(a[2] * a[3]);
+                L->bytes = 4.0 * static_cast<double>(elem_count(desc(L->y).shape));
+                break;
+            }
+            default:
+                fail("operator " + std::to_string(static_cast<int>(n.op)) + " is outside the conv-graph path");
+            }
+            if (L->name.empty()) L->name = desc(L->y).name;
+            launches_.push_back(std::move(L));
+        }
+    }
+
+    void require_fp16_activation(TensorId id) const
+    {
+        if (is_weight(id) || desc(id).dtype != aot::DataType::FP16) fail("operand must be an FP16 activation");
+    }
+
+    std::vector<std::uint16_t> weight_fp16(TensorId id) const
+    {
+        const auto& w = std::get<aot::WeightLocation>(desc(id).storage);
+        std::vector<std::uint16_t> v(w.bytes / 2);
+        std::memcpy(v.data(), graph_.weights.data() + w.offset, w.bytes);
+        return v;
+    }
+
+    std::vector<float> bias_f32(const aot::Node& n, int oc, std::size_t padded) const
+    {
+        std::vector<float> b(padded, 0.0F);
+        if (n.inputs.size() >= 3 && n.inputs[2]) {
+            if (!is_weight(n.inputs[2]) || desc(n.inputs[2]).dtype != aot::DataType::FP16) fail("conv bias must be an FP16 initializer");
+            const auto raw = weight_fp16(n.inputs[2]);
+            if (static_cast<int>(raw.size()) != oc) fail("conv bias length mismatch");
+            for (int i = 0; i < oc; ++i) b[static_cast<std::size_t>(i)] = half_to_float(raw[static_cast<std::size_t>(i)]);
+        }
+        return b;
+    }
+
+    template <typename SingleFn>
+    void lower_conv(Launch& L, const aot::Node& n, std::map<TensorId, std::size_t>& producer, const std::vector<bool>& folded,
+                    std::vector<bool>& done, SingleFn internal_single, std::map<TensorId, std::size_t>& first_consumer)
+    {
+        const auto& ns = nodes();
+        const auto& xs = desc(n.inputs[0]).shape;
+        const auto& ws = desc(n.inputs[1]).shape;
+        const auto& ys = desc(n.outputs[0]).shape;
+        if (xs.size() != 4 || ws.size() != 4 || ys.size() != 4) fail("conv expects 4-D NCHW tensors");
+        if (!is_weight(n.inputs[1])) fail("conv weights must be an initializer");
+        const auto& a = n.conv();
+        mlvc_hip_conv_desc& d = L.conv;
+        d = mlvc_hip_conv_desc{};
+        d.n = static_cast<int>(xs[0]);
+        d.ic = static_cast<int>(xs[1]);
+        d.ih = static_cast<int>(xs[2]);
+        d.iw = static_cast<int>(xs[3]);
+        d.oc = static_cast<int>(ys[1]);
+        d.oh = static_cast<int>(ys[2]);
+        d.ow = static_cast<int>(ys[3]);
+        d.kh = static_cast<int>(ws[2]);
+        d.kw = static_cast<int>(ws[3]);
+        d.stride_h = a.strides[0];
+        d.stride_w = a.strides[1];
+        d.pad_h = a.pads[0];
+        d.pad_w = a.pads[1];
+        if (ws[0] != ys[1] || ws[1] != xs[1]) fail("conv weight shape mismatch");
+        L.kind = Launch::kConv;
+        L.name = desc(n.outputs[0]).name;
+        std::string tags;
+
+        // Input side: a folded SPACE_TO_DEPTH or CONCAT producer.
+        TensorId in = n.inputs[0];
+        L.x = in;
+        if (producer.count(in) && folded[producer[in]]) {
+            const aot::Node& p = ns[producer[in]];
+            if (p.op == Op::SPACE_TO_DEPTH) {
+                L.x = p.inputs[0];
+                d.in_s2d_block = p.block_size();
+                tags += "+s2d";
+            } else {
+                L.x = p.inputs[0];
+                L.x2 = p.inputs[1];
+                d.ic_split = static_cast<int>(desc(p.inputs[0]).shape[1]);
+                tags += "+concat";
+            }
+        }
+        // Epilogue (fusion_matcher.cpp:352-411).
+        TensorId out = n.outputs[0];
+        if (n.index + 1 < ns.size() && internal_single(out)) {
+            const aot::Node& nx = ns[n.index + 1];
+            if (nx.op == Op::LEAKY_RELU && nx.inputs[0] == out) {
+                d.epilogue = MLVC_EPI_LEAKY_RELU;
+                d.alpha = nx.alpha();
+                done[nx.index] = true;
+                out = nx.outputs[0];
+                tags += "+lrelu";
+            } else if (nx.op == Op::ADD && (nx.inputs[0] == out || nx.inputs[1] == out)) {
+                const TensorId r = nx.inputs[0] == out ? nx.inputs[1] : nx.inputs[0];
+                if (r != out && !is_weight(r) && desc(r).dtype == aot::DataType::FP16 && desc(r).shape == desc(out).shape) {
+                    d.epilogue = MLVC_EPI_RESIDUAL_ADD;
+                    L.res = r;
+                    done[nx.index] = true;
+                    out = nx.outputs[0];
+                    tags += "+residual";
+                }
+            }
+        }
+        // Output side: a DEPTH_TO_SPACE that is the only consumer.
+        if (internal_single(out)) {
+            const aot::Node& c = ns[first_consumer[out]];
+            if (c.op == Op::DEPTH_TO_SPACE && c.inputs[0] == out && !done[c.index]) {
+                d.out_d2s_block = c.block_size();
+                done[c.index] = true;
+                out = c.outputs[0];
+                tags += "+d2s";
+            }
+        }
+        L.y = out;
+        hip_check(mlvc_hip_conv_plan(&d), "conv planning");
+        L.kind_name = std::string(mlvc_hip_conv_variant_name(d.variant)) + tags;
+        // Pack weights into the variant's fragment order, widen the bias.
+        const auto w = weight_fp16(n.inputs[1]);
+        std::vector<std::uint8_t> packed(mlvc_hip_conv_packed_bytes(&d));
+        hip_check(mlvc_hip_conv_pack(&d, w.data(), packed.data()), "weight packing");
+        L.packed = DeviceMem(packed.size());
+        pending_uploads_.push_back({L.packed.ptr, std::move(packed)});
+        const auto b = bias_f32(n, d.oc, mlvc_hip_conv_bias_len(&d));
+        L.bias = DeviceMem(b.size() * 4);
+        std::vector<std::uint8_t> braw(b.size() * 4);
+        std::memcpy(braw.data(), b.data(), braw.size());
+        pending_uploads_.push_back({L.bias.ptr, std::move(braw)});
+        // Algorithmic work: 2*N*OC*OH*OW*IC*KH*KW FLOPs; bytes = each tensor once.
+        L.flops = 2.0 * d.n * d.oc * d.oh * d.ow * static_cast<double>(d.ic) * d.kh * d.kw;
+        L.bytes = 2.0 * (static_cast<double>(d.n) * d.ic * d.ih * d.iw + static_cast<double>(d.oc) * d.ic * d.kh * d.kw + d.oc +
+                         static_cast<double>(d.n) * d.oc * d.oh * d.ow * (L.res ? 2.0 : 1.0));
+    }
+
+    void lower_depthwise(Launch& L, const aot::Node& n)
+    {
+        const auto& xs = desc(n.inputs[0]).shape;
+        const auto& ws = desc(n.inputs[1]).shape;
+        const auto& ys = desc(n.outputs[0]).shape;
+        if (xs.size() != 4 || ws.size() != 4 || ys.size() != 4) fail("conv expects 4-D NCHW tensors");
+        const int groups = n.conv().groups;
+        if (!(groups == xs[1] && ys[1] == xs[1] && ws[1] == 1)) fail("general grouped convolution (1 < groups < IC) unsupported");
+        require_fp16_activation(n.inputs[0]);
+        const auto& a = n.conv();
+        L.kind = Launch::kDepthwise;
+        L.kind_name = "depthwise";
+        L.x = n.inputs[0];
+        L.y = n.outputs[0];
+        L.n = static_cast<int>(xs[0]);
+        L.c = static_cast<int>(xs[1]);
+        L.ih = static_cast<int>(xs[2]);
+        L.iw = static_cast<int>(xs[3]);
+        L.oh = static_cast<int>(ys[2]);
+        L.ow = static_cast<int>(ys[3]);
+        L.kh = static_cast<int>(ws[2]);
+        L.kw = static_cast<int>(ws[3]);
+        L.sh = a.strides[0];
+        L.sw = a.strides[1];
+        L.ph = a.pads[0];
+        L.pw = a.pads[1];
+        const auto w = weight_fp16(n.inputs[1]);
+        std::vector<std::uint8_t> wr(w.size() * 2);
+        std::memcpy(wr.data(), w.data(), wr.size());
+        L.packed = DeviceMem(wr.size());
+        pending_uploads_.push_back({L.packed.ptr, std::move(wr)});
+        const auto b = bias_f32(n, L.c, static_cast<std::size_t>(L.c));
+        std::vector<std::uint8_t> braw(b.size() * 4);
+        std::memcpy(braw.data(), b.data(), braw.size());
+        L.bias = DeviceMem(braw.size());
+        pending_uploads_.push_back({L.bias.ptr, std::move(braw)});
+        L.flops = 2.0 * L.n * L.c * L.oh * L.ow * static_cast<double>(L.kh) * L.kw;
+        L.bytes = 2.0 * (static_cast<double>(L.n) * L.c * L.ih * L.iw + static_cast<double>(L.n) * L.c * L.oh * L.ow +
+                         static_cast<double>(L.c) * (L.kh * L.kw + 1));
+    }
+
+    // ---------------------------------------------------------- memory
+    // Tensors live in one device arena, re-planned over the fused launch
+    // schedule: a tensor is live from the launch that writes it to the last
+    // launch that reads it (graph outputs to the end); first-fit placement
+    // by start then size, 256-byte aligned (the reference CPU plan does the
+    // same over its fused steps, execution_plan.cpp:668-804).
+    void plan_memory()
+    {
+        const std::size_t n = launches_.size();
+        std::map<TensorId, std::pair<std::size_t, std::size_t>> live;
+        auto arena_resident = [&](TensorId id) {
+            return id && !is_weight(id) && !state_in_.count(id) && !state_out_.count(id) &&
+                   std::find(graph_.descriptor.inputs.begin(), graph_.descriptor.inputs.end(), id) == graph_.descriptor.inputs.end();
+        };
+        for (std::size_t i = 0; i < n; ++i) {
+            const Launch& l = *launches_[i];
+            if (arena_resident(l.y)) {
+                auto it = live.find(l.y);
+                if (it == live.end()) live[l.y] = {i, i};
+                else it->second.second = std::max(it->second.second, i);
+            }
+            for (TensorId r : {l.x, l.x2, l.res}) {
+                if (!arena_resident(r)) continue;
+                auto it = live.find(r);
+                if (it == live.end()) fail("tensor read before it is written: " + desc(r).name);
+                it->second.second = std::max(it->second.second, i);
+            }
+        }
+        for (TensorId o : graph_.descriptor.outputs)
+            if (live.count(o)) live[o].second = n;
+        std::vector<TensorId> order;
+        for (auto& kv : live) order.push_back(kv.first);
+        std::sort(order.begin(), order.end(), [&](TensorId a, TensorId b) {
+            if (live[a].first != live[b].first) return live[a].first < live[b].first;
+            return aot::tensor_bytes(desc(a)) > aot::tensor_bytes(desc(b));
+        });
+        struct Placed { std::size_t off, size, first, last; };
+        std::vector<Placed> placed;
+        std::size_t peak = 256;
+        for (TensorId id : order) {
+            const std::size_t sz = (aot::tensor_bytes(desc(id)) + 255) / 256 * 256;
+            const auto [f, l] = live[id];
+            std::vector<std::pair<std::size_t, std::size_t>> busy;
+            for (const Placed& p : placed)
+                if (p.first <= l && f <= p.last) busy.emplace_back(p.off, p.off + p.size);
+            std::sort(busy.begin(), busy.end());
+            std::size_t cand = 0;
+            for (const auto& [b0, b1] : busy) {
+                if (cand + sz <= b0) break;
+                cand = std::max(cand, b1);
+            }
+            offset_[id] = cand;
+            placed.push_back({cand, sz, f, l});
+            peak = std::max(peak, cand + sz);
+        }
+        arena_bytes_ = peak;
+        arena_ = DeviceMem(peak);
+    }
+
+    void allocate_io()
+    {
+        for (TensorId id : ext_in_) input_buf_.emplace(id, DeviceMem(aot::tensor_bytes(desc(id))));
+        for (auto& b : bindings_)
+            for (auto& buf : b.buf) buf = DeviceMem(b.bytes);
+        for (TensorId id : ext_in_) in_stage_.emplace_back(aot::tensor_bytes(desc(id)));
+        for (TensorId id : ext_out_) out_stage_.emplace_back(aot::tensor_bytes(desc(id)));
+    }
+
+    void upload_parameters()
+    {
+        for (auto& [dst, bytes] : pending_uploads_)
+            hip_check(mlvc_hip_memcpy_h2d(dst, bytes.data(), bytes.size(), stream_), "parameter upload");
+        hip_check(mlvc_hip_stream_synchronize(stream_), "stream sync");
+        pending_uploads_.clear();
+    }
+
+    void* ptr(TensorId id, int parity)
+    {
+        if (auto it = state_in_.find(id); it != state_in_.end()) return bindings_[it->second].buf[parity].ptr;
+        if (auto it = state_out_.find(id); it != state_out_.end()) return bindings_[it->second].buf[parity ^ 1].ptr;
+        if (auto it = input_buf_.find(id); it != input_buf_.end()) return it->second.ptr;
+        if (auto it = offset_.find(id); it != offset_.end()) return static_cast<char*>(arena_.ptr) + it->second;
+        fail("tensor without device storage: " + desc(id).name);
+    }
+
+    void enqueue_one(Launch& l, int parity)
+    {
+        switch (l.kind) {
+        case Launch::kConv: {
+            mlvc_hip_conv_desc d = l.conv;
+            d.x = ptr(l.x, parity);
+            d.x2 = l.x2 ? ptr(l.x2, parity) : nullptr;
+            d.residual = l.res ? ptr(l.res, parity) : nullptr;
+            d.y = ptr(l.y, parity);
+            d.packed_w = l.packed.ptr;
+            d.bias = static_cast<const float*>(l.bias.ptr);
+            hip_check(mlvc_hip_conv_launch(&d, stream_), "conv launch");
+            break;
+        }
+        case Launch::kDepthwise:
+            hip_check(mlvc_hip_depthwise(ptr(l.x, parity), static_cast<const std::uint16_t*>(l.packed.ptr),
+                                         static_cast<const float*>(l.bias.ptr), ptr(l.y, parity), l.n, l.c, l.ih, l.iw, l.oh,
+                                         l.ow, l.kh, l.kw, l.sh, l.sw, l.ph, l.pw, stream_),
+                      "depthwise launch");
+            break;
+        case Launch::kLeaky:
+            hip_check(mlvc_hip_leaky_relu(ptr(l.x, parity), ptr(l.y, parity), l.count, l.alpha, stream_), "leaky_relu launch");
+            break;
+        case Launch::kAdd:
+            hip_check(mlvc_hip_add(ptr(l.x, parity), ptr(l.x2, parity), ptr(l.y, parity), l.count, stream_), "add launch");
+            break;
+        case Launch::kD2S:
+            hip_check(mlvc_hip_depth_to_space(ptr(l.x, parity), ptr(l.y, parity), l.n, l.c, l.ih, l.iw, l.block, stream_),
+                      "depth_to_space launch");
+            break;
+        case Launch::kS2D:
+            hip_check(mlvc_hip_space_to_depth(ptr(l.x, parity), ptr(l.y, parity), l.n, l.c, l.ih, l.iw, l.block, stream_),
+                      "space_to_depth launch");
+            break;
+        case Launch::kConcat:
+            hip_check(mlvc_hip_concat_channels(ptr(l.x, parity), l.ca, ptr(l.x2, parity), l.cb, ptr(l.y, parity), l.n, l.hw,
+                                               stream_),
+                      "concat launch");
+            break;
+        }
+    }
+
+    void capture()
+    {
+        const int parities = bindings_.empty() ? 1 : 2;
+        for (int p = 0; p < parities; ++p) {
+            hip_check(mlvc_hip_capture_begin(stream_), "graph capture begin");
+            try {
+                for (auto& l : launches_) enqueue_one(*l, p);
+            } catch (...) {
+                mlvc_hip_graph g = nullptr;
+                mlvc_hip_capture_end(stream_, &g);
+                if (g) mlvc_hip_graph_destroy(g);
+                throw;
+            }
+            mlvc_hip_graph g = nullptr;
+            hip_check(mlvc_hip_capture_end(stream_, &g), "graph capture end");
+            graphs_.push_back(g);
+        }
+    }
+
+    void enqueue_downloads()
+    {
+        for (std::size_t i = 0; i < ext_out_.size(); ++i)
+            hip_check(mlvc_hip_memcpy_d2h(out_stage_[i].ptr, ptr(ext_out_[i], parity_), aot::tensor_bytes(desc(ext_out_[i])), stream_),
+                      "output download");
+    }
+
+    int device_;
+    aot::LoadedGraph graph_;
+    mlvc_hip_stream stream_ = nullptr;
+    mlvc_hip_event ev0_ = nullptr, ev1_ = nullptr;
+    std::vector<Binding> bindings_;
+    std::map<TensorId, std::size_t> state_in_, state_out_;
+    std::vector<TensorId> ext_in_, ext_out_;
+    std::vector<std::unique_ptr<Launch>> launches_;
+    std::vector<std::pair<void*, std::vector<std::uint8_t>>> pending_uploads_;
+    std::map<TensorId, std::size_t> offset_;
+    std::size_t arena_bytes_ = 0;
+    DeviceMem arena_;
+    std::map<TensorId, DeviceMem> input_buf_;
+    std::vector<HostMem> in_stage_, out_stage_;
+    std::vector<mlvc_hip_graph> graphs_;
+    int parity_ = 0;
+    bool initialized_ = false;
+};
+
+HipBackend::HipBackend(BackendOptions options) : options_(std::move(options))
+{
+    if (!options_.allow_cpu_fallback && (options_.execution_preference == ExecutionPreference::kCpu ||
+                                         options_.execution_preference == ExecutionPreference::kNpu))
+        fail("disallowed by strict non-GPU execution preference");
+}
+
+HipBackend::~HipBackend() = default;
+
+Plan& HipBackend::require_plan(const char* caller) const
+{
+    if (!plan_) fail(std::string("load() must be called before ") + caller);
+    return *plan_;
+}
+
+void HipBackend::load(const std::string& model_name, const ModelExecutionConfig& config)
+{
+    plan_.reset();
+    plan_ = std::make_unique<Plan>(options_, model_name, config);
+}
+
+std::vector<Tensor> HipBackend::run(const std::vector<Tensor>& inputs) { return require_plan("run()").run(inputs); }
+void HipBackend::reset_state() { require_plan("reset_state()").reset_state(); }
+std::vector<std::vector<std::int64_t>> HipBackend::io_shapes(bool outputs) const { return require_plan("io_shapes()").io_shapes(outputs); }
+void HipBackend::upload_inputs(const std::vector<const std::uint16_t*>& inputs) { require_plan("upload_inputs()").upload_inputs(inputs); }
+float HipBackend::time_frames(int frames) { return require_plan("time_frames()").time_frames(frames); }
+void HipBackend::download_outputs(const std::vector<std::uint16_t*>& outputs) { require_plan("download_outputs()").download_outputs(outputs); }
+std::size_t HipBackend::launch_count() const { return require_plan("launch_count()").launch_count(); }
+LaunchInfo HipBackend::launch_info(std::size_t index) const { return require_plan("launch_info()").launch_info(index); }
+float HipBackend::time_launch(std::size_t index, int reps) { return require_plan("time_launch()").time_launch(index, reps); }
+
+void register_hip_backend(bool make_default)
+{
+    register_backend(
+        "hip", [](const BackendOptions& o) { return std::make_unique<HipBackend>(o); }, make_default);
+}
+
+}  // namespace mlvc::hip_backend

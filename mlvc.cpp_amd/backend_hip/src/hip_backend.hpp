@@ -1,0 +1,59 @@
+#pragma once
+// "hip" inference backend: runs schema-3 FP16 conv graphs on one MI355X.
+//
+// Sits beside the reference's backends/cpu and backends/driver_cubin behind
+// mlvc::InferenceBackend. load() validates the graph, lowers it to a
+// schedule of hand-written gfx950 kernels with fusions, plans device memory
+// for that schedule and captures one hipGraph per state parity; run()
+// uploads inputs, replays the frame's graph and downloads outputs.
+
+#include "mlvc/runtime/aot_graph.hpp"
+#include "mlvc/runtime/backend.hpp"
+
+#include <cstdint>
+#include <memory>
+#include <string>
+#include <vector>
+
+namespace mlvc::hip_backend {
+
+struct LaunchInfo {
+    std::string name;
+    std::string kind;
+    double flops = 0.0;
+    double bytes = 0.0;
+};
+
+class Plan;
+
+class HipBackend final : public InferenceBackend {
+public:
+    explicit HipBackend(BackendOptions options);
+    ~HipBackend() override;
+
+    std::string_view name() const noexcept override { return "hip"; }
+    void load(const std::string& model_name, const ModelExecutionConfig& config) override;
+    std::vector<Tensor> run(const std::vector<Tensor>& inputs) override;
+    void reset_state() override;
+
+    // External (non-state) graph inputs / outputs in graph order.
+    std::vector<std::vector<std::int64_t>> io_shapes(bool outputs) const;
+
+    // Device-resident measurement helpers.
+    void upload_inputs(const std::vector<const std::uint16_t*>& inputs);
+    float time_frames(int frames);
+    void download_outputs(const std::vector<std::uint16_t*>& outputs);
+    std::size_t launch_count() const;
+    LaunchInfo launch_info(std::size_t index) const;
+    float time_launch(std::size_t index, int reps);
+
+private:
+    Plan& require_plan(const char* caller) const;
+
+    BackendOptions options_;
+    std::unique_ptr<Plan> plan_;
+};
+
+void register_hip_backend(bool make_default);
+
+}  // namespace mlvc::hip_backend

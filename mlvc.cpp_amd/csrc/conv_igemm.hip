@@ -1,0 +1,559 @@
+// FP16 convolution (groups == 1) on gfx950 MFMA as an implicit GEMM.
+//
+//   D[oc, p] = bias[oc] + sum_k W[oc, k] * X[k, p],  k = (chunk, tap, c16)
+//
+// One workgroup (4 waves) owns BM output channels x a TH x TW output-pixel
+// tile. Per input-channel chunk of KC channels it stages
+//   * the NCHW input halo tile into LDS channel-last ([pixel][KC + 8 pad]),
+//     so the MFMA B fragment of a lane (8 consecutive channels of one pixel)
+//     is a single 16-byte LDS read for every tap; for stride 2 the even and
+//     odd input columns are stored in separate halves of an LDS row so that
+//     consecutive output pixels read consecutive LDS pixels;
+//   * the chunk's weights, pre-packed at load time in exact A-fragment order
+//     ([tap][k16][m32][lane][8]), as a contiguous 16-byte-vector copy.
+// The next chunk is fetched into registers while the current one is
+// consumed (v_mfma_f32_32x32x16_f16, FP32 accumulators seeded with the
+// bias). The epilogue rounds to FP16 (RNE), applies LeakyReLU or the
+// residual add on the rounded value exactly like the reference CPU GEMM
+// epilogue (backends/cpu/src/kernels_scalar.cpp:178-192), and stores either
+// plainly or through the DEPTH_TO_SPACE (CRD) index map.
+//
+// Reference kernels this replaces: pointwise_conv.cu:116-338 (1x1 mma.sync),
+// cutlass.cu:116-161 (1x1 EVT epilogues, spatial fprop), spatial_conv.cu:
+// 1-293 (implicit-GEMM KxK), generic_conv.cu:1-82 (fallback).
+
+#include "common.hpp"
+#include "mlvc_hip_device.h"
+
+#include <algorithm>
+#include <cstring>
+#include <vector>
+
+namespace mlvc_hip {
+namespace {
+
+struct ConvArgs {
+    const std::uint16_t* x;
+    const std::uint16_t* x2;
+    const std::uint16_t* w;
+    const float* bias;
+    const std::uint16_t* res;
+    std::uint16_t* y;
+    int ic_split, s2d, d2s;
+    int ic, ih, iw, oc, oh, ow, kh, kw, sh, sw, ph, pw;
+    int epi;
+    float alpha;
+    int tiles_x, nchunks;
+};
+
+// KC consecutive channels [c0, c0 + KC) of input pixel (iy, ix) of batch b,
+// packed in pairs, through the optional SPACE_TO_DEPTH / CONCAT maps. Zero
+// outside the image (padding) and for channels past IC (chunk padding).
+template <int KC>
+__device__ __forceinline__ void load_pixel(const ConvArgs& a, int b, int c0, int iy, int ix, std::uint32_t (&out)[KC / 2])
+{
+    std::uint16_t v[KC];
+#pragma unroll
+    for (int j = 0; j < KC; ++j) v[j] = 0;
+    if (iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw) {
+        if (a.s2d > 1) {
+            const int bs = a.s2d, b2 = bs * bs;
+            const int sW = a.iw * bs;
+            const size_t splane = static_cast<size_t>(a.ih) * bs * sW;
+            const std::uint16_t* p = a.x + static_cast<size_t>(b) * (a.ic / b2) * splane +
+                                     static_cast<size_t>(iy * bs) * sW + ix * bs;
+#pragma unroll
+            for (int j = 0; j < KC; ++j) {
+                const int c = c0 + j;
+                if (c < a.ic) {
+                    const int cs = c / b2, r = c - cs * b2, dy = r / bs, dx = r - dy * bs;
+                    v[j] = p[cs * splane + static_cast<size_t>(dy) * sW + dx];
+                }
+            }
+        } else {
+            const size_t hw = static_cast<size_t>(a.ih) * a.iw;
+            const size_t po = static_cast<size_t>(iy) * a.iw + ix;
+            const int c1 = a.x2 ? a.ic_split : a.ic;
+            const std::uint16_t* p = a.x + static_cast<size_t>(b) * c1 * hw + po;
+            const std::uint16_t* p2 = a.x2 ? a.x2 + static_cast<size_t>(b) * (a.ic - c1) * hw + po : nullptr;
+#pragma unroll
+            for (int j = 0; j < KC; ++j) {
+                const int c = c0 + j;
+                if (c < c1)
+                    v[j] = p[c * hw];
+                else if (c < a.ic)
+                    v[j] = p2[(c - c1) * hw];
+            }
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < KC / 2; ++j) out[j] = static_cast<std::uint32_t>(v[2 * j]) | (static_cast<std::uint32_t>(v[2 * j + 1]) << 16);
+}
+
+// Single element of the conv input (used by the direct fallback).
+__device__ __forceinline__ std::uint16_t load_input(const ConvArgs& a, int b, int c, int iy, int ix)
+{
+    if (c >= a.ic || iy < 0 || iy >= a.ih || ix < 0 || ix >= a.iw) return 0;
+    if (a.s2d > 1) {
+        const int bs = a.s2d, b2 = bs * bs;
+        const int cs = c / b2, r = c - cs * b2, dy = r / bs, dx = r - dy * bs;
+        const int sc = a.ic / b2, sh = a.ih * bs, sw = a.iw * bs;
+        return a.x[(static_cast<size_t>(b * sc + cs) * sh + iy * bs + dy) * sw + ix * bs + dx];
+    }
+    if (a.x2) {
+        if (c >= a.ic_split)
+            return a.x2[(static_cast<size_t>(b * (a.ic - a.ic_split) + c - a.ic_split) * a.ih + iy) * a.iw + ix];
+        return a.x[(static_cast<size_t>(b * a.ic_split + c) * a.ih + iy) * a.iw + ix];
+    }
+    return a.x[(static_cast<size_t>(b * a.ic + c) * a.ih + iy) * a.iw + ix];
+}
+
+__device__ __forceinline__ std::uint16_t finish(const ConvArgs& a, float acc, int b, int oc, int oy, int ox)
+{
+    std::uint16_t h = f2h(acc);
+    if (a.epi == MLVC_EPI_LEAKY_RELU) {
+        const float f = h2f(h);
+        if (f < 0.0f) h = f2h(f * a.alpha);
+    } else if (a.epi == MLVC_EPI_RESIDUAL_ADD) {
+        h = f2h(h2f(h) + h2f(a.res[(static_cast<size_t>(b * a.oc + oc) * a.oh + oy) * a.ow + ox]));
+    }
+    return h;
+}
+
+__device__ __forceinline__ void store_output(const ConvArgs& a, std::uint16_t h, int b, int oc, int oy, int ox)
+{
+    if (a.d2s > 1) {
+        const int bs = a.d2s, b2 = bs * bs;
+        const int c = oc / b2, r = oc - c * b2, dy = r / bs, dx = r - dy * bs;
+        const int occ = a.oc / b2, H = a.oh * bs, W = a.ow * bs;
+        a.y[(static_cast<size_t>(b * occ + c) * H + oy * bs + dy) * W + ox * bs + dx] = h;
+    } else {
+        a.y[(static_cast<size_t>(b * a.oc + oc) * a.oh + oy) * a.ow + ox] = h;
+    }
+}
+
+template <int BM_, int TH_, int TW_, int KH_, int KW_, int S_, int KC_>
+struct Cfg {
+    static constexpr int BM = BM_, TH = TH_, TW = TW_, KH = KH_, KW = KW_, S = S_, KC = KC_;
+    static constexpr int kThreads = 256;
+    static constexpr int BN = TH * TW;
+    static constexpr int TAPS = KH * KW;
+    static constexpr int KS = KC / 16;  // 16-deep MFMA K steps per tap
+    static constexpr int MT = BM / 32;
+    static constexpr int WN = BN / 4;
+    static constexpr int NT = WN / 32;
+    static constexpr int IH_T = (TH - 1) * S + KH;
+    static constexpr int IW_T = (TW - 1) * S + KW;
+    static constexpr int IW_E = (IW_T + 1) / 2;  // even columns (stride 2 layout)
+    static constexpr int PST = KC + 8;           // LDS halves per staged pixel
+    static constexpr int IN_PIX = IH_T * IW_T;
+    static constexpr int IN_LDS = IN_PIX * PST;
+    static constexpr int W_LDS = TAPS * KS * MT * 64 * 8;  // halves per chunk
+    static constexpr int PIX_PER_T = (IN_PIX + kThreads - 1) / kThreads;
+    static constexpr int W_VEC = W_LDS / 8;
+    static constexpr int W_PER_T = (W_VEC + kThreads - 1) / kThreads;
+    static constexpr int EPI_ROW = BN + 8;  // output staging row (one channel), halves
+    static constexpr int EPI_LDS = BM * EPI_ROW;
+    static constexpr int LDS = (IN_LDS + W_LDS) > EPI_LDS ? (IN_LDS + W_LDS) : EPI_LDS;
+    static_assert(BM % 32 == 0 && WN % 32 == 0 && KC % 16 == 0, "tile shape");
+    static_assert(LDS * 2 <= 160 * 1024, "LDS budget");
+
+    __device__ static constexpr int col(int xi) { return S == 2 ? ((xi & 1) ? IW_E + (xi >> 1) : (xi >> 1)) : xi; }
+};
+
+template <class C>
+__global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a)
+{
+    __shared__ __attribute__((aligned(16))) std::uint16_t lds[C::LDS];
+    std::uint16_t* const lds_in = lds;
+    std::uint16_t* const lds_w = lds + C::IN_LDS;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tile = blockIdx.x;
+    const int tx0 = (tile % a.tiles_x) * C::TW, ty0 = (tile / a.tiles_x) * C::TH;
+    const int ocb = blockIdx.y, b = blockIdx.z;
+    const int iy0 = ty0 * C::S - a.ph, ix0 = tx0 * C::S - a.pw;
+
+    floatx16 acc[C::MT][C::NT];
+#pragma unroll
+    for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const float bv = a.bias[ocb * C::BM + mt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)];
+#pragma unroll
+            for (int nt = 0; nt < C::NT; ++nt) acc[mt][nt][r] = bv;
+        }
+
+    std::uint32_t in_reg[C::PIX_PER_T][C::KC / 2];
+    u32x4 w_reg[C::W_PER_T];
+    auto fetch = [&](int chunk) {
+        const int c0 = chunk * C::KC;
+#pragma unroll
+        for (int i = 0; i < C::PIX_PER_T; ++i) {
+            const int pix = tid + i * C::kThreads;
+            if (pix < C::IN_PIX) {
+                const int yi = pix / C::IW_T, xi = pix - yi * C::IW_T;
+                load_pixel<C::KC>(a, b, c0, iy0 + yi, ix0 + xi, in_reg[i]);
+            }
+        }
+        const u32x4* ws = reinterpret_cast<const u32x4*>(a.w + (static_cast<size_t>(ocb) * a.nchunks + chunk) * C::W_LDS);
+#pragma unroll
+        for (int i = 0; i < C::W_PER_T; ++i) {
+            const int e = tid + i * C::kThreads;
+            if (e < C::W_VEC) w_reg[i] = ws[e];
+        }
+    };
+    auto commit = [&]() {
+#pragma unroll
+        for (int i = 0; i < C::PIX_PER_T; ++i) {
+            const int pix = tid + i * C::kThreads;
+            if (pix < C::IN_PIX) {
+                const int yi = pix / C::IW_T, xi = pix - yi * C::IW_T;
+                u32x4* dst = reinterpret_cast<u32x4*>(&lds_in[(yi * C::IW_T + C::col(xi)) * C::PST]);
+#pragma unroll
+                for (int q = 0; q < C::KC / 8; ++q)
+                    dst[q] = u32x4{in_reg[i][4 * q], in_reg[i][4 * q + 1], in_reg[i][4 * q + 2], in_reg[i][4 * q + 3]};
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < C::W_PER_T; ++i) {
+            const int e = tid + i * C::kThreads;
+            if (e < C::W_VEC) reinterpret_cast<u32x4*>(lds_w)[e] = w_reg[i];
+        }
+    };
+
+    // Per-lane output pixel of each 32-wide N block, in tile coordinates.
+    int pyi[C::NT], pxi[C::NT];
+#pragma unroll
+    for (int nt = 0; nt < C::NT; ++nt) {
+        const int p = wave * C::WN + nt * 32 + (lane & 31);
+        pyi[nt] = (p / C::TW) * C::S;
+        pxi[nt] = (p % C::TW) * C::S;
+    }
+    const int koff = (lane >> 5) * 8;
+
+    fetch(0);
+    commit();
+    __syncthreads();
+    for (int chunk = 0; chunk < a.nchunks; ++chunk) {
+        const bool more = chunk + 1 < a.nchunks;
+        if (more) fetch(chunk + 1);
+#pragma unroll
+        for (int tap = 0; tap < C::TAPS; ++tap) {
+            const int ky = tap / C::KW, kx = tap % C::KW;
+#pragma unroll
+            for (int ks = 0; ks < C::KS; ++ks) {
+                half8 av[C::MT], bv[C::NT];
+#pragma unroll
+                for (int mt = 0; mt < C::MT; ++mt)
+                    av[mt] = *reinterpret_cast<const half8*>(&lds_w[(((tap * C::KS + ks) * C::MT + mt) * 64 + lane) * 8]);
+#pragma unroll
+                for (int nt = 0; nt < C::NT; ++nt) {
+                    const int pix = (pyi[nt] + ky) * C::IW_T + C::col(pxi[nt] + kx);
+                    bv[nt] = *reinterpret_cast<const half8*>(&lds_in[pix * C::PST + ks * 16 + koff]);
+                }
+#pragma unroll
+                for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+                    for (int nt = 0; nt < C::NT; ++nt)
+                        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[mt], bv[nt], acc[mt][nt], 0, 0, 0);
+            }
+        }
+        __syncthreads();
+        if (more) {
+            commit();
+            __syncthreads();
+        }
+    }
+
+    // Epilogue, stage 1: each lane writes its FP16-rounded accumulators into
+    // an LDS tile [oc][pixel] (all indices static, so nothing spills).
+    // The main loop ended with a barrier, so the staging buffers are free.
+#pragma unroll
+    for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < C::NT; ++nt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int ocl = mt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                const int pl = wave * C::WN + nt * 32 + (lane & 31);
+                lds[ocl * C::EPI_ROW + pl] = f2h(acc[mt][nt][r]);
+            }
+    __syncthreads();
+    // Stage 2: consecutive threads take consecutive pixels of one channel,
+    // apply the epilogue to the rounded value and store.
+    for (int e = tid; e < C::BM * C::BN; e += C::kThreads) {
+        const int ocl = e / C::BN, pl = e - ocl * C::BN;
+        const int oc = ocb * C::BM + ocl;
+        const int oy = ty0 + pl / C::TW, ox = tx0 + pl % C::TW;
+        if (oc < a.oc && oy < a.oh && ox < a.ow) {
+            std::uint16_t h = lds[ocl * C::EPI_ROW + pl];
+            if (a.epi == MLVC_EPI_LEAKY_RELU) {
+                const float f = h2f(h);
+                if (f < 0.0f) h = f2h(f * a.alpha);
+            } else if (a.epi == MLVC_EPI_RESIDUAL_ADD) {
+                h = f2h(h2f(h) + h2f(a.res[(static_cast<size_t>(b * a.oc + oc) * a.oh + oy) * a.ow + ox]));
+            }
+            store_output(a, h, b, oc, oy, ox);
+        }
+    }
+}
+
+// Generic fallback: one thread per output, FP32 fused multiply-add in
+// (ic, ky, kx) order. Used only for shapes without an MFMA variant.
+__global__ __launch_bounds__(256) void conv_direct_kernel(ConvArgs a, int n)
+{
+    const size_t total = static_cast<size_t>(n) * a.oc * a.oh * a.ow;
+    for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < total;
+         i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+        const int ox = static_cast<int>(i % a.ow);
+        const int oy = static_cast<int>((i / a.ow) % a.oh);
+        const int oc = static_cast<int>((i / (static_cast<size_t>(a.ow) * a.oh)) % a.oc);
+        const int b = static_cast<int>(i / (static_cast<size_t>(a.ow) * a.oh * a.oc));
+        float acc = a.bias[oc];
+        const std::uint16_t* wr = a.w + static_cast<size_t>(oc) * a.ic * a.kh * a.kw;
+        for (int c = 0; c < a.ic; ++c)
+            for (int ky = 0; ky < a.kh; ++ky)
+                for (int kx = 0; kx < a.kw; ++kx) {
+                    const int iy = oy * a.sh - a.ph + ky, ix = ox * a.sw - a.pw + kx;
+                    if (iy < 0 || iy >= a.ih || ix < 0 || ix >= a.iw) continue;
+                    acc = fmaf(h2f(load_input(a, b, c, iy, ix)), h2f(wr[(c * a.kh + ky) * a.kw + kx]), acc);
+                }
+        store_output(a, finish(a, acc, b, oc, oy, ox), b, oc, oy, ox);
+    }
+}
+
+// ---------------------------------------------------------------- variants
+struct Variant {
+    const char* name;
+    int bm, th, tw, kh, kw, s, kc;  // bm == 0: direct fallback
+    void (*launch)(const ConvArgs&, dim3, hipStream_t);
+};
+
+template <class C>
+void launch_mfma(const ConvArgs& a, dim3 grid, hipStream_t s)
+{
+    hipLaunchKernelGGL(conv_mfma_kernel<C>, grid, dim3(C::kThreads), 0, s, a);
+}
+
+#define MLVC_VARIANT(BM, TH, TW, KH, KW, S, KC)                                                       \
+    Variant{"mfma_bm" #BM "_" #TH "x" #TW "_k" #KH "x" #KW "_s" #S "_kc" #KC, BM, TH, TW, KH, KW, S, KC, \
+            &launch_mfma<Cfg<BM, TH, TW, KH, KW, S, KC>>}
+
+const Variant kVariants[] = {
+    Variant{"direct_fp32", 0, 0, 0, 0, 0, 0, 0, nullptr},
+    // 3x3 stride 1
+    MLVC_VARIANT(64, 4, 64, 3, 3, 1, 16),
+    MLVC_VARIANT(64, 8, 32, 3, 3, 1, 16),
+    MLVC_VARIANT(64, 16, 16, 3, 3, 1, 16),
+    MLVC_VARIANT(64, 2, 64, 3, 3, 1, 16),
+    MLVC_VARIANT(64, 4, 32, 3, 3, 1, 16),
+    MLVC_VARIANT(64, 8, 16, 3, 3, 1, 16),
+    MLVC_VARIANT(128, 4, 64, 3, 3, 1, 16),
+    MLVC_VARIANT(128, 8, 32, 3, 3, 1, 16),
+    MLVC_VARIANT(128, 16, 16, 3, 3, 1, 16),
+    // 3x3 stride 2
+    MLVC_VARIANT(64, 2, 64, 3, 3, 2, 16),
+    MLVC_VARIANT(64, 4, 32, 3, 3, 2, 16),
+    MLVC_VARIANT(64, 8, 16, 3, 3, 2, 16),
+    MLVC_VARIANT(128, 2, 64, 3, 3, 2, 16),
+    // 1x1 (flattened pixels unless an unshuffle is fused)
+    MLVC_VARIANT(64, 1, 256, 1, 1, 1, 32),
+    MLVC_VARIANT(64, 1, 128, 1, 1, 1, 32),
+    MLVC_VARIANT(128, 1, 128, 1, 1, 1, 32),
+    MLVC_VARIANT(64, 2, 64, 1, 1, 1, 32),
+    MLVC_VARIANT(64, 4, 32, 1, 1, 1, 32),
+};
+constexpr int kVariantCount = static_cast<int>(sizeof(kVariants) / sizeof(kVariants[0]));
+
+int cu_count()
+{
+    static int cus = [] {
+        int dev = 0, n = 256;
+        if (hipGetDevice(&dev) == hipSuccess) {
+            hipDeviceProp_t p;
+            if (hipGetDeviceProperties(&p, dev) == hipSuccess) n = p.multiProcessorCount;
+        }
+        return n;
+    }();
+    return cus;
+}
+
+bool flat_1x1(const mlvc_hip_conv_desc& d)
+{
+    return d.kh == 1 && d.kw == 1 && d.in_s2d_block <= 1 && d.out_d2s_block <= 1;
+}
+
+const Variant& variant_of(const mlvc_hip_conv_desc& d)
+{
+    if (d.variant < 0 || d.variant >= kVariantCount) throw std::runtime_error("conv: invalid variant");
+    return kVariants[d.variant];
+}
+
+void validate(const mlvc_hip_conv_desc& d)
+{
+    if (d.n <= 0 || d.ic <= 0 || d.ih <= 0 || d.iw <= 0 || d.oc <= 0 || d.oh <= 0 || d.ow <= 0 || d.kh <= 0 ||
+        d.kw <= 0 || d.stride_h <= 0 || d.stride_w <= 0 || d.pad_h < 0 || d.pad_w < 0)
+        throw std::runtime_error("conv: invalid geometry");
+    if (d.oh != (d.ih + 2 * d.pad_h - d.kh) / d.stride_h + 1 || d.ow != (d.iw + 2 * d.pad_w - d.kw) / d.stride_w + 1)
+        throw std::runtime_error("conv: output shape does not match the geometry");
+    if (d.in_s2d_block > 1 && (d.ic % (d.in_s2d_block * d.in_s2d_block) != 0 || d.x2))
+        throw std::runtime_error("conv: invalid space_to_depth fusion");
+    if (d.x2 && (d.ic_split <= 0 || d.ic_split >= d.ic)) throw std::runtime_error("conv: invalid concat split");
+    if (d.out_d2s_block > 1 && d.oc % (d.out_d2s_block * d.out_d2s_block) != 0)
+        throw std::runtime_error("conv: invalid depth_to_space fusion");
+    if (d.epilogue == MLVC_EPI_RESIDUAL_ADD && !d.residual) throw std::runtime_error("conv: residual missing");
+    if (!d.x || !d.y) throw std::runtime_error("conv: null tensor");
+}
+
+// Geometry as the kernel sees it (1x1 convs run over flattened pixels).
+void kernel_geometry(const mlvc_hip_conv_desc& d, int& ih, int& iw, int& oh, int& ow)
+{
+    if (flat_1x1(d) && d.stride_h == 1 && d.stride_w == 1 && d.pad_h == 0 && d.pad_w == 0) {
+        ih = oh = 1;
+        iw = ow = d.oh * d.ow;
+    } else {
+        ih = d.ih;
+        iw = d.iw;
+        oh = d.oh;
+        ow = d.ow;
+    }
+}
+
+}  // namespace
+}  // namespace mlvc_hip
+
+using namespace mlvc_hip;
+
+extern "C" {
+
+int mlvc_hip_conv_plan(mlvc_hip_conv_desc* desc)
+{
+    return guard([&] {
+        validate(*desc);
+        const mlvc_hip_conv_desc& d = *desc;
+        int ih, iw, oh, ow;
+        kernel_geometry(d, ih, iw, oh, ow);
+        const bool flat = ih == 1 && oh == 1 && d.kh == 1 && d.kw == 1;
+        const int slots = 2 * cu_count();
+        int best = 0;
+        double best_cost = 0.0;
+        for (int v = 1; v < kVariantCount; ++v) {
+            const Variant& k = kVariants[v];
+            if (k.kh != d.kh || k.kw != d.kw || k.s != d.stride_h || k.s != d.stride_w) continue;
+            if (d.kh == 1 && (d.pad_h || d.pad_w)) continue;
+            if (d.kh == 1 && flat != (k.th == 1)) continue;
+            const long tiles = static_cast<long>((oh + k.th - 1) / k.th) * ((ow + k.tw - 1) / k.tw) *
+                               ((d.oc + k.bm - 1) / k.bm) * d.n;
+            const long rounds = (tiles + slots - 1) / slots;
+            // Work per round in MACs plus a fixed per-tile overhead.
+            const double cost = static_cast<double>(rounds) * (static_cast<double>(k.bm) * k.th * k.tw + 4096.0);
+            if (best == 0 || cost < best_cost) {
+                best = v;
+                best_cost = cost;
+            }
+        }
+        desc->variant = best;
+    });
+}
+
+const char* mlvc_hip_conv_variant_name(int variant)
+{
+    return variant >= 0 && variant < kVariantCount ? kVariants[variant].name : "invalid";
+}
+
+size_t mlvc_hip_conv_bias_len(const mlvc_hip_conv_desc* desc)
+{
+    const Variant& k = variant_of(*desc);
+    if (k.bm == 0) return static_cast<size_t>(desc->oc);
+    return static_cast<size_t>((desc->oc + k.bm - 1) / k.bm * k.bm);
+}
+
+size_t mlvc_hip_conv_packed_bytes(const mlvc_hip_conv_desc* desc)
+{
+    const mlvc_hip_conv_desc& d = *desc;
+    const Variant& k = variant_of(d);
+    if (k.bm == 0) return static_cast<size_t>(d.oc) * d.ic * d.kh * d.kw * 2;
+    const size_t ocb = static_cast<size_t>((d.oc + k.bm - 1) / k.bm);
+    const size_t chunks = static_cast<size_t>((d.ic + k.kc - 1) / k.kc);
+    return ocb * chunks * static_cast<size_t>(k.kh * k.kw) * k.kc * k.bm * 2;
+}
+
+int mlvc_hip_conv_pack(const mlvc_hip_conv_desc* desc, const uint16_t* w, void* dst_host)
+{
+    return guard([&] {
+        const mlvc_hip_conv_desc& d = *desc;
+        const Variant& k = variant_of(d);
+        auto* out = static_cast<std::uint16_t*>(dst_host);
+        if (k.bm == 0) {
+            std::memcpy(out, w, static_cast<size_t>(d.oc) * d.ic * d.kh * d.kw * 2);
+            return;
+        }
+        const int taps = k.kh * k.kw, ks_n = k.kc / 16, mt_n = k.bm / 32;
+        const int ocb_n = (d.oc + k.bm - 1) / k.bm, chunks = (d.ic + k.kc - 1) / k.kc;
+        size_t o = 0;
+        // Layout [ocb][chunk][tap][ks][mt][lane][8]: lane l of m-tile mt
+        // holds W[oc = ocb*BM + mt*32 + l%32][ic = chunk*KC + ks*16 + 8*(l/32) + j][tap].
+        for (int ocb = 0; ocb < ocb_n; ++ocb)
+            for (int ch = 0; ch < chunks; ++ch)
+                for (int tap = 0; tap < taps; ++tap)
+                    for (int ks = 0; ks < ks_n; ++ks)
+                        for (int mt = 0; mt < mt_n; ++mt)
+                            for (int lane = 0; lane < 64; ++lane)
+                                for (int j = 0; j < 8; ++j) {
+                                    const int oc = ocb * k.bm + mt * 32 + (lane & 31);
+                                    const int ic = ch * k.kc + ks * 16 + 8 * (lane >> 5) + j;
+                                    out[o++] = (oc < d.oc && ic < d.ic)
+                                                   ? w[(static_cast<size_t>(oc) * d.ic + ic) * taps + tap]
+                                                   : std::uint16_t{0};
+                                }
+    });
+}
+
+int mlvc_hip_conv_launch(const mlvc_hip_conv_desc* desc, mlvc_hip_stream s)
+{
+    return guard([&] {
+        const mlvc_hip_conv_desc& d = *desc;
+        validate(d);
+        const Variant& k = variant_of(d);
+        ConvArgs a{};
+        a.x = static_cast<const std::uint16_t*>(d.x);
+        a.x2 = static_cast<const std::uint16_t*>(d.x2);
+        a.w = static_cast<const std::uint16_t*>(d.packed_w);
+        a.bias = d.bias;
+        a.res = static_cast<const std::uint16_t*>(d.residual);
+        a.y = static_cast<std::uint16_t*>(d.y);
+        a.ic_split = d.x2 ? d.ic_split : 0;
+        a.s2d = d.in_s2d_block;
+        a.d2s = d.out_d2s_block;
+        a.ic = d.ic;
+        a.oc = d.oc;
+        a.kh = d.kh;
+        a.kw = d.kw;
+        a.sh = d.stride_h;
+        a.sw = d.stride_w;
+        a.ph = d.pad_h;
+        a.pw = d.pad_w;
+        a.epi = d.epilogue;
+        a.alpha = d.alpha;
+        if (k.bm == 0) {
+            a.ih = d.ih; a.iw = d.iw; a.oh = d.oh; a.ow = d.ow;
+            const size_t total = static_cast<size_t>(d.n) * d.oc * d.oh * d.ow;
+            const unsigned blocks = static_cast<unsigned>(std::min<size_t>((total + 255) / 256, 65535));
+            hipLaunchKernelGGL(conv_direct_kernel, dim3(blocks), dim3(256), 0, to_stream(s), a, d.n);
+        } else {
+            if (k.kh != d.kh || k.kw != d.kw || k.s != d.stride_h || k.s != d.stride_w)
+                throw std::runtime_error("conv: variant does not match the geometry");
+            kernel_geometry(d, a.ih, a.iw, a.oh, a.ow);
+            if (a.s2d > 1 && a.ih == 1 && d.ih != 1) throw std::runtime_error("conv: flattened geometry with fusion");
+            a.tiles_x = (a.ow + k.tw - 1) / k.tw;
+            a.nchunks = (d.ic + k.kc - 1) / k.kc;
+            const unsigned tiles = static_cast<unsigned>(a.tiles_x * ((a.oh + k.th - 1) / k.th));
+            const dim3 grid(tiles, static_cast<unsigned>((d.oc + k.bm - 1) / k.bm), static_cast<unsigned>(d.n));
+            k.launch(a, grid, to_stream(s));
+        }
+        check(hipGetLastError(), "conv kernel launch");
+    });
+}
+
+}  // extern "C"

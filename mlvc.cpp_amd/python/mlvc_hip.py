@@ -1,0 +1,236 @@
+"""ctypes binding of the MI355X backend's C ABI (include/mlvc_hip_backend.h
+and include/mlvc_hip_device.h).
+
+`Backend` mirrors mlvc::InferenceBackend (reference
+runtime/include/mlvc/runtime/backend.hpp:48-63): load(model, bindings),
+run(inputs) -> outputs, reset_state(). Tensors are numpy uint16 arrays of
+raw binary16 values in NCHW order. Errors raise MlvcError with the library's
+message. The libraries must have been built (python mlvc.cpp_amd/build.py);
+nothing here falls back to another implementation.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import pathlib
+
+import numpy as np
+
+LIB_DIR = pathlib.Path(__file__).resolve().parent.parent / "lib"
+BACKEND_LIB = LIB_DIR / "libmlvc_hip.so"
+DEVICE_LIB = LIB_DIR / "libmlvc_hip_device.so"
+
+_i64p = C.POINTER(C.c_int64)
+_u16p = C.POINTER(C.c_uint16)
+
+
+class MlvcError(RuntimeError):
+    pass
+
+
+_lib = None
+_dev = None
+
+
+def _load(path: pathlib.Path) -> C.CDLL:
+    if not path.exists():
+        raise MlvcError(f"{path} is not built; run `python mlvc.cpp_amd/build.py`")
+    return C.CDLL(str(path))
+
+
+def backend_lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        lib = _load(BACKEND_LIB)
+        lib.mlvc_backend_last_error.restype = C.c_char_p
+        lib.mlvc_backend_name.restype = C.c_char_p
+        lib.mlvc_backend_create.argtypes = [C.c_char_p, C.c_char_p, C.c_int, C.c_int, C.POINTER(C.c_void_p)]
+        lib.mlvc_backend_destroy.argtypes = [C.c_void_p]
+        lib.mlvc_backend_name.argtypes = [C.c_void_p]
+        lib.mlvc_backend_load.argtypes = [C.c_void_p, C.c_char_p, _i64p, C.c_int]
+        lib.mlvc_backend_io_count.argtypes = [C.c_void_p, C.c_int, C.POINTER(C.c_int)]
+        lib.mlvc_backend_io_shape.argtypes = [C.c_void_p, C.c_int, C.c_int, _i64p, C.POINTER(C.c_int)]
+        lib.mlvc_backend_run.argtypes = [C.c_void_p, C.POINTER(_u16p), C.POINTER(_u16p)]
+        lib.mlvc_backend_reset_state.argtypes = [C.c_void_p]
+        lib.mlvc_backend_available.argtypes = [C.c_char_p, C.c_size_t]
+        lib.mlvc_hip_backend_upload_inputs.argtypes = [C.c_void_p, C.POINTER(_u16p)]
+        lib.mlvc_hip_backend_time_frames.argtypes = [C.c_void_p, C.c_int, C.POINTER(C.c_float)]
+        lib.mlvc_hip_backend_download_outputs.argtypes = [C.c_void_p, C.POINTER(_u16p)]
+        lib.mlvc_hip_backend_launch_count.argtypes = [C.c_void_p, C.POINTER(C.c_int)]
+        lib.mlvc_hip_backend_launch_info.argtypes = [C.c_void_p, C.c_int, C.c_char_p, C.c_size_t, C.c_char_p,
+                                                     C.c_size_t, C.POINTER(C.c_double), C.POINTER(C.c_double)]
+        lib.mlvc_hip_backend_time_launch.argtypes = [C.c_void_p, C.c_int, C.c_int, C.POINTER(C.c_float)]
+        lib.mlvc_synth_configs.argtypes = [C.c_char_p, C.c_size_t]
+        lib.mlvc_synth_write.argtypes = [C.c_char_p, C.c_char_p, C.c_uint64]
+        lib.mlvc_synth_input.argtypes = [C.c_char_p, C.c_int, C.c_int, C.c_uint64, _u16p, C.c_size_t]
+        lib.mlvc_synth_bindings.argtypes = [C.c_char_p, _i64p, C.c_int, C.POINTER(C.c_int), C.POINTER(C.c_int)]
+        lib.mlvc_aot_inspect.argtypes = [C.c_char_p, C.c_char_p, C.POINTER(C.c_int), C.POINTER(C.c_int),
+                                         C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]
+        _lib = lib
+    return _lib
+
+
+def device_lib() -> C.CDLL:
+    global _dev
+    if _dev is None:
+        _dev = _load(DEVICE_LIB)
+        _dev.mlvc_hip_last_error.restype = C.c_char_p
+    return _dev
+
+
+def _check(rc: int) -> None:
+    if rc != 0:
+        raise MlvcError(backend_lib().mlvc_backend_last_error().decode())
+
+
+def _ptrs(arrays):
+    arr = (_u16p * len(arrays))()
+    for i, a in enumerate(arrays):
+        arr[i] = a.ctypes.data_as(_u16p)
+    return arr
+
+
+def available_backends() -> list[str]:
+    buf = C.create_string_buffer(4096)
+    _check(backend_lib().mlvc_backend_available(buf, len(buf)))
+    return [s for s in buf.value.decode().split(",") if s]
+
+
+class Backend:
+    """An mlvc::InferenceBackend created through the registry."""
+
+    def __init__(self, model_dir: str | pathlib.Path, backend_name: str = "hip", device_id: int = 0,
+                 num_threads: int = 0):
+        self._lib = backend_lib()
+        h = C.c_void_p()
+        _check(self._lib.mlvc_backend_create(backend_name.encode(), str(model_dir).encode(), device_id, num_threads,
+                                             C.byref(h)))
+        self._h = h
+        self.in_shapes: list[tuple[int, ...]] = []
+        self.out_shapes: list[tuple[int, ...]] = []
+
+    @property
+    def name(self) -> str:
+        return self._lib.mlvc_backend_name(self._h).decode()
+
+    def close(self) -> None:
+        if self._h:
+            self._lib.mlvc_backend_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def _shapes(self, is_output: int) -> list[tuple[int, ...]]:
+        n = C.c_int()
+        _check(self._lib.mlvc_backend_io_count(self._h, is_output, C.byref(n)))
+        out = []
+        for i in range(n.value):
+            s = (C.c_int64 * 4)()
+            r = C.c_int()
+            _check(self._lib.mlvc_backend_io_shape(self._h, is_output, i, s, C.byref(r)))
+            out.append(tuple(int(s[j]) for j in range(r.value)))
+        return out
+
+    def load(self, model_name: str, bindings=()) -> None:
+        flat = (C.c_int64 * max(1, 2 * len(bindings)))(*[v for b in bindings for v in b])
+        _check(self._lib.mlvc_backend_load(self._h, model_name.encode(), flat, len(bindings)))
+        self.in_shapes = self._shapes(0)
+        self.out_shapes = self._shapes(1)
+
+    def _check_inputs(self, inputs):
+        if len(inputs) != len(self.in_shapes):
+            raise MlvcError("graph input count mismatch")
+        arrs = []
+        for a, s in zip(inputs, self.in_shapes):
+            a = np.ascontiguousarray(a, dtype=np.uint16)
+            if a.size != int(np.prod(s)):
+                raise MlvcError("graph input shape mismatch")
+            arrs.append(a)
+        return arrs
+
+    def run(self, inputs) -> list[np.ndarray]:
+        arrs = self._check_inputs(inputs)
+        outs = [np.empty(s, dtype=np.uint16) for s in self.out_shapes]
+        _check(self._lib.mlvc_backend_run(self._h, _ptrs(arrs), _ptrs(outs)))
+        return outs
+
+    def reset_state(self) -> None:
+        _check(self._lib.mlvc_backend_reset_state(self._h))
+
+    # ---- device-resident measurement helpers ("hip" backend only) ----
+    def upload_inputs(self, inputs) -> None:
+        arrs = self._check_inputs(inputs)
+        _check(self._lib.mlvc_hip_backend_upload_inputs(self._h, _ptrs(arrs)))
+
+    def time_frames(self, frames: int) -> float:
+        ms = C.c_float()
+        _check(self._lib.mlvc_hip_backend_time_frames(self._h, frames, C.byref(ms)))
+        return ms.value
+
+    def download_outputs(self) -> list[np.ndarray]:
+        outs = [np.empty(s, dtype=np.uint16) for s in self.out_shapes]
+        _check(self._lib.mlvc_hip_backend_download_outputs(self._h, _ptrs(outs)))
+        return outs
+
+    def launches(self) -> list[dict]:
+        n = C.c_int()
+        _check(self._lib.mlvc_hip_backend_launch_count(self._h, C.byref(n)))
+        out = []
+        for i in range(n.value):
+            name = C.create_string_buffer(256)
+            kind = C.create_string_buffer(256)
+            fl, by = C.c_double(), C.c_double()
+            _check(self._lib.mlvc_hip_backend_launch_info(self._h, i, name, 256, kind, 256, C.byref(fl), C.byref(by)))
+            out.append({"index": i, "name": name.value.decode(), "kind": kind.value.decode(),
+                        "flops": fl.value, "bytes": by.value})
+        return out
+
+    def time_launch(self, index: int, reps: int) -> float:
+        ms = C.c_float()
+        _check(self._lib.mlvc_hip_backend_time_launch(self._h, index, reps, C.byref(ms)))
+        return ms.value
+
+
+# ---- seeded synthetic graphs ----------------------------------------------
+
+def synth_configs() -> list[str]:
+    buf = C.create_string_buffer(4096)
+    _check(backend_lib().mlvc_synth_configs(buf, len(buf)))
+    return buf.value.decode().split(",")
+
+
+def synth_write(config: str, out_dir: str | pathlib.Path, seed: int = 0) -> None:
+    _check(backend_lib().mlvc_synth_write(config.encode(), str(out_dir).encode(), seed))
+
+
+def synth_input(config: str, index: int, frame: int, shape, seed: int = 0) -> np.ndarray:
+    a = np.empty(shape, dtype=np.uint16)
+    _check(backend_lib().mlvc_synth_input(config.encode(), index, frame, seed, a.ctypes.data_as(_u16p), a.size))
+    return a
+
+
+def synth_bindings(config: str) -> tuple[list[tuple[int, int]], int]:
+    pairs = (C.c_int64 * 16)()
+    n, frames = C.c_int(), C.c_int()
+    _check(backend_lib().mlvc_synth_bindings(config.encode(), pairs, 8, C.byref(n), C.byref(frames)))
+    return [(int(pairs[2 * i]), int(pairs[2 * i + 1])) for i in range(n.value)], frames.value
+
+
+def aot_inspect(model_dir, model_name: str) -> dict:
+    """Loads and validates aot/<model>/graph.pb without touching a GPU."""
+    nodes, tensors = C.c_int(), C.c_int()
+    arena, weights = C.c_uint64(), C.c_uint64()
+    _check(backend_lib().mlvc_aot_inspect(str(model_dir).encode(), model_name.encode(), C.byref(nodes),
+                                          C.byref(tensors), C.byref(arena), C.byref(weights)))
+    return {"nodes": nodes.value, "tensors": tensors.value, "arena_bytes": arena.value,
+            "weights_bytes": weights.value}

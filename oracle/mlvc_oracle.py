@@ -1,0 +1,241 @@
+"""ctypes binding of the CPU oracle (oracle/liboracle.so) and of the
+reference CPU kernels built from source (oracle/_ref/libmlvc_ref_kernels.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's cpu_baseline leg, as the checker and the CPU baseline. The
+product never imports this module.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import pathlib
+
+import numpy as np
+
+HERE = pathlib.Path(__file__).resolve().parent
+ORACLE_LIB = HERE / "liboracle.so"
+REF_LIB = HERE / "_ref" / "libmlvc_ref_kernels.so"
+
+_u16p = C.POINTER(C.c_uint16)
+_i64p = C.POINTER(C.c_int64)
+
+
+class OracleError(RuntimeError):
+    pass
+
+
+def _kernel_api(lib: C.CDLL, prefix: str) -> None:
+    f = lambda name: getattr(lib, prefix + name)  # noqa: E731
+    f("last_error").restype = C.c_char_p
+    f("pack_conv").argtypes = [_u16p, _u16p, C.c_int, C.c_int, C.c_int, C.c_int, _u16p, C.c_size_t]
+    f("pack_depthwise").argtypes = [_u16p, _u16p, C.c_int, C.c_int, C.c_int, _u16p, C.c_size_t]
+    f("gemm_nhwc").argtypes = [C.c_size_t, C.c_size_t, C.c_size_t, _u16p, _u16p, _u16p, C.c_int, C.c_float, C.c_float,
+                               C.c_float, _u16p, C.c_int, C.c_int]
+    f("spatial_conv_nhwc").argtypes = [_u16p, _u16p, _u16p] + [C.c_int] * 15 + [C.c_float, _u16p, C.c_int, C.c_int]
+    f("depthwise_nhwc").argtypes = [_u16p, _u16p, _u16p] + [C.c_int] * 14
+    f("leaky_relu").argtypes = [_u16p, _u16p, C.c_size_t, C.c_float, C.c_int]
+    f("add").argtypes = [_u16p, _u16p, _u16p, C.c_size_t, C.c_int]
+    f("depth_to_space_nhwc").argtypes = [_u16p, _u16p] + [C.c_int] * 5
+    f("space_to_depth_nhwc").argtypes = [_u16p, _u16p] + [C.c_int] * 5
+    f("nchw_to_nhwc").argtypes = [_u16p, _u16p, C.c_size_t, C.c_size_t, C.c_size_t]
+    f("nhwc_to_nchw").argtypes = [_u16p, _u16p, C.c_size_t, C.c_size_t, C.c_size_t]
+    f("float_to_half").argtypes = [C.c_float]
+    f("float_to_half").restype = C.c_uint16
+    f("half_to_float").argtypes = [C.c_uint16]
+    f("half_to_float").restype = C.c_float
+
+
+_oracle = None
+_ref = None
+
+
+def oracle_lib() -> C.CDLL:
+    global _oracle
+    if _oracle is None:
+        if not ORACLE_LIB.exists():
+            raise OracleError(f"{ORACLE_LIB} is not built; run `python mlvc.cpp_amd/build.py`")
+        lib = C.CDLL(str(ORACLE_LIB))
+        _kernel_api(lib, "oracle_")
+        lib.oracle_packed_conv_elems.restype = C.c_size_t
+        lib.oracle_packed_conv_elems.argtypes = [C.c_int] * 4
+        lib.oracle_packed_depthwise_elems.restype = C.c_size_t
+        lib.oracle_packed_depthwise_elems.argtypes = [C.c_int] * 3
+        lib.oracle_load.restype = C.c_void_p
+        lib.oracle_load.argtypes = [C.c_char_p, C.c_char_p, _i64p, C.c_int, C.c_int, C.c_int, C.c_int]
+        lib.oracle_free.argtypes = [C.c_void_p]
+        lib.oracle_reset_state.argtypes = [C.c_void_p]
+        lib.oracle_thread_count.argtypes = [C.c_void_p]
+        lib.oracle_step_count.argtypes = [C.c_void_p]
+        lib.oracle_io_count.argtypes = [C.c_void_p, C.c_int]
+        lib.oracle_io_shape.argtypes = [C.c_void_p, C.c_int, C.c_int, _i64p, C.POINTER(C.c_int)]
+        lib.oracle_run.argtypes = [C.c_void_p, C.POINTER(_u16p), C.POINTER(_u16p)]
+        _oracle = lib
+    return _oracle
+
+
+def ref_available() -> bool:
+    return REF_LIB.exists()
+
+
+def ref_lib() -> C.CDLL:
+    global _ref
+    if _ref is None:
+        if not REF_LIB.exists():
+            raise OracleError(f"{REF_LIB} is not built (needs the reference checkout)")
+        lib = C.CDLL(str(REF_LIB))
+        _kernel_api(lib, "ref_")
+        _ref = lib
+    return _ref
+
+
+def _p(a) -> C.POINTER(C.c_uint16):
+    return None if a is None else a.ctypes.data_as(_u16p)
+
+
+class Kernels:
+    """Kernel-level entry points (NHWC buffers) of the oracle or reference."""
+
+    def __init__(self, which: str = "oracle"):
+        self.lib = oracle_lib() if which == "oracle" else ref_lib()
+        self.prefix = "oracle_" if which == "oracle" else "ref_"
+
+    def _call(self, name, *args):
+        rc = getattr(self.lib, self.prefix + name)(*args)
+        if rc != 0:
+            raise OracleError(getattr(self.lib, self.prefix + "last_error")().decode())
+
+    def pack_conv(self, w, b, oc, ic, kh, kw):
+        n = oracle_lib().oracle_packed_conv_elems(oc, ic, kh, kw)
+        out = np.zeros(n, np.uint16)
+        self._call("pack_conv", _p(w), _p(b), oc, ic, kh, kw, _p(out), n)
+        return out
+
+    def pack_depthwise(self, w, b, c, kh, kw):
+        n = oracle_lib().oracle_packed_depthwise_elems(c, kh, kw)
+        out = np.zeros(n, np.uint16)
+        self._call("pack_depthwise", _p(w), _p(b), c, kh, kw, _p(out), n)
+        return out
+
+    def gemm(self, m, n, k, lhs, packed, epi=0, alpha=0.01, cmin=0.0, cmax=0.0, residual=None, isa=0, threads=2):
+        out = np.zeros(m * n, np.uint16)
+        self._call("gemm_nhwc", m, n, k, _p(lhs), _p(packed), _p(out), epi, alpha, cmin, cmax, _p(residual), isa,
+                   threads)
+        return out
+
+    def spatial_conv(self, x, packed, n, ic, ih, iw, oc, oh, ow, kh, kw, sh, sw, ph, pw, epi=0, alpha=0.01,
+                     residual=None, isa=0, threads=2):
+        out = np.zeros(n * oh * ow * oc, np.uint16)
+        self._call("spatial_conv_nhwc", _p(x), _p(packed), _p(out), n, ic, ih, iw, oc, oh, ow, kh, kw, sh, sw, ph, pw,
+                   epi, alpha, _p(residual), isa, threads)
+        return out
+
+    def depthwise(self, x, packed, n, c, ih, iw, oh, ow, kh, kw, sh, sw, ph, pw, isa=0, threads=2):
+        out = np.zeros(n * oh * ow * c, np.uint16)
+        self._call("depthwise_nhwc", _p(x), _p(packed), _p(out), n, c, ih, iw, oh, ow, kh, kw, sh, sw, ph, pw, isa,
+                   threads)
+        return out
+
+    def leaky_relu(self, x, alpha, isa=0):
+        out = np.zeros_like(x)
+        self._call("leaky_relu", _p(x), _p(out), x.size, alpha, isa)
+        return out
+
+    def add(self, a, b, isa=0):
+        out = np.zeros_like(a)
+        self._call("add", _p(a), _p(b), _p(out), a.size, isa)
+        return out
+
+    def depth_to_space(self, x, n, c, h, w, block):
+        out = np.zeros_like(x)
+        self._call("depth_to_space_nhwc", _p(x), _p(out), n, c, h, w, block)
+        return out
+
+    def space_to_depth(self, x, n, c, h, w, block):
+        out = np.zeros_like(x)
+        self._call("space_to_depth_nhwc", _p(x), _p(out), n, c, h, w, block)
+        return out
+
+    def nchw_to_nhwc(self, x, n, c, hw):
+        out = np.zeros_like(x)
+        self._call("nchw_to_nhwc", _p(x), _p(out), n, c, hw)
+        return out
+
+    def nhwc_to_nchw(self, x, n, hw, c):
+        out = np.zeros_like(x)
+        self._call("nhwc_to_nchw", _p(x), _p(out), n, hw, c)
+        return out
+
+    def float_to_half(self, f: float) -> int:
+        return int(getattr(self.lib, self.prefix + "float_to_half")(f))
+
+    def half_to_float(self, h: int) -> float:
+        return float(getattr(self.lib, self.prefix + "half_to_float")(h))
+
+
+class OraclePlan:
+    """Graph-level oracle: the reference CpuExecutionPlan restated."""
+
+    def __init__(self, model_dir, model_name: str, bindings=(), num_threads: int = 0, isa: int = 0,
+                 fusion: bool = True):
+        lib = oracle_lib()
+        flat = (C.c_int64 * max(1, 2 * len(bindings)))(*[v for b in bindings for v in b])
+        h = lib.oracle_load(str(model_dir).encode(), model_name.encode(), flat, len(bindings), num_threads, isa,
+                            1 if fusion else 0)
+        if not h:
+            raise OracleError(lib.oracle_last_error().decode())
+        self._lib, self._h = lib, h
+        self.in_shapes = [self._shape(0, i) for i in range(lib.oracle_io_count(h, 0))]
+        self.out_shapes = [self._shape(1, i) for i in range(lib.oracle_io_count(h, 1))]
+
+    def _shape(self, is_out, i):
+        s = (C.c_int64 * 4)()
+        r = C.c_int()
+        if self._lib.oracle_io_shape(self._h, is_out, i, s, C.byref(r)) != 0:
+            raise OracleError(self._lib.oracle_last_error().decode())
+        return tuple(int(s[j]) for j in range(r.value))
+
+    @property
+    def threads(self) -> int:
+        return self._lib.oracle_thread_count(self._h)
+
+    @property
+    def steps(self) -> int:
+        return self._lib.oracle_step_count(self._h)
+
+    def reset_state(self) -> None:
+        if self._lib.oracle_reset_state(self._h) != 0:
+            raise OracleError(self._lib.oracle_last_error().decode())
+
+    def run(self, inputs) -> list[np.ndarray]:
+        ins = [np.ascontiguousarray(a, dtype=np.uint16) for a in inputs]
+        if len(ins) != len(self.in_shapes):
+            raise OracleError("graph input count mismatch")
+        outs = [np.empty(s, np.uint16) for s in self.out_shapes]
+        ip = (_u16p * len(ins))(*[_p(a) for a in ins])
+        op = (_u16p * len(outs))(*[_p(a) for a in outs])
+        if self._lib.oracle_run(self._h, ip, op) != 0:
+            raise OracleError(self._lib.oracle_last_error().decode())
+        return outs
+
+    def close(self) -> None:
+        if self._h:
+            self._lib.oracle_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def parity_stats(got: np.ndarray, want: np.ndarray) -> dict:
+    """max|d|/RMS(want) and mean|d|/RMS(want) over FP16 tensors (raw bits)."""
+    g = got.view(np.float16).astype(np.float64)
+    w = want.view(np.float16).astype(np.float64)
+    rms = float(np.sqrt(np.mean(w * w)))
+    d = np.abs(g - w)
+    scale = rms if rms > 0 else 1.0
+    return {"max_rel": float(d.max() / scale), "mean_rel": float(d.mean() / scale), "rms": rms,
+            "finite": bool(np.isfinite(g).all())}

@@ -1,0 +1,74 @@
+/*
+ * CPU oracle for the FP16 conv-graph path — TEST INFRASTRUCTURE ONLY.
+ *
+ * A restatement of the reference CPU backend (backends/cpu) used as the
+ * parity checker for the HIP backend and as the CPU baseline timed by
+ * bench.py. Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * leg may load it. Nothing in the product links or calls it.
+ *
+ * All buffers are host memory. FP16 values are raw binary16 bit patterns.
+ * Graph-level tensors are NCHW at this interface (the oracle re-lays them
+ * to NHWC internally exactly like the reference plan); kernel-level entry
+ * points take the NHWC buffers and packed weights the reference kernels
+ * take. Every function returns 0 on success and -1 on error, with the
+ * message available from oracle_last_error().
+ */
+#ifndef MLVC_ORACLE_H
+#define MLVC_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+const char* oracle_last_error(void);
+
+/* ISA selector: 0 = AVX2+FMA+F16C path (reference default on x86),
+ * 1 = scalar path (reference MLVC_CPU_ISA=scalar). */
+
+/* ---- graph level: CpuExecutionPlan (execution_plan.cpp:241-254) ---- */
+/* bindings: n_bindings pairs (graph input index, graph output index). */
+void* oracle_load(const char* model_dir, const char* model_name, const int64_t* bindings,
+                  int n_bindings, int num_threads, int isa, int enable_fusion);
+void oracle_free(void* plan);
+int oracle_reset_state(void* plan);
+int oracle_thread_count(void* plan);
+int oracle_step_count(void* plan);
+/* Counts and shapes of external inputs / outputs (bound state removed). */
+int oracle_io_count(void* plan, int is_output);
+int oracle_io_shape(void* plan, int is_output, int index, int64_t* shape4, int* rank);
+int oracle_run(void* plan, const uint16_t* const* inputs, uint16_t* const* outputs);
+
+/* ---- kernel level (NHWC buffers, reference kernel signatures) ---- */
+int oracle_pack_conv(const uint16_t* w_oihw, const uint16_t* bias, int oc, int ic, int kh, int kw,
+                     uint16_t* packed, size_t packed_elems);
+size_t oracle_packed_conv_elems(int oc, int ic, int kh, int kw);
+int oracle_pack_depthwise(const uint16_t* w_c1hw, const uint16_t* bias, int c, int kh, int kw,
+                          uint16_t* packed, size_t packed_elems);
+size_t oracle_packed_depthwise_elems(int c, int kh, int kw);
+/* epi: 0 none, 1 clamp, 2 leaky relu, 3 residual add (residual NHWC [m, n]). */
+int oracle_gemm_nhwc(size_t m, size_t n, size_t k, const uint16_t* lhs, const uint16_t* packed,
+                     uint16_t* dst, int epi, float alpha, float cmin, float cmax,
+                     const uint16_t* residual, int isa, int threads);
+int oracle_spatial_conv_nhwc(const uint16_t* input, const uint16_t* packed, uint16_t* output, int n,
+                             int ic, int ih, int iw, int oc, int oh, int ow, int kh, int kw, int sh,
+                             int sw, int ph, int pw, int epi, float alpha, const uint16_t* residual,
+                             int isa, int threads);
+int oracle_depthwise_nhwc(const uint16_t* input, const uint16_t* packed, uint16_t* output, int n,
+                          int c, int ih, int iw, int oh, int ow, int kh, int kw, int sh, int sw,
+                          int ph, int pw, int isa, int threads);
+int oracle_leaky_relu(const uint16_t* in, uint16_t* out, size_t count, float alpha, int isa);
+int oracle_add(const uint16_t* a, const uint16_t* b, uint16_t* out, size_t count, int isa);
+int oracle_depth_to_space_nhwc(const uint16_t* in, uint16_t* out, int n, int c, int h, int w, int block);
+int oracle_space_to_depth_nhwc(const uint16_t* in, uint16_t* out, int n, int c, int h, int w, int block);
+int oracle_nchw_to_nhwc(const uint16_t* in, uint16_t* out, size_t n, size_t c, size_t hw);
+int oracle_nhwc_to_nchw(const uint16_t* in, uint16_t* out, size_t n, size_t hw, size_t c);
+uint16_t oracle_float_to_half(float f);
+float oracle_half_to_float(uint16_t h);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
