@@ -390,7 +390,8 @@ const Variant& variant_of(const mlvc_hip_conv_desc& d)
     return kVariants[d.variant];
 }
 
-void validate(const mlvc_hip_conv_desc& d)
+// Geometry and fusion checks (planning and launch); pointers at launch only.
+void validate(const mlvc_hip_conv_desc& d, bool pointers)
 {
     if (d.n <= 0 || d.ic <= 0 || d.ih <= 0 || d.iw <= 0 || d.oc <= 0 || d.oh <= 0 || d.ow <= 0 || d.kh <= 0 ||
         d.kw <= 0 || d.stride_h <= 0 || d.stride_w <= 0 || d.pad_h < 0 || d.pad_w < 0)
@@ -402,8 +403,9 @@ void validate(const mlvc_hip_conv_desc& d)
     if (d.x2 && (d.ic_split <= 0 || d.ic_split >= d.ic)) throw std::runtime_error("conv: invalid concat split");
     if (d.out_d2s_block > 1 && d.oc % (d.out_d2s_block * d.out_d2s_block) != 0)
         throw std::runtime_error("conv: invalid depth_to_space fusion");
+    if (!pointers) return;
     if (d.epilogue == MLVC_EPI_RESIDUAL_ADD && !d.residual) throw std::runtime_error("conv: residual missing");
-    if (!d.x || !d.y) throw std::runtime_error("conv: null tensor");
+    if (!d.x || !d.y || !d.packed_w || !d.bias) throw std::runtime_error("conv: null tensor");
 }
 
 // Geometry as the kernel sees it (1x1 convs run over flattened pixels).
@@ -430,7 +432,7 @@ extern "C" {
 int mlvc_hip_conv_plan(mlvc_hip_conv_desc* desc)
 {
     return guard([&] {
-        validate(*desc);
+        validate(*desc, false);
         const mlvc_hip_conv_desc& d = *desc;
         int ih, iw, oh, ow;
         kernel_geometry(d, ih, iw, oh, ow);
@@ -514,7 +516,7 @@ int mlvc_hip_conv_launch(const mlvc_hip_conv_desc* desc, mlvc_hip_stream s)
 {
     return guard([&] {
         const mlvc_hip_conv_desc& d = *desc;
-        validate(d);
+        validate(d, true);
         const Variant& k = variant_of(d);
         ConvArgs a{};
         a.x = static_cast<const std::uint16_t*>(d.x);
