@@ -32,7 +32,7 @@ def _kernel_api(lib: C.CDLL, prefix: str) -> None:
     f("pack_depthwise").argtypes = [_u16p, _u16p, C.c_int, C.c_int, C.c_int, _u16p, C.c_size_t]
     f("gemm_nhwc").argtypes = [C.c_size_t, C.c_size_t, C.c_size_t, _u16p, _u16p, _u16p, C.c_int, C.c_float, C.c_float,
                                C.c_float, _u16p, C.c_int, C.c_int]
-    f("spatial_conv_nhwc").argtypes = [_u16p, _u16p, _u16p] + [C.c_int] * 15 + [C.c_float, _u16p, C.c_int, C.c_int]
+    f("spatial_conv_nhwc").argtypes = [_u16p, _u16p, _u16p] + [C.c_int] * 14 + [C.c_float, _u16p, C.c_int, C.c_int]
     f("depthwise_nhwc").argtypes = [_u16p, _u16p, _u16p] + [C.c_int] * 14
     f("leaky_relu").argtypes = [_u16p, _u16p, C.c_size_t, C.c_float, C.c_int]
     f("add").argtypes = [_u16p, _u16p, _u16p, C.c_size_t, C.c_int]
