@@ -116,6 +116,34 @@ int mlvc_hip_depthwise(const void* x, const uint16_t* w, const float* bias, void
                        int ih, int iw, int oh, int ow, int kh, int kw, int stride_h, int stride_w,
                        int pad_h, int pad_w, mlvc_hip_stream s);
 
+/* ---- fused depthwise-separable residual block ----
+ * y = fp16(fp16(W2 e + b2) + x), e = fp16(LeakyReLU(fp16(W1 d + b1))),
+ * d = fp16(DW3x3(x) + b0): one kernel for the DW conv (depthwise_conv.cu),
+ * the 1x1 expand with LeakyReLU epilogue and the 1x1 project with residual
+ * epilogue (pointwise_conv.cu / cutlass.cu EVT epilogues) that the
+ * reference runs as three launches; rounding points are unchanged.
+ * x, y: [n, c, h, w]; dw_w: [c, 1, 3, 3] fp16 (stride 1, pad 1);
+ * w1: W1 [e, c] packed by mlvc_hip_dwblock_pack; w2: W2 [c, e] packed. */
+typedef struct mlvc_hip_dwblock_desc {
+    int n, c, e, h, w;
+    const void* x;
+    void* y;
+    const uint16_t* dw_w;
+    const float* dw_b;
+    const void* w1;
+    const float* b1;
+    const void* w2;
+    const float* b2;
+    float alpha;
+} mlvc_hip_dwblock_desc;
+
+/* 1 when (c, e, h, w) has a fused-block kernel, else 0. */
+int mlvc_hip_dwblock_supported(int c, int e, int h, int w);
+size_t mlvc_hip_dwblock_packed_bytes(int m, int k);
+/* Host-side repack of a row-major [m, k] fp16 matrix into MFMA A-fragment order. */
+int mlvc_hip_dwblock_pack(const uint16_t* w_mk, int m, int k, void* dst_host);
+int mlvc_hip_dwblock_launch(const mlvc_hip_dwblock_desc* desc, mlvc_hip_stream s);
+
 /* ---- pixel layout, CRD (tensor_ops.cu:62-116, mode 1) ----
  * DEPTH_TO_SPACE: in [n, c*b*b, h, w] -> out [n, c, h*b, w*b].
  * SPACE_TO_DEPTH: in [n, c, h, w] -> out [n, c*b*b, h/b, w/b]. */

@@ -26,6 +26,7 @@
 #include "mlvc_hip_device.h"
 
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <set>
@@ -38,6 +39,16 @@ using aot::Op;
 using aot::TensorId;
 
 [[noreturn]] void fail(const std::string& what) { throw std::runtime_error("hip: " + what); }
+
+// MLVC_HIP_DISABLE_FUSION=1 lowers every node to its own kernel (the
+// counterpart of the reference's MLVC_CPU_DISABLE_FUSION,
+// backends/cpu/src/execution_plan.cpp:89-93); used to check that fused and
+// unfused schedules agree.
+bool fusion_enabled()
+{
+    const char* env = std::getenv("MLVC_HIP_DISABLE_FUSION");
+    return !(env && env[0] == '1' && env[1] == '\0');
+}
 
 void hip_check(int rc, const char* what)
 {
@@ -88,11 +99,12 @@ struct HostMem {
 };
 
 struct Launch {
-    enum Kind { kConv, kDepthwise, kLeaky, kAdd, kD2S, kS2D, kConcat } kind = kConv;
+    enum Kind { kConv, kDepthwise, kDwBlock, kLeaky, kAdd, kD2S, kS2D, kConcat } kind = kConv;
     std::string name, kind_name;
     TensorId x = 0, x2 = 0, res = 0, y = 0;  // tensors read (x, x2, res) and written (y)
     mlvc_hip_conv_desc conv{};
-    DeviceMem packed, bias;
+    mlvc_hip_dwblock_desc blk{};
+    DeviceMem packed, bias, packed2, bias2, packed3, bias3;
     int n = 0, c = 0, ih = 0, iw = 0, oh = 0, ow = 0, kh = 0, kw = 0, sh = 1, sw = 1, ph = 0, pw = 0;
     int block = 0, ca = 0, cb = 0;
     std::size_t count = 0, hw = 0;
@@ -313,7 +325,9 @@ private:
         };
         // Producers folded into the input staging of their only consumer conv.
         std::vector<bool> folded(ns.size(), false);
+        const bool fuse = fusion_enabled();
         for (const aot::Node& n : ns) {
+            if (!fuse) break;
             const TensorId out = n.outputs[0];
             if ((n.op != Op::SPACE_TO_DEPTH && n.op != Op::CONCAT) || !internal_single(out)) continue;
             const aot::Node& c = ns[first_consumer[out]];
@@ -336,8 +350,8 @@ private:
             switch (n.op) {
             case Op::CONV:
                 if (n.conv().groups == 1) {
-                    lower_conv(*L, n, producer, folded, done, internal_single, first_consumer);
-                } else {
+                    lower_conv(*L, n, producer, folded, done, internal_single, first_consumer, fuse);
+                } else if (!(fuse && lower_dwblock(*L, n, done, internal_single, first_consumer))) {
                     lower_depthwise(*L, n);
                 }
                 break;
@@ -435,7 +449,8 @@ private:
 
     template <typename SingleFn>
     void lower_conv(Launch& L, const aot::Node& n, std::map<TensorId, std::size_t>& producer, const std::vector<bool>& folded,
-                    std::vector<bool>& done, SingleFn internal_single, std::map<TensorId, std::size_t>& first_consumer)
+                    std::vector<bool>& done, SingleFn internal_single, std::map<TensorId, std::size_t>& first_consumer,
+                    bool fuse)
     {
         const auto& ns = nodes();
         const auto& xs = desc(n.inputs[0]).shape;
@@ -482,7 +497,7 @@ private:
         }
         // Epilogue (fusion_matcher.cpp:352-411).
         TensorId out = n.outputs[0];
-        if (n.index + 1 < ns.size() && internal_single(out)) {
+        if (fuse && n.index + 1 < ns.size() && internal_single(out)) {
             const aot::Node& nx = ns[n.index + 1];
             if (nx.op == Op::LEAKY_RELU && nx.inputs[0] == out) {
                 d.epilogue = MLVC_EPI_LEAKY_RELU;
@@ -502,7 +517,7 @@ private:
             }
         }
         // Output side: a DEPTH_TO_SPACE that is the only consumer.
-        if (internal_single(out)) {
+        if (fuse && internal_single(out)) {
             const aot::Node& c = ns[first_consumer[out]];
             if (c.op == Op::DEPTH_TO_SPACE && c.inputs[0] == out && !done[c.index]) {
                 d.out_d2s_block = c.block_size();
@@ -529,6 +544,94 @@ private:
         L.flops = 2.0 * d.n * d.oc * d.oh * d.ow * static_cast<double>(d.ic) * d.kh * d.kw;
         L.bytes = 2.0 * (static_cast<double>(d.n) * d.ic * d.ih * d.iw + static_cast<double>(d.oc) * d.ic * d.kh * d.kw + d.oc +
                          static_cast<double>(d.n) * d.oc * d.oh * d.ow * (L.res ? 2.0 : 1.0));
+    }
+
+    // DW3x3 s1 p1 -> 1x1 C->E -> LEAKY_RELU -> 1x1 E->C -> ADD(block input),
+    // every intermediate with exactly one consumer and not a graph output.
+    template <typename SingleFn>
+    bool lower_dwblock(Launch& L, const aot::Node& n0, std::vector<bool>& done, SingleFn internal_single,
+                       std::map<TensorId, std::size_t>& first_consumer)
+    {
+        const auto& ns = nodes();
+        const TensorId t = n0.inputs[0];
+        const auto& xs = desc(t).shape;
+        const auto& ws = desc(n0.inputs[1]).shape;
+        if (xs.size() != 4 || ws.size() != 4 || is_weight(t) || desc(t).dtype != aot::DataType::FP16) return false;
+        const auto& a0 = n0.conv();
+        const int c = static_cast<int>(xs[1]);
+        if (a0.groups != c || ws[0] != c || ws[1] != 1 || ws[2] != 3 || ws[3] != 3 || a0.strides != std::array<int, 2>{1, 1} ||
+            a0.pads != std::array<int, 4>{1, 1, 1, 1} || desc(n0.outputs[0]).shape != xs)
+            return false;
+        auto next = [&](TensorId id) -> const aot::Node* {
+            if (!internal_single(id)) return nullptr;
+            return &ns[first_consumer[id]];
+        };
+        auto is_pointwise = [&](const aot::Node* m, TensorId in) {
+            if (!m || m->op != Op::CONV || m->inputs[0] != in || m->conv().groups != 1 || !is_weight(m->inputs[1])) return false;
+            const auto& w = desc(m->inputs[1]).shape;
+            return w.size() == 4 && w[2] == 1 && w[3] == 1 && m->conv().strides == std::array<int, 2>{1, 1} &&
+                   m->conv().pads == std::array<int, 4>{0, 0, 0, 0};
+        };
+        const aot::Node* n1 = next(n0.outputs[0]);
+        if (!is_pointwise(n1, n0.outputs[0])) return false;
+        const aot::Node* n2 = next(n1->outputs[0]);
+        if (!n2 || n2->op != Op::LEAKY_RELU || n2->inputs[0] != n1->outputs[0]) return false;
+        const aot::Node* n3 = next(n2->outputs[0]);
+        if (!is_pointwise(n3, n2->outputs[0])) return false;
+        const aot::Node* n4 = next(n3->outputs[0]);
+        if (!n4 || n4->op != Op::ADD) return false;
+        const TensorId f = n3->outputs[0];
+        if (!((n4->inputs[0] == f && n4->inputs[1] == t) || (n4->inputs[1] == f && n4->inputs[0] == t))) return false;
+        const int e = static_cast<int>(desc(n1->inputs[1]).shape[0]);
+        if (desc(n3->inputs[1]).shape[0] != c || desc(n3->inputs[1]).shape[1] != e || desc(n1->inputs[1]).shape[1] != c ||
+            desc(n4->outputs[0]).shape != xs)
+            return false;
+        const int h = static_cast<int>(xs[2]), w = static_cast<int>(xs[3]);
+        if (!mlvc_hip_dwblock_supported(c, e, h, w)) return false;
+
+        L.kind = Launch::kDwBlock;
+        L.kind_name = "dwblock_c" + std::to_string(c) + "_e" + std::to_string(e);
+        L.name = desc(n0.outputs[0]).name + "+block";
+        L.x = t;
+        L.y = n4->outputs[0];
+        auto upload = [&](DeviceMem& dst, std::vector<std::uint8_t> bytes) {
+            dst = DeviceMem(bytes.size());
+            pending_uploads_.push_back({dst.ptr, std::move(bytes)});
+        };
+        auto as_bytes = [](const void* p, std::size_t n) {
+            std::vector<std::uint8_t> v(n);
+            std::memcpy(v.data(), p, n);
+            return v;
+        };
+        const auto wdw = weight_fp16(n0.inputs[1]);
+        upload(L.packed, as_bytes(wdw.data(), wdw.size() * 2));
+        const auto bdw = bias_f32(n0, c, static_cast<std::size_t>(c));
+        upload(L.bias, as_bytes(bdw.data(), bdw.size() * 4));
+        const auto w1 = weight_fp16(n1->inputs[1]);
+        std::vector<std::uint8_t> p1(mlvc_hip_dwblock_packed_bytes(e, c));
+        hip_check(mlvc_hip_dwblock_pack(w1.data(), e, c, p1.data()), "block weight packing");
+        upload(L.packed2, std::move(p1));
+        const auto b1 = bias_f32(*n1, e, static_cast<std::size_t>(e));
+        upload(L.bias2, as_bytes(b1.data(), b1.size() * 4));
+        const auto w2 = weight_fp16(n3->inputs[1]);
+        std::vector<std::uint8_t> p2(mlvc_hip_dwblock_packed_bytes(c, e));
+        hip_check(mlvc_hip_dwblock_pack(w2.data(), c, e, p2.data()), "block weight packing");
+        upload(L.packed3, std::move(p2));
+        const auto b2 = bias_f32(*n3, c, static_cast<std::size_t>(c));
+        upload(L.bias3, as_bytes(b2.data(), b2.size() * 4));
+        mlvc_hip_dwblock_desc& d = L.blk;
+        d = mlvc_hip_dwblock_desc{};
+        d.n = static_cast<int>(xs[0]);
+        d.c = c;
+        d.e = e;
+        d.h = h;
+        d.w = w;
+        d.alpha = n2->alpha();
+        for (const aot::Node* m : {n1, n2, n3, n4}) done[m->index] = true;
+        const double px = static_cast<double>(d.n) * h * w;
+        L.flops = 2.0 * px * c * 9 + 4.0 * px * c * e;
+        L.bytes = 2.0 * (2.0 * px * c + 9.0 * c + 2.0 * c * e) + 4.0 * (2.0 * c + e);
+        return true;
     }
 
     void lower_depthwise(Launch& L, const aot::Node& n)
@@ -677,6 +780,19 @@ private:
                                          l.ow, l.kh, l.kw, l.sh, l.sw, l.ph, l.pw, stream_),
                       "depthwise launch");
             break;
+        case Launch::kDwBlock: {
+            mlvc_hip_dwblock_desc d = l.blk;
+            d.x = ptr(l.x, parity);
+            d.y = ptr(l.y, parity);
+            d.dw_w = static_cast<const std::uint16_t*>(l.packed.ptr);
+            d.dw_b = static_cast<const float*>(l.bias.ptr);
+            d.w1 = l.packed2.ptr;
+            d.b1 = static_cast<const float*>(l.bias2.ptr);
+            d.w2 = l.packed3.ptr;
+            d.b2 = static_cast<const float*>(l.bias3.ptr);
+            hip_check(mlvc_hip_dwblock_launch(&d, stream_), "dwblock launch");
+            break;
+        }
         case Launch::kLeaky:
             hip_check(mlvc_hip_leaky_relu(ptr(l.x, parity), ptr(l.y, parity), l.count, l.alpha, stream_), "leaky_relu launch");
             break;

@@ -203,7 +203,7 @@ const std::vector<ConfigEntry>& registry()
         {"mlvc_s_640x368", [](GraphBuilder& g, Rng& r, SyntheticModel& i) { build_mlvc(g, r, i, 368, 640, 3, 6, 8); }},
         {"mlvc_1920x1088", [](GraphBuilder& g, Rng& r, SyntheticModel& i) { build_mlvc(g, r, i, 1088, 1920, 4, 12, 32); }},
         {"mlvc_s_tiny", [](GraphBuilder& g, Rng& r, SyntheticModel& i) { build_mlvc(g, r, i, 32, 64, 3, 2, 4); }},
-        {"mlvc_tiny", [](GraphBuilder& g, Rng& r, SyntheticModel& i) { build_mlvc(g, r, i, 64, 96, 4, 2, 4); }},
+        {"mlvc_tiny", [](GraphBuilder& g, Rng& r, SyntheticModel& i) { build_mlvc(g, r, i, 64, 128, 4, 2, 4); }},
     };
     return entries;
 }

@@ -113,3 +113,29 @@ def test_device_resident_replay_matches_run(tmp_path):
     assert (got[0] == want[0]).all()
     a.close()
     b.close()
+
+
+@pytest.mark.parametrize("config", ["mlvc_s_tiny", "mlvc_tiny", "dwblock_92x160_c128", "dwblock_46x80_c256"])
+def test_fused_and_unfused_schedules_bit_identical(tmp_path, monkeypatch, config):
+    """Every GPU fusion (S2D/CONCAT loads, epilogues, D2S stores, the fused
+    depthwise-separable block) keeps the unfused rounding points and K order,
+    so both schedules give identical bits."""
+    bindings, _ = _write(tmp_path, config)
+    fused = mlvc_hip.Backend(tmp_path, "hip")
+    fused.load(config, bindings)
+    monkeypatch.setenv("MLVC_HIP_DISABLE_FUSION", "1")
+    plain = mlvc_hip.Backend(tmp_path, "hip")
+    plain.load(config, bindings)
+    monkeypatch.delenv("MLVC_HIP_DISABLE_FUSION")
+    assert len(fused.launches()) < len(plain.launches())
+    kinds = " ".join(l["kind"] for l in fused.launches())
+    assert "dwblock" in kinds, kinds
+    for b in (fused, plain):
+        if bindings:
+            b.reset_state()
+    for f in range(2):
+        ins = [mlvc_hip.synth_input(config, i, f, s) for i, s in enumerate(fused.in_shapes)]
+        for g, p in zip(fused.run(ins), plain.run(ins)):
+            assert (g == p).all(), f"frame {f}"
+    fused.close()
+    plain.close()
