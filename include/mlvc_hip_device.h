@@ -94,6 +94,7 @@ typedef struct mlvc_hip_conv_desc {
     void* y;
     int out_d2s_block;
     int variant;                       /* tile configuration; set by mlvc_hip_conv_plan */
+    int vector_io;                     /* 16-byte row staging eligible; set by mlvc_hip_conv_plan */
 } mlvc_hip_conv_desc;
 
 /* Chooses the kernel variant for the geometry (sets desc->variant). */

@@ -132,9 +132,10 @@ __device__ __forceinline__ void store_output(const ConvArgs& a, std::uint16_t h,
     }
 }
 
-template <int BM_, int TH_, int TW_, int KH_, int KW_, int S_, int KC_>
+template <int BM_, int TH_, int TW_, int KH_, int KW_, int S_, int KC_, bool VEC_>
 struct Cfg {
     static constexpr int BM = BM_, TH = TH_, TW = TW_, KH = KH_, KW = KW_, S = S_, KC = KC_;
+    static constexpr bool VEC = VEC_;  // 16-byte row-segment staging (needs W % 8 == 0)
     static constexpr int kThreads = 256;
     static constexpr int BN = TH * TW;
     static constexpr int TAPS = KH * KW;
@@ -144,22 +145,37 @@ struct Cfg {
     static constexpr int NT = WN / 32;
     static constexpr int IH_T = (TH - 1) * S + KH;
     static constexpr int IW_T = (TW - 1) * S + KW;
-    static constexpr int IW_E = (IW_T + 1) / 2;  // even columns (stride 2 layout)
+    // Vector staging covers input columns [floor8(ix0), floor8(ix0) + IW_S).
+    static constexpr int NSEG = (IW_T + 14) / 8;
+    static constexpr int IW_S = VEC ? NSEG * 8 : IW_T;
+    static constexpr int IW_E = (IW_S + 1) / 2;  // even columns (stride-2 layout)
     static constexpr int PST = KC + 8;           // LDS halves per staged pixel
+    // One extra 16-byte pad per 8 staged columns keeps both the transposed
+    // 8-pixel writes and the consecutive-pixel B reads free of bank conflicts.
+    static constexpr int ROW = IW_S * PST + ((IW_S - 1) / 8 + 1) * 8;
+    static constexpr int IN_LDS = IH_T * ROW;
+    static constexpr int UNITS = (KC / 8) * IH_T * NSEG;  // 8 channels x 8 columns
+    static constexpr int UNITS_PER_T = (UNITS + kThreads - 1) / kThreads;
     static constexpr int IN_PIX = IH_T * IW_T;
-    static constexpr int IN_LDS = IN_PIX * PST;
-    static constexpr int W_LDS = TAPS * KS * MT * 64 * 8;  // halves per chunk
     static constexpr int PIX_PER_T = (IN_PIX + kThreads - 1) / kThreads;
+    static constexpr int W_LDS = TAPS * KS * MT * 64 * 8;  // halves per chunk
     static constexpr int W_VEC = W_LDS / 8;
     static constexpr int W_PER_T = (W_VEC + kThreads - 1) / kThreads;
     static constexpr int EPI_ROW = BN + 8;  // output staging row (one channel), halves
     static constexpr int EPI_LDS = BM * EPI_ROW;
     static constexpr int LDS = (IN_LDS + W_LDS) > EPI_LDS ? (IN_LDS + W_LDS) : EPI_LDS;
-    static_assert(BM % 32 == 0 && WN % 32 == 0 && KC % 16 == 0, "tile shape");
+    static_assert(BM % 32 == 0 && WN % 32 == 0 && KC % 16 == 0 && TW % 8 == 0, "tile shape");
     static_assert(LDS * 2 <= 160 * 1024, "LDS budget");
 
-    __device__ static constexpr int col(int xi) { return S == 2 ? ((xi & 1) ? IW_E + (xi >> 1) : (xi >> 1)) : xi; }
+    __device__ static constexpr int col(int x) { return S == 2 ? ((x & 1) ? IW_E + (x >> 1) : (x >> 1)) : x; }
+    // LDS offset (halves) of staged pixel (row, column).
+    __device__ static constexpr int at(int row, int x) { return row * ROW + col(x) * PST + (col(x) >> 3) * 8; }
 };
+
+__device__ __forceinline__ std::uint32_t pack_half(std::uint32_t lo_word, std::uint32_t hi_word, bool upper)
+{
+    return upper ? ((lo_word >> 16) | (hi_word & 0xFFFF0000u)) : ((lo_word & 0xFFFFu) | (hi_word << 16));
+}
 
 template <class C>
 __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a)
@@ -173,6 +189,9 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a)
     const int tx0 = (tile % a.tiles_x) * C::TW, ty0 = (tile / a.tiles_x) * C::TH;
     const int ocb = blockIdx.y, b = blockIdx.z;
     const int iy0 = ty0 * C::S - a.ph, ix0 = tx0 * C::S - a.pw;
+    // First staged input column (8-aligned for the vector path).
+    const int xa = C::VEC ? ix0 - (((ix0 % 8) + 8) % 8) : ix0;
+    const int col_off = ix0 - xa;
 
     floatx16 acc[C::MT][C::NT];
 #pragma unroll
@@ -184,16 +203,43 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a)
             for (int nt = 0; nt < C::NT; ++nt) acc[mt][nt][r] = bv;
         }
 
-    std::uint32_t in_reg[C::PIX_PER_T][C::KC / 2];
+    const size_t hw = static_cast<size_t>(a.ih) * a.iw;
+    const int c1 = a.x2 ? a.ic_split : a.ic;
+    u32x4 vin[C::VEC ? C::UNITS_PER_T : 1][8];
+    std::uint32_t in_reg[C::VEC ? 1 : C::PIX_PER_T][C::KC / 2];
     u32x4 w_reg[C::W_PER_T];
     auto fetch = [&](int chunk) {
         const int c0 = chunk * C::KC;
+        if constexpr (C::VEC) {
 #pragma unroll
-        for (int i = 0; i < C::PIX_PER_T; ++i) {
-            const int pix = tid + i * C::kThreads;
-            if (pix < C::IN_PIX) {
-                const int yi = pix / C::IW_T, xi = pix - yi * C::IW_T;
-                load_pixel<C::KC>(a, b, c0, iy0 + yi, ix0 + xi, in_reg[i]);
+            for (int i = 0; i < C::UNITS_PER_T; ++i) {
+                const int u = tid + i * C::kThreads;
+                if (u < C::UNITS) {
+                    const int sg = u % C::NSEG, yi = (u / C::NSEG) % C::IH_T, c8 = u / (C::NSEG * C::IH_T);
+                    const int iy = iy0 + yi, ix = xa + sg * 8;
+                    const bool ok = iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw;
+                    const size_t po = static_cast<size_t>(iy) * a.iw + ix;
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) {
+                        const int c = c0 + c8 * 8 + k;
+                        u32x4 v = {0u, 0u, 0u, 0u};
+                        if (ok && c < a.ic) {
+                            const std::uint16_t* src = c < c1 ? a.x + (static_cast<size_t>(b) * c1 + c) * hw
+                                                              : a.x2 + (static_cast<size_t>(b) * (a.ic - c1) + c - c1) * hw;
+                            v = *reinterpret_cast<const u32x4*>(src + po);
+                        }
+                        vin[i][k] = v;
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < C::PIX_PER_T; ++i) {
+                const int pix = tid + i * C::kThreads;
+                if (pix < C::IN_PIX) {
+                    const int yi = pix / C::IW_T, xi = pix - yi * C::IW_T;
+                    load_pixel<C::KC>(a, b, c0, iy0 + yi, ix0 + xi, in_reg[i]);
+                }
             }
         }
         const u32x4* ws = reinterpret_cast<const u32x4*>(a.w + (static_cast<size_t>(ocb) * a.nchunks + chunk) * C::W_LDS);
@@ -204,15 +250,35 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a)
         }
     };
     auto commit = [&]() {
+        if constexpr (C::VEC) {
+            // 8x8 transpose in registers: staged pixel j of the segment gets
+            // the 8 channels of the unit as one 16-byte LDS write.
 #pragma unroll
-        for (int i = 0; i < C::PIX_PER_T; ++i) {
-            const int pix = tid + i * C::kThreads;
-            if (pix < C::IN_PIX) {
-                const int yi = pix / C::IW_T, xi = pix - yi * C::IW_T;
-                u32x4* dst = reinterpret_cast<u32x4*>(&lds_in[(yi * C::IW_T + C::col(xi)) * C::PST]);
+            for (int i = 0; i < C::UNITS_PER_T; ++i) {
+                const int u = tid + i * C::kThreads;
+                if (u < C::UNITS) {
+                    const int sg = u % C::NSEG, yi = (u / C::NSEG) % C::IH_T, c8 = u / (C::NSEG * C::IH_T);
 #pragma unroll
-                for (int q = 0; q < C::KC / 8; ++q)
-                    dst[q] = u32x4{in_reg[i][4 * q], in_reg[i][4 * q + 1], in_reg[i][4 * q + 2], in_reg[i][4 * q + 3]};
+                    for (int j = 0; j < 8; ++j) {
+                        const bool up = j & 1;
+                        const int wd = j >> 1;
+                        const u32x4 t = {pack_half(vin[i][0][wd], vin[i][1][wd], up), pack_half(vin[i][2][wd], vin[i][3][wd], up),
+                                         pack_half(vin[i][4][wd], vin[i][5][wd], up), pack_half(vin[i][6][wd], vin[i][7][wd], up)};
+                        *reinterpret_cast<u32x4*>(&lds_in[C::at(yi, sg * 8 + j) + c8 * 8]) = t;
+                    }
+                }
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < C::PIX_PER_T; ++i) {
+                const int pix = tid + i * C::kThreads;
+                if (pix < C::IN_PIX) {
+                    const int yi = pix / C::IW_T, xi = pix - yi * C::IW_T;
+                    u32x4* dst = reinterpret_cast<u32x4*>(&lds_in[C::at(yi, xi)]);
+#pragma unroll
+                    for (int q = 0; q < C::KC / 8; ++q)
+                        dst[q] = u32x4{in_reg[i][4 * q], in_reg[i][4 * q + 1], in_reg[i][4 * q + 2], in_reg[i][4 * q + 3]};
+                }
             }
         }
 #pragma unroll
@@ -228,7 +294,7 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a)
     for (int nt = 0; nt < C::NT; ++nt) {
         const int p = wave * C::WN + nt * 32 + (lane & 31);
         pyi[nt] = (p / C::TW) * C::S;
-        pxi[nt] = (p % C::TW) * C::S;
+        pxi[nt] = (p % C::TW) * C::S + col_off;
     }
     const int koff = (lane >> 5) * 8;
 
@@ -241,6 +307,9 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a)
 #pragma unroll
         for (int tap = 0; tap < C::TAPS; ++tap) {
             const int ky = tap / C::KW, kx = tap % C::KW;
+            int boff[C::NT];
+#pragma unroll
+            for (int nt = 0; nt < C::NT; ++nt) boff[nt] = C::at(pyi[nt] + ky, pxi[nt] + kx) + koff;
 #pragma unroll
             for (int ks = 0; ks < C::KS; ++ks) {
                 half8 av[C::MT], bv[C::NT];
@@ -248,10 +317,7 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a)
                 for (int mt = 0; mt < C::MT; ++mt)
                     av[mt] = *reinterpret_cast<const half8*>(&lds_w[(((tap * C::KS + ks) * C::MT + mt) * 64 + lane) * 8]);
 #pragma unroll
-                for (int nt = 0; nt < C::NT; ++nt) {
-                    const int pix = (pyi[nt] + ky) * C::IW_T + C::col(pxi[nt] + kx);
-                    bv[nt] = *reinterpret_cast<const half8*>(&lds_in[pix * C::PST + ks * 16 + koff]);
-                }
+                for (int nt = 0; nt < C::NT; ++nt) bv[nt] = *reinterpret_cast<const half8*>(&lds_in[boff[nt] + ks * 16]);
 #pragma unroll
                 for (int mt = 0; mt < C::MT; ++mt)
 #pragma unroll
@@ -280,21 +346,78 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a)
                 lds[ocl * C::EPI_ROW + pl] = f2h(acc[mt][nt][r]);
             }
     __syncthreads();
-    // Stage 2: consecutive threads take consecutive pixels of one channel,
-    // apply the epilogue to the rounded value and store.
-    for (int e = tid; e < C::BM * C::BN; e += C::kThreads) {
-        const int ocl = e / C::BN, pl = e - ocl * C::BN;
-        const int oc = ocb * C::BM + ocl;
-        const int oy = ty0 + pl / C::TW, ox = tx0 + pl % C::TW;
-        if (oc < a.oc && oy < a.oh && ox < a.ow) {
-            std::uint16_t h = lds[ocl * C::EPI_ROW + pl];
-            if (a.epi == MLVC_EPI_LEAKY_RELU) {
-                const float f = h2f(h);
-                if (f < 0.0f) h = f2h(f * a.alpha);
-            } else if (a.epi == MLVC_EPI_RESIDUAL_ADD) {
-                h = f2h(h2f(h) + h2f(a.res[(static_cast<size_t>(b * a.oc + oc) * a.oh + oy) * a.ow + ox]));
+
+    // Stage 2: the epilogue acts on the rounded value. Vector path: 8
+    // consecutive pixels of a channel per thread, 16-byte stores; with a
+    // fused DEPTH_TO_SPACE(2) the two dx channels of one (c, dy) are
+    // interleaved into 16 contiguous output pixels.
+    constexpr int GROUPS = C::BN / 8;
+    auto epi8 = [&](std::uint16_t (&h)[8], int oc, int oy, int ox) {
+        if (a.epi == MLVC_EPI_LEAKY_RELU) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const float f = h2f(h[j]);
+                if (f < 0.0f) h[j] = f2h(f * a.alpha);
             }
-            store_output(a, h, b, oc, oy, ox);
+        } else if (a.epi == MLVC_EPI_RESIDUAL_ADD) {
+            const u32x4 rv = *reinterpret_cast<const u32x4*>(a.res + (static_cast<size_t>(b * a.oc + oc) * a.oh + oy) * a.ow + ox);
+            const std::uint16_t* r = reinterpret_cast<const std::uint16_t*>(&rv);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) h[j] = f2h(h2f(h[j]) + h2f(r[j]));
+        }
+    };
+    if (a.ow % 8 == 0 && (a.d2s <= 1 || a.d2s == 2)) {
+        const bool d2s2 = a.d2s == 2;
+        const int units = d2s2 ? (C::BM / 4) * 2 * GROUPS : C::BM * GROUPS;
+        for (int u = tid; u < units; u += C::kThreads) {
+            const int g = u % GROUPS;
+            const int pl = g * 8;
+            const int oy = ty0 + pl / C::TW, ox = tx0 + pl % C::TW;
+            if (oy >= a.oh || ox >= a.ow) continue;
+            if (d2s2) {
+                const int dy = (u / GROUPS) & 1, cq = u / (2 * GROUPS);
+                const int ocl = cq * 4 + dy * 2, oc = ocb * C::BM + ocl;
+                if (oc >= a.oc) continue;
+                std::uint16_t h0[8], h1[8];
+                *reinterpret_cast<u32x4*>(h0) = *reinterpret_cast<const u32x4*>(&lds[ocl * C::EPI_ROW + pl]);
+                *reinterpret_cast<u32x4*>(h1) = *reinterpret_cast<const u32x4*>(&lds[(ocl + 1) * C::EPI_ROW + pl]);
+                epi8(h0, oc, oy, ox);
+                epi8(h1, oc + 1, oy, ox);
+                std::uint16_t o[16];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    o[2 * j] = h0[j];
+                    o[2 * j + 1] = h1[j];
+                }
+                const int W2 = a.ow * 2;
+                std::uint16_t* dst = a.y + (static_cast<size_t>(b * (a.oc / 4) + oc / 4) * (a.oh * 2) + oy * 2 + dy) * W2 + ox * 2;
+                reinterpret_cast<u32x4*>(dst)[0] = *reinterpret_cast<const u32x4*>(o);
+                reinterpret_cast<u32x4*>(dst)[1] = *reinterpret_cast<const u32x4*>(o + 8);
+            } else {
+                const int ocl = u / GROUPS, oc = ocb * C::BM + ocl;
+                if (oc >= a.oc) continue;
+                std::uint16_t h[8];
+                *reinterpret_cast<u32x4*>(h) = *reinterpret_cast<const u32x4*>(&lds[ocl * C::EPI_ROW + pl]);
+                epi8(h, oc, oy, ox);
+                *reinterpret_cast<u32x4*>(a.y + (static_cast<size_t>(b * a.oc + oc) * a.oh + oy) * a.ow + ox) =
+                    *reinterpret_cast<const u32x4*>(h);
+            }
+        }
+    } else {
+        for (int e = tid; e < C::BM * C::BN; e += C::kThreads) {
+            const int ocl = e / C::BN, pl = e - ocl * C::BN;
+            const int oc = ocb * C::BM + ocl;
+            const int oy = ty0 + pl / C::TW, ox = tx0 + pl % C::TW;
+            if (oc < a.oc && oy < a.oh && ox < a.ow) {
+                std::uint16_t h = lds[ocl * C::EPI_ROW + pl];
+                if (a.epi == MLVC_EPI_LEAKY_RELU) {
+                    const float f = h2f(h);
+                    if (f < 0.0f) h = f2h(f * a.alpha);
+                } else if (a.epi == MLVC_EPI_RESIDUAL_ADD) {
+                    h = f2h(h2f(h) + h2f(a.res[(static_cast<size_t>(b * a.oc + oc) * a.oh + oy) * a.ow + ox]));
+                }
+                store_output(a, h, b, oc, oy, ox);
+            }
         }
     }
 }
@@ -327,7 +450,8 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(ConvArgs a, int n)
 struct Variant {
     const char* name;
     int bm, th, tw, kh, kw, s, kc;  // bm == 0: direct fallback
-    void (*launch)(const ConvArgs&, dim3, hipStream_t);
+    void (*launch_scalar)(const ConvArgs&, dim3, hipStream_t);
+    void (*launch_vec)(const ConvArgs&, dim3, hipStream_t);
 };
 
 template <class C>
@@ -338,10 +462,10 @@ void launch_mfma(const ConvArgs& a, dim3 grid, hipStream_t s)
 
 #define MLVC_VARIANT(BM, TH, TW, KH, KW, S, KC)                                                       \
     Variant{"mfma_bm" #BM "_" #TH "x" #TW "_k" #KH "x" #KW "_s" #S "_kc" #KC, BM, TH, TW, KH, KW, S, KC, \
-            &launch_mfma<Cfg<BM, TH, TW, KH, KW, S, KC>>}
+            &launch_mfma<Cfg<BM, TH, TW, KH, KW, S, KC, false>>, &launch_mfma<Cfg<BM, TH, TW, KH, KW, S, KC, true>>}
 
 const Variant kVariants[] = {
-    Variant{"direct_fp32", 0, 0, 0, 0, 0, 0, 0, nullptr},
+    Variant{"direct_fp32", 0, 0, 0, 0, 0, 0, 0, nullptr, nullptr},
     // 3x3 stride 1
     MLVC_VARIANT(64, 4, 64, 3, 3, 1, 16),
     MLVC_VARIANT(64, 8, 32, 3, 3, 1, 16),
@@ -456,6 +580,9 @@ int mlvc_hip_conv_plan(mlvc_hip_conv_desc* desc)
             }
         }
         desc->variant = best;
+        // 16-byte row-segment staging: plain or channel-concat input whose
+        // split falls on 8 channels, rows of 8-aligned width.
+        desc->vector_io = best != 0 && d.in_s2d_block <= 1 && (!d.x2 || d.ic_split % 8 == 0) && iw % 8 == 0;
     });
 }
 
@@ -548,11 +675,14 @@ int mlvc_hip_conv_launch(const mlvc_hip_conv_desc* desc, mlvc_hip_stream s)
                 throw std::runtime_error("conv: variant does not match the geometry");
             kernel_geometry(d, a.ih, a.iw, a.oh, a.ow);
             if (a.s2d > 1 && a.ih == 1 && d.ih != 1) throw std::runtime_error("conv: flattened geometry with fusion");
+            const bool aligned = (reinterpret_cast<std::uintptr_t>(d.x) & 15u) == 0 &&
+                                 (!d.x2 || (reinterpret_cast<std::uintptr_t>(d.x2) & 15u) == 0);
+            const bool vec = d.vector_io && aligned && a.s2d <= 1 && (!a.x2 || a.ic_split % 8 == 0) && a.iw % 8 == 0;
             a.tiles_x = (a.ow + k.tw - 1) / k.tw;
             a.nchunks = (d.ic + k.kc - 1) / k.kc;
             const unsigned tiles = static_cast<unsigned>(a.tiles_x * ((a.oh + k.th - 1) / k.th));
             const dim3 grid(tiles, static_cast<unsigned>((d.oc + k.bm - 1) / k.bm), static_cast<unsigned>(d.n));
-            k.launch(a, grid, to_stream(s));
+            (vec ? k.launch_vec : k.launch_scalar)(a, grid, to_stream(s));
         }
         check(hipGetLastError(), "conv kernel launch");
     });
