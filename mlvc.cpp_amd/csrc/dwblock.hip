@@ -8,16 +8,22 @@
 // conv with a LeakyReLU epilogue and a conv with a residual epilogue:
 // backends/cpu/src/kernels_x86_avx2.cpp:237-302, kernels_scalar.cpp:178-192),
 // but d and e never leave the chip. One workgroup (4 waves) owns a 4x8 pixel
-// tile and all channels:
-//   1. x is staged in channel chunks of 64 as 16-byte vectors (rows padded to
-//      24 halves so the 3x3 halo of an 8-wide, 8-aligned tile is covered);
-//      the depthwise result goes to LDS channel-last, d[pixel][C + 8];
-//   2. expand: each wave owns E/128 m-tiles of 32 channels; A fragments (W1,
-//      pre-packed in fragment order) stream from L2 one k-step ahead, B
-//      fragments are 16-byte LDS reads of d; e goes to LDS as e[pixel][E + 8];
-//   3. project: each wave owns C/128 m-tiles; the residual is read from x in
-//      global memory (L2-hot) and the result stored NCHW.
-// Requires W % 8 == 0 (16-byte aligned rows); other shapes run unfused.
+// tile and all channels. At 1920x1088 / 16 the grid is one workgroup per CU,
+// so the kernel is bound by how fast each CU streams the 2*C*E weight halves
+// it needs, not by MFMA issue. It is organised around that stream:
+//   * every wave runs ONE register ring of RING weight fragments (16 bytes per
+//     lane, pre-packed in A-fragment order) through both GEMMs, so W1 and then
+//     W2 are in flight from the first instruction to the last MFMA, across
+//     the depthwise stage and the barriers between stages;
+//   * the 6x24 halo tile of all C channels is staged with one batch of
+//     16-byte loads; each thread then runs the depthwise taps for two
+//     adjacent channels from registers and writes d[pixel][C + 8] as packed
+//     pairs;
+//   * accumulators are seeded with the bias (float4 loads issued at start);
+//   * the project result is rounded into LDS as [channel][pixel] and leaves
+//     as 16-byte rows with the residual added from 16-byte loads of x.
+// LDS: xs (halo tile) aliases es (expand result); ds (depthwise result)
+// aliases ys (project result). Requires W % 8 == 0 (16-byte rows).
 
 #include "common.hpp"
 #include "mlvc_hip_device.h"
@@ -28,8 +34,10 @@ namespace mlvc_hip {
 namespace {
 
 constexpr int kTH = 4, kTW = 8, kP = kTH * kTW;  // 32 pixels per workgroup
-constexpr int kCC = 64;                           // depthwise channel chunk
 constexpr int kRow = 24;                          // staged halves per input row
+constexpr int kXC = (kTH + 2) * kRow + 8;         // staged halves per channel (+8: bank spread)
+constexpr int kYS = kP + 8;                       // ys row stride (halves)
+constexpr int kRing = 16;                         // weight fragments in flight per wave
 
 struct DwBlockArgs {
     const std::uint16_t* x;
@@ -44,142 +52,255 @@ struct DwBlockArgs {
     float alpha;
 };
 
+// LDS-only barrier: waits for this wave's LDS traffic, not for its global
+// loads, so the weight ring stays in flight across stages.
+__device__ __forceinline__ void lds_barrier()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+__device__ __forceinline__ float lo_h(std::uint32_t v) { return h2f(static_cast<std::uint16_t>(v & 0xFFFFu)); }
+__device__ __forceinline__ float hi_h(std::uint32_t v) { return h2f(static_cast<std::uint16_t>(v >> 16)); }
+
 template <int C, int E>
 __global__ __launch_bounds__(256) void dwblock_kernel(DwBlockArgs a)
 {
     constexpr int DST = C + 8, EST = E + 8;
-    constexpr int XS = kCC * (kTH + 2) * kRow;
     constexpr int MT1 = E / 32 / 4, MT2 = C / 32 / 4;  // m-tiles per wave
     constexpr int KS1 = C / 16, KS2 = E / 16;
+    constexpr int NF1 = MT1 * KS1, NF = NF1 + MT2 * KS2;  // fragments per wave
+    constexpr int XV = C * (kTH + 2) * 3 / 256;           // staged 16-byte vectors per thread
+    constexpr int RV = C * kTH / 256;                     // residual rows per thread
+    constexpr int CP = C / 2, RPT = kTH * CP / 256;       // channel pairs, output rows per thread
     static_assert(C % 128 == 0 && E % 128 == 0, "channel counts");
-    __shared__ __attribute__((aligned(16))) std::uint16_t xs[XS];
-    __shared__ __attribute__((aligned(16))) std::uint16_t ds[kP * DST];
-    __shared__ __attribute__((aligned(16))) std::uint16_t es[kP * EST];
+    static_assert(C * (kTH + 2) * 3 % 256 == 0 && C * kTH % 256 == 0 && kTH * CP % 256 == 0, "thread mapping");
+    constexpr int XS_BYTES = C * kXC * 2, ES_BYTES = kP * EST * 2;
+    constexpr int DS_BYTES = kP * DST * 2, YS_BYTES = C * kYS * 2;
+    __shared__ __attribute__((aligned(16))) std::uint8_t lds_a[XS_BYTES > ES_BYTES ? XS_BYTES : ES_BYTES];
+    __shared__ __attribute__((aligned(16))) std::uint8_t lds_b[DS_BYTES > YS_BYTES ? DS_BYTES : YS_BYTES];
+    std::uint16_t* xs = reinterpret_cast<std::uint16_t*>(lds_a);
+    std::uint16_t* es = reinterpret_cast<std::uint16_t*>(lds_a);
+    std::uint16_t* ds = reinterpret_cast<std::uint16_t*>(lds_b);
+    std::uint16_t* ys = reinterpret_cast<std::uint16_t*>(lds_b);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int x0 = (blockIdx.x % a.tiles_x) * kTW, y0 = (blockIdx.x / a.tiles_x) * kTH;
     const int b = blockIdx.y;
     const size_t plane = static_cast<size_t>(a.h) * a.w;
     const std::uint16_t* xb = a.x + static_cast<size_t>(b) * C * plane;
+    const u32x4* w1 = reinterpret_cast<const u32x4*>(a.w1);
+    const u32x4* w2 = reinterpret_cast<const u32x4*>(a.w2);
+    const int koff = (lane >> 5) * 8, pl = lane & 31, hsel = 4 * (lane >> 5);
 
-    // ---- 1. depthwise 3x3, channel chunks of 64 -------------------------
-    for (int c0 = 0; c0 < C; c0 += kCC) {
-        // 64 channels x 6 rows x 3 vectors of 8 halves.
-        for (int v = tid; v < kCC * (kTH + 2) * 3; v += 256) {
-            const int seg = v % 3, row = (v / 3) % (kTH + 2), c = v / (3 * (kTH + 2));
-            const int iy = y0 - 1 + row, ix = x0 - 8 + seg * 8;
-            u32x4 val = {0u, 0u, 0u, 0u};
-            if (iy >= 0 && iy < a.h && ix >= 0 && ix < a.w)
-                val = *reinterpret_cast<const u32x4*>(xb + (c0 + c) * plane + static_cast<size_t>(iy) * a.w + ix);
-            *reinterpret_cast<u32x4*>(&xs[(c * (kTH + 2) + row) * kRow + seg * 8]) = val;
+    // Fragment f of this wave's stream: W1 in (k-step, m-tile) order, then W2.
+    auto frag = [&](int f) -> u32x4 {
+        if (f < NF1) return w1[((wave * MT1 + f % MT1) * KS1 + f / MT1) * 64 + lane];
+        f -= NF1;
+        return w2[((wave * MT2 + f % MT2) * KS2 + f / MT2) * 64 + lane];
+    };
+    u32x4 ring[kRing];
+#pragma unroll
+    for (int f = 0; f < kRing; ++f) ring[f] = frag(f);
+
+    // Expand accumulators seeded with b1: lane holds rows 8j + hsel + (0..3).
+    floatx16 acc1[MT1];
+#pragma unroll
+    for (int m = 0; m < MT1; ++m)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const floatx4 bv = *reinterpret_cast<const floatx4*>(a.b1 + (wave * MT1 + m) * 32 + 8 * j + hsel);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc1[m][4 * j + i] = bv[i];
         }
-        __syncthreads();
-        for (int o = tid; o < kCC * kP; o += 256) {
-            const int p = o % kP, c = o / kP;
-            const int py = p / kTW, px = p % kTW;
-            const int gy = y0 + py, gx = x0 + px;
-            const int ch = c0 + c;
-            float acc = a.dw_b[ch];
-            const std::uint16_t* wc = a.dw_w + ch * 9;
+    // The scheduler would otherwise sink every ring load down to its MFMA
+    // (minimising live registers) and serialise the stream on L2 latency;
+    // scheduling barriers keep each load in the stage that issues it.
+    __builtin_amdgcn_sched_barrier(0);
+
+    // ---- 1. stage the 6-row halo of all C channels (one batch of loads) ----
+    // Loads are unconditional (addresses clamped into the image, out-of-image
+    // vectors zeroed afterwards): a branch around a load makes the compiler
+    // wait for every load in flight, the weight ring included.
+    {
+        u32x4 v[XV];
 #pragma unroll
-            for (int ky = 0; ky < 3; ++ky) {
-                const int iy = gy + ky - 1;
-                if (iy < 0 || iy >= a.h) continue;
+        for (int i = 0; i < XV; ++i) {
+            const int q = tid + 256 * i;
+            const int seg = q % 3, row = (q / 3) % (kTH + 2), c = q / (3 * (kTH + 2));
+            const int iy = min(max(y0 - 1 + row, 0), a.h - 1), ix = min(max(x0 - 8 + seg * 8, 0), a.w - 8);
+            v[i] = *reinterpret_cast<const u32x4*>(xb + c * plane + static_cast<size_t>(iy) * a.w + ix);
+        }
 #pragma unroll
-                for (int kx = 0; kx < 3; ++kx) {
-                    const int ix = gx + kx - 1;
-                    if (ix < 0 || ix >= a.w) continue;
-                    acc = fmaf(h2f(xs[(c * (kTH + 2) + py + ky) * kRow + 7 + px + kx]), h2f(wc[ky * 3 + kx]), acc);
+        for (int i = 0; i < XV; ++i) {
+            const int q = tid + 256 * i;
+            const int seg = q % 3, row = (q / 3) % (kTH + 2), c = q / (3 * (kTH + 2));
+            const int iy = y0 - 1 + row, ix = x0 - 8 + seg * 8;
+            const bool in = iy >= 0 && iy < a.h && ix >= 0 && ix < a.w;
+            *reinterpret_cast<u32x4*>(&xs[c * kXC + row * kRow + seg * 8]) = in ? v[i] : u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+    // Depthwise weights and bias of this thread's channel pair.
+    const int cp = tid % CP, rg = tid / CP;
+    std::uint32_t wdw[9];
+#pragma unroll
+    for (int i = 0; i < 9; ++i) wdw[i] = reinterpret_cast<const std::uint32_t*>(a.dw_w)[cp * 9 + i];
+    const float bd0 = a.dw_b[2 * cp], bd1 = a.dw_b[2 * cp + 1];
+    lds_barrier();
+
+    // ---- 2. depthwise 3x3 for channels 2cp, 2cp+1, output rows rg*RPT.. ----
+    {
+        const bool left = x0 > 0, right = x0 + kTW < a.w;
+        float d0[RPT][kTW], d1[RPT][kTW];
+#pragma unroll
+        for (int r = 0; r < RPT; ++r)
+#pragma unroll
+            for (int px = 0; px < kTW; ++px) {
+                d0[r][px] = bd0;
+                d1[r][px] = bd1;
+            }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const std::uint16_t* xc = xs + (2 * cp + j) * kXC;
+            float wt[9];
+#pragma unroll
+            for (int t = 0; t < 9; ++t) {
+                const int e = j * 9 + t;  // halves 18cp + e of the pair's weights
+                wt[t] = (e & 1) ? hi_h(wdw[e >> 1]) : lo_h(wdw[e >> 1]);
+            }
+#pragma unroll
+            for (int r = 0; r < RPT; ++r) {
+                const int orow = rg * RPT + r, gy = y0 + orow;
+#pragma unroll
+                for (int ky = 0; ky < 3; ++ky) {
+                    const int iy = gy + ky - 1;
+                    if (iy < 0 || iy >= a.h) continue;
+                    const std::uint16_t* row = xc + (orow + ky) * kRow;
+                    const std::uint32_t l = *reinterpret_cast<const std::uint32_t*>(row + 6);
+                    const u32x4 m = *reinterpret_cast<const u32x4*>(row + 8);
+                    const std::uint32_t rr = *reinterpret_cast<const std::uint32_t*>(row + 16);
+                    float xv[kTW + 2];
+                    xv[0] = hi_h(l);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        xv[1 + 2 * i] = lo_h(m[i]);
+                        xv[2 + 2 * i] = hi_h(m[i]);
+                    }
+                    xv[kTW + 1] = lo_h(rr);
+#pragma unroll
+                    for (int px = 0; px < kTW; ++px)
+#pragma unroll
+                        for (int kx = 0; kx < 3; ++kx) {
+                            if (px + kx == 0 && !left) continue;
+                            if (px + kx == kTW + 1 && !right) continue;
+                            float& acc = j ? d1[r][px] : d0[r][px];
+                            acc = fmaf(xv[px + kx], wt[ky * 3 + kx], acc);
+                        }
                 }
             }
-            ds[p * DST + ch] = f2h(acc);
         }
-        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < RPT; ++r)
+#pragma unroll
+            for (int px = 0; px < kTW; ++px) {
+                const int p = (rg * RPT + r) * kTW + px;
+                const std::uint32_t v = static_cast<std::uint32_t>(f2h(d0[r][px])) |
+                                        (static_cast<std::uint32_t>(f2h(d1[r][px])) << 16);
+                *reinterpret_cast<std::uint32_t*>(&ds[p * DST + 2 * cp]) = v;
+            }
     }
+    lds_barrier();
 
-    const int koff = (lane >> 5) * 8, pl = lane & 31;
-    // ---- 2. expand 1x1 C -> E, bias, round, LeakyReLU, round -------------
-    {
-        floatx16 acc[MT1];
+    // ---- 3. expand 1x1 C -> E, round, LeakyReLU, round -> es --------------
+#pragma unroll
+    for (int ks = 0; ks < KS1; ++ks) {
+        const half8 bv = *reinterpret_cast<const half8*>(&ds[pl * DST + ks * 16 + koff]);
 #pragma unroll
         for (int m = 0; m < MT1; ++m) {
-            const int mt = wave * MT1 + m;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[m][r] = a.b1[mt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)];
+            const int f = ks * MT1 + m;
+            const u32x4 av = ring[f % kRing];
+            if (f + kRing < NF) ring[f % kRing] = frag(f + kRing);
+            acc1[m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, av), bv, acc1[m], 0, 0, 0);
         }
-        const u32x4* w1 = reinterpret_cast<const u32x4*>(a.w1);
-        u32x4 cur[MT1], nxt[MT1];
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // Project accumulators (b2) and the residual rows, loaded ahead of use.
+    floatx16 acc2[MT2];
 #pragma unroll
-        for (int m = 0; m < MT1; ++m) cur[m] = w1[((wave * MT1 + m) * KS1 + 0) * 64 + lane];
-        for (int ks = 0; ks < KS1; ++ks) {
-            if (ks + 1 < KS1) {
+    for (int m = 0; m < MT2; ++m)
 #pragma unroll
-                for (int m = 0; m < MT1; ++m) nxt[m] = w1[((wave * MT1 + m) * KS1 + ks + 1) * 64 + lane];
-            }
-            const half8 bv = *reinterpret_cast<const half8*>(&ds[pl * DST + ks * 16 + koff]);
+        for (int j = 0; j < 4; ++j) {
+            const floatx4 bv = *reinterpret_cast<const floatx4*>(a.b2 + (wave * MT2 + m) * 32 + 8 * j + hsel);
 #pragma unroll
-            for (int m = 0; m < MT1; ++m)
-                acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, cur[m]), bv, acc[m], 0, 0, 0);
-            if (ks + 1 < KS1) {
-#pragma unroll
-                for (int m = 0; m < MT1; ++m) cur[m] = nxt[m];
-            }
+            for (int i = 0; i < 4; ++i) acc2[m][4 * j + i] = bv[i];
         }
+    u32x4 res[RV];
 #pragma unroll
-        for (int m = 0; m < MT1; ++m) {
-            const int mt = wave * MT1 + m;
+    for (int i = 0; i < RV; ++i) {
+        const int q = tid + 256 * i, ch = q / kTH, gy = min(y0 + q % kTH, a.h - 1);  // rows past h are not stored
+        res[i] = *reinterpret_cast<const u32x4*>(xb + ch * plane + static_cast<size_t>(gy) * a.w + x0);
+    }
+    // es aliases xs: every wave finished its depthwise reads before the
+    // barrier above, so the expand results may overwrite the halo tile.
 #pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                std::uint16_t hv = f2h(acc[m][r]);
-                const float f = h2f(hv);
-                if (f < 0.0f) hv = f2h(f * a.alpha);
-                es[pl * EST + mt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)] = hv;
+    for (int m = 0; m < MT1; ++m) {
+        const int mt = wave * MT1 + m;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            std::uint16_t hv[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                hv[i] = f2h(acc1[m][4 * j + i]);
+                const float f = h2f(hv[i]);
+                if (f < 0.0f) hv[i] = f2h(f * a.alpha);
             }
+            const std::uint32_t lo = hv[0] | (static_cast<std::uint32_t>(hv[1]) << 16);
+            const std::uint32_t hi = hv[2] | (static_cast<std::uint32_t>(hv[3]) << 16);
+            typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+            *reinterpret_cast<u32x2*>(&es[pl * EST + mt * 32 + 8 * j + hsel]) = u32x2{lo, hi};
         }
     }
-    __syncthreads();
-    // ---- 3. project 1x1 E -> C, bias, round, + residual, round -----------
-    {
-        floatx16 acc[MT2];
+    lds_barrier();
+
+    // ---- 4. project 1x1 E -> C, round -> ys[channel][pixel] ---------------
+#pragma unroll
+    for (int ks = 0; ks < KS2; ++ks) {
+        const half8 bv = *reinterpret_cast<const half8*>(&es[pl * EST + ks * 16 + koff]);
 #pragma unroll
         for (int m = 0; m < MT2; ++m) {
-            const int mt = wave * MT2 + m;
-#pragma unroll
-            for (int r = 0; r < 16; ++r) acc[m][r] = a.b2[mt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)];
+            const int f = NF1 + ks * MT2 + m;
+            const u32x4 av = ring[f % kRing];
+            if (f + kRing < NF) ring[f % kRing] = frag(f + kRing);
+            acc2[m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, av), bv, acc2[m], 0, 0, 0);
         }
-        const u32x4* w2 = reinterpret_cast<const u32x4*>(a.w2);
-        u32x4 cur[MT2], nxt[MT2];
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    // ys aliases ds, which no wave reads after the expand stage.
 #pragma unroll
-        for (int m = 0; m < MT2; ++m) cur[m] = w2[((wave * MT2 + m) * KS2 + 0) * 64 + lane];
-        for (int ks = 0; ks < KS2; ++ks) {
-            if (ks + 1 < KS2) {
+    for (int m = 0; m < MT2; ++m) {
+        const int mt = wave * MT2 + m;
 #pragma unroll
-                for (int m = 0; m < MT2; ++m) nxt[m] = w2[((wave * MT2 + m) * KS2 + ks + 1) * 64 + lane];
-            }
-            const half8 bv = *reinterpret_cast<const half8*>(&es[pl * EST + ks * 16 + koff]);
+        for (int r = 0; r < 16; ++r)
+            ys[(mt * 32 + 8 * (r >> 2) + hsel + (r & 3)) * kYS + pl] = f2h(acc2[m][r]);
+    }
+    lds_barrier();
+
+    // ---- 5. residual add, 16-byte rows out ------------------------------
+    std::uint16_t* yb = a.y + static_cast<size_t>(b) * C * plane;
 #pragma unroll
-            for (int m = 0; m < MT2; ++m)
-                acc[m] = __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(half8, cur[m]), bv, acc[m], 0, 0, 0);
-            if (ks + 1 < KS2) {
+    for (int i = 0; i < RV; ++i) {
+        const int q = tid + 256 * i, ch = q / kTH, row = q % kTH, gy = y0 + row;
+        if (gy >= a.h) continue;
+        const u32x4 pv = *reinterpret_cast<const u32x4*>(&ys[ch * kYS + row * kTW]);
+        u32x4 o;
 #pragma unroll
-                for (int m = 0; m < MT2; ++m) cur[m] = nxt[m];
-            }
+        for (int k = 0; k < 4; ++k) {
+            const std::uint32_t lo = f2h(lo_h(pv[k]) + lo_h(res[i][k]));
+            const std::uint32_t hi = f2h(hi_h(pv[k]) + hi_h(res[i][k]));
+            o[k] = lo | (hi << 16);
         }
-        const int gy = y0 + pl / kTW, gx = x0 + pl % kTW;
-        if (gy < a.h && gx < a.w) {
-            const size_t po = static_cast<size_t>(gy) * a.w + gx;
-            std::uint16_t* yb = a.y + static_cast<size_t>(b) * C * plane;
-#pragma unroll
-            for (int m = 0; m < MT2; ++m) {
-                const int mt = wave * MT2 + m;
-#pragma unroll
-                for (int r = 0; r < 16; ++r) {
-                    const int ch = mt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                    const std::uint16_t hv = f2h(acc[m][r]);
-                    yb[ch * plane + po] = f2h(h2f(hv) + h2f(xb[ch * plane + po]));
-                }
-            }
-        }
+        *reinterpret_cast<u32x4*>(yb + ch * plane + static_cast<size_t>(gy) * a.w + x0) = o;
     }
 }
 
