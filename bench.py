@@ -72,6 +72,67 @@ def cpu_baseline(model_dir, bindings, shape, budget_s: float):
                       f"{el:.1f} s wall, oracle AVX2+FMA+F16C path, {plan.threads} threads"}
 
 
+PMC_REPS = 10
+CALIB_BYTES = 128 << 20  # calibration stream kernel: reads and writes this many bytes
+
+
+def pmc_pass(indices) -> int:
+    """Dispatches for rocprofv3 --pmc: the calibration stream kernel (FP16
+    LeakyReLU over CALIB_BYTES, so FETCH_SIZE and WRITE_SIZE each have a
+    known algorithmic value) and then the chosen launches of the graph. Their
+    per-dispatch counters, scaled by calibration, give HBM bytes per launch."""
+    import ctypes as C
+
+    import mlvc_hip
+
+    dev = mlvc_hip.device_lib()
+    dev.mlvc_hip_malloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
+    dev.mlvc_hip_free.argtypes = [C.c_void_p]
+    dev.mlvc_hip_zero.argtypes = [C.c_void_p, C.c_size_t, C.c_void_p]
+    dev.mlvc_hip_leaky_relu.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_float, C.c_void_p]
+    dev.mlvc_hip_stream_synchronize.argtypes = [C.c_void_p]
+    bufs = [C.c_void_p(), C.c_void_p()]
+    for b in bufs:
+        if dev.mlvc_hip_malloc(C.byref(b), CALIB_BYTES) != 0:
+            raise mlvc_hip.MlvcError(dev.mlvc_hip_last_error().decode())
+    if dev.mlvc_hip_zero(bufs[0], CALIB_BYTES, None) != 0:
+        raise mlvc_hip.MlvcError(dev.mlvc_hip_last_error().decode())
+    for _ in range(PMC_REPS):
+        if dev.mlvc_hip_leaky_relu(bufs[0], bufs[1], CALIB_BYTES // 2, 0.1, None) != 0:
+            raise mlvc_hip.MlvcError(dev.mlvc_hip_last_error().decode())
+    dev.mlvc_hip_stream_synchronize(None)
+    for b in bufs:
+        dev.mlvc_hip_free(b)
+    with tempfile.TemporaryDirectory() as d:
+        mlvc_hip.synth_write(CONFIG, d, 0)
+        bindings, _ = mlvc_hip.synth_bindings(CONFIG)
+        gpu = mlvc_hip.Backend(d, "hip", device_id=0)
+        gpu.load(CONFIG, bindings)
+        gpu.upload_inputs([mlvc_hip.synth_input(CONFIG, 0, 0, gpu.in_shapes[0])])
+        gpu.reset_state()
+        gpu.time_frames(1)
+        launches = gpu.launches()
+        for i in indices:
+            log(f"pmc launch {i}: {launches[i]['name']} [{launches[i]['kind']}] x{PMC_REPS + 1}")
+            gpu.time_launch(i, PMC_REPS)
+        gpu.close()
+    log(f"pmc calibration: {PMC_REPS} x leaky_relu over {CALIB_BYTES} bytes")
+    return 0
+
+
+def measured_traffic(path, launch_name):
+    """HBM bytes per launch (FETCH_SIZE + WRITE_SIZE, calibrated) for
+    `launch_name` from a committed rocprofv3 --pmc summary, or None."""
+    try:
+        for line in pathlib.Path(path).read_text().splitlines():
+            f = line.split()
+            if len(f) == 4 and f[0] == "traffic:" and f[1] == launch_name:
+                return float(f[2]) + float(f[3])
+    except OSError:
+        pass
+    return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--gpus", type=int, default=1)
@@ -80,6 +141,11 @@ def main() -> int:
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--pmc-pass", default=None, metavar="I,J,...",
+                    help="counter-collection mode for rocprofv3 --pmc: run the calibration stream kernel, then "
+                         "launches I,J,... of the graph, PMC_REPS times each; no timing, no JSON line")
+    ap.add_argument("--traffic", default=str(REPO / "profiles" / "hbm_traffic_1920x1088.md"),
+                    help="PMC summary holding 'traffic: <launch> <fetch bytes> <write bytes>' lines")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: the per-frame schedule is a serial chain linked by the recurrent "
@@ -89,6 +155,9 @@ def main() -> int:
     rank = int(os.environ.get("RANK", "0"))
 
     import mlvc_hip
+
+    if args.pmc_pass is not None:
+        return pmc_pass([int(i) for i in args.pmc_pass.split(",") if i])
 
     with tempfile.TemporaryDirectory() as d:
         mlvc_hip.synth_write(CONFIG, d, 0)
@@ -117,7 +186,7 @@ def main() -> int:
         else:
             roof = {"bound": "hbm", "achieved": dom["bytes"] / dom_t / 1e9, "peak": PEAK_HBM_GBS, "unit": "GB/s"}
         roof["frac"] = roof["achieved"] / roof["peak"]
-        roof["traffic"] = None
+        roof["traffic"] = measured_traffic(args.traffic, dom["name"])
         roof["kernel"] = f"{dom['name']} [{dom['kind']}]"
         roof["kernel_ms"] = dom["ms"]
         log(f"{'#':>3} {'launch':28} {'kernel':48} {'us':>9} {'TFLOP/s':>8} {'GB/s':>8} {'AI':>7} bound frac")
