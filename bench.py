@@ -120,14 +120,15 @@ def pmc_pass(indices) -> int:
     return 0
 
 
-def measured_traffic(path, launch_name):
-    """HBM bytes per launch (FETCH_SIZE + WRITE_SIZE, calibrated) for
-    `launch_name` from a committed rocprofv3 --pmc summary, or None."""
+def measured_traffic(path, launch_name, kind):
+    """HBM bytes per launch (FETCH_SIZE + WRITE_SIZE, calibrated) for the
+    launch `launch_name` run by kernel variant `kind`, from a committed
+    rocprofv3 --pmc summary; None when no entry was measured on that variant."""
     try:
         for line in pathlib.Path(path).read_text().splitlines():
             f = line.split()
-            if len(f) == 4 and f[0] == "traffic:" and f[1] == launch_name:
-                return float(f[2]) + float(f[3])
+            if len(f) == 5 and f[0] == "traffic:" and f[1] == launch_name and f[2] == kind:
+                return float(f[3]) + float(f[4])
     except OSError:
         pass
     return None
@@ -145,7 +146,7 @@ def main() -> int:
                     help="counter-collection mode for rocprofv3 --pmc: run the calibration stream kernel, then "
                          "launches I,J,... of the graph, PMC_REPS times each; no timing, no JSON line")
     ap.add_argument("--traffic", default=str(REPO / "profiles" / "hbm_traffic_1920x1088.md"),
-                    help="PMC summary holding 'traffic: <launch> <fetch bytes> <write bytes>' lines")
+                    help="PMC summary holding 'traffic: <launch> <variant> <fetch bytes> <write bytes>' lines")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: the per-frame schedule is a serial chain linked by the recurrent "
@@ -186,7 +187,7 @@ def main() -> int:
         else:
             roof = {"bound": "hbm", "achieved": dom["bytes"] / dom_t / 1e9, "peak": PEAK_HBM_GBS, "unit": "GB/s"}
         roof["frac"] = roof["achieved"] / roof["peak"]
-        roof["traffic"] = measured_traffic(args.traffic, dom["name"])
+        roof["traffic"] = measured_traffic(args.traffic, dom["name"], dom["kind"])
         roof["kernel"] = f"{dom['name']} [{dom['kind']}]"
         roof["kernel_ms"] = dom["ms"]
         log(f"{'#':>3} {'launch':28} {'kernel':48} {'us':>9} {'TFLOP/s':>8} {'GB/s':>8} {'AI':>7} bound frac")

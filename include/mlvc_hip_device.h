@@ -97,8 +97,15 @@ typedef struct mlvc_hip_conv_desc {
     int vector_io;                     /* 16-byte row staging eligible; set by mlvc_hip_conv_plan */
 } mlvc_hip_conv_desc;
 
-/* Chooses the kernel variant for the geometry (sets desc->variant). */
+/* Chooses the kernel variant for the geometry by a cost model (sets
+ * desc->variant and desc->vector_io). Every 3x3 variant accumulates in the
+ * same K order, and so does every 1x1 variant, so the choice never changes
+ * results. Role of the reference's per-shape tile choice by fixed thresholds
+ * (backends/driver_cubin/src/execution_plan.cpp:151-181, 374-432). */
 int mlvc_hip_conv_plan(mlvc_hip_conv_desc* desc);
+/* Lists every variant that can run the geometry (for measuring them on the
+ * device and keeping the fastest); *count receives the total. */
+int mlvc_hip_conv_candidates(const mlvc_hip_conv_desc* desc, int* variants, int capacity, int* count);
 const char* mlvc_hip_conv_variant_name(int variant);
 size_t mlvc_hip_conv_packed_bytes(const mlvc_hip_conv_desc* desc);
 size_t mlvc_hip_conv_bias_len(const mlvc_hip_conv_desc* desc);

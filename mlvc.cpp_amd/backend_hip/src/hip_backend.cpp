@@ -105,6 +105,8 @@ struct Launch {
     mlvc_hip_conv_desc conv{};
     mlvc_hip_dwblock_desc blk{};
     DeviceMem packed, bias, packed2, bias2, packed3, bias3;
+    std::vector<std::uint16_t> w_oihw;  // conv weights kept for re-packing after tuning
+    std::vector<float> bias_oc;         // conv bias, unpadded
     int n = 0, c = 0, ih = 0, iw = 0, oh = 0, ow = 0, kh = 0, kw = 0, sh = 1, sw = 1, ph = 0, pw = 0;
     int block = 0, ca = 0, cb = 0;
     std::size_t count = 0, hw = 0;
@@ -133,6 +135,7 @@ public:
         plan_memory();
         allocate_io();
         upload_parameters();
+        if (tuning_enabled()) tune();
         capture();
         initialized_ = bindings_.empty();
     }
@@ -447,6 +450,22 @@ private:
         return b;
     }
 
+    // Packs L's weights into the fragment order of d.variant and queues the
+    // upload of weights and padded FP32 bias into (w, b).
+    void pack_conv(const Launch& L, DeviceMem& w, DeviceMem& b, const mlvc_hip_conv_desc& d)
+    {
+        std::vector<std::uint8_t> packed(mlvc_hip_conv_packed_bytes(&d));
+        hip_check(mlvc_hip_conv_pack(&d, L.w_oihw.data(), packed.data()), "weight packing");
+        w = DeviceMem(packed.size());
+        pending_uploads_.push_back({w.ptr, std::move(packed)});
+        std::vector<float> bias(mlvc_hip_conv_bias_len(&d), 0.0F);
+        std::copy(L.bias_oc.begin(), L.bias_oc.end(), bias.begin());
+        b = DeviceMem(bias.size() * 4);
+        std::vector<std::uint8_t> braw(bias.size() * 4);
+        std::memcpy(braw.data(), bias.data(), braw.size());
+        pending_uploads_.push_back({b.ptr, std::move(braw)});
+    }
+
     template <typename SingleFn>
     void lower_conv(Launch& L, const aot::Node& n, std::map<TensorId, std::size_t>& producer, const std::vector<bool>& folded,
                     std::vector<bool>& done, SingleFn internal_single, std::map<TensorId, std::size_t>& first_consumer,
@@ -530,16 +549,9 @@ private:
         hip_check(mlvc_hip_conv_plan(&d), "conv planning");
         L.kind_name = std::string(mlvc_hip_conv_variant_name(d.variant)) + tags;
         // Pack weights into the variant's fragment order, widen the bias.
-        const auto w = weight_fp16(n.inputs[1]);
-        std::vector<std::uint8_t> packed(mlvc_hip_conv_packed_bytes(&d));
-        hip_check(mlvc_hip_conv_pack(&d, w.data(), packed.data()), "weight packing");
-        L.packed = DeviceMem(packed.size());
-        pending_uploads_.push_back({L.packed.ptr, std::move(packed)});
-        const auto b = bias_f32(n, d.oc, mlvc_hip_conv_bias_len(&d));
-        L.bias = DeviceMem(b.size() * 4);
-        std::vector<std::uint8_t> braw(b.size() * 4);
-        std::memcpy(braw.data(), b.data(), braw.size());
-        pending_uploads_.push_back({L.bias.ptr, std::move(braw)});
+        L.w_oihw = weight_fp16(n.inputs[1]);
+        L.bias_oc = bias_f32(n, d.oc, static_cast<std::size_t>(d.oc));
+        pack_conv(L, L.packed, L.bias, d);
         // Algorithmic work: 2*N*OC*OH*OW*IC*KH*KW FLOPs; bytes = each tensor once.
         L.flops = 2.0 * d.n * d.oc * d.oh * d.ow * static_cast<double>(d.ic) * d.kh * d.kw;
         L.bytes = 2.0 * (static_cast<double>(d.n) * d.ic * d.ih * d.iw + static_cast<double>(d.oc) * d.ic * d.kh * d.kw + d.oc +
@@ -813,6 +825,69 @@ private:
                       "concat launch");
             break;
         }
+    }
+
+    // Measures every eligible tile variant of each conv launch on the real
+    // buffers (zeroed first) and keeps the fastest. All variants of one kernel
+    // size share the K order, so the choice changes timing, never results.
+    void tune()
+    {
+        select();
+        hip_check(mlvc_hip_zero(arena_.ptr, arena_bytes_, stream_), "arena clear");
+        for (auto& [id, buf] : input_buf_) hip_check(mlvc_hip_zero(buf.ptr, aot::tensor_bytes(desc(id)), stream_), "input clear");
+        for (auto& b : bindings_)
+            for (auto& buf : b.buf) hip_check(mlvc_hip_zero(buf.ptr, b.bytes, stream_), "state clear");
+        constexpr int kWarm = 2, kReps = 5;
+        for (auto& lp : launches_) {
+            Launch& L = *lp;
+            if (L.kind != Launch::kConv) continue;
+            int count = 0;
+            hip_check(mlvc_hip_conv_candidates(&L.conv, nullptr, 0, &count), "conv candidates");
+            if (count < 2) continue;
+            std::vector<int> cand(static_cast<std::size_t>(count));
+            hip_check(mlvc_hip_conv_candidates(&L.conv, cand.data(), count, &count), "conv candidates");
+            const mlvc_hip_conv_desc planned = L.conv;
+            int best = planned.variant;
+            float best_ms = -1.0F;
+            for (int v : cand) {
+                mlvc_hip_conv_desc d = planned;
+                d.variant = v;
+                DeviceMem w, b;
+                pack_conv(L, w, b, d);
+                upload_parameters();
+                std::swap(L.packed, w);
+                std::swap(L.bias, b);
+                L.conv = d;
+                for (int r = 0; r < kWarm; ++r) enqueue_one(L, 0);
+                hip_check(mlvc_hip_event_record(ev0_, stream_), "event record");
+                for (int r = 0; r < kReps; ++r) enqueue_one(L, 0);
+                hip_check(mlvc_hip_event_record(ev1_, stream_), "event record");
+                hip_check(mlvc_hip_event_synchronize(ev1_), "event sync");
+                float ms = 0.0F;
+                hip_check(mlvc_hip_event_elapsed_ms(ev0_, ev1_, &ms), "event timing");
+                std::swap(L.packed, w);
+                std::swap(L.bias, b);
+                if (best_ms < 0.0F || ms < best_ms) {
+                    best_ms = ms;
+                    best = v;
+                }
+            }
+            L.conv = planned;
+            if (best != planned.variant) {
+                L.conv.variant = best;
+                pack_conv(L, L.packed, L.bias, L.conv);
+                upload_parameters();
+                const std::string old_name = mlvc_hip_conv_variant_name(planned.variant);
+                L.kind_name = mlvc_hip_conv_variant_name(best) + L.kind_name.substr(old_name.size());
+            }
+        }
+        hip_check(mlvc_hip_stream_synchronize(stream_), "stream sync");
+    }
+
+    static bool tuning_enabled()
+    {
+        const char* e = std::getenv("MLVC_HIP_TUNE");
+        return !(e && std::string(e) == "0");
     }
 
     void capture()

@@ -35,6 +35,20 @@ int guard(F&& fn)
     }
 }
 
+// gfx950 deals the workgroups of a dispatch round-robin over its 8 XCDs
+// (workgroup i runs on XCD i % 8), and each XCD has its own L2. xcd_order
+// renumbers a 1-D grid of n workgroups so that XCD k runs the contiguous
+// range of logical work items [k*(n/8) + min(k, n%8), ...) in order: work
+// items that share input (neighbouring tiles, the output-channel blocks of
+// one tile) then share an L2 instead of being fetched once per XCD. It is a
+// bijection on [0, n) whatever n is.
+constexpr int kXcds = 8;
+__device__ __forceinline__ int xcd_order(int id, int n)
+{
+    const int per = n / kXcds, rem = n % kXcds, xcd = id % kXcds;
+    return xcd * per + min(xcd, rem) + id / kXcds;
+}
+
 inline hipStream_t to_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 __device__ __forceinline__ float h2f(std::uint16_t h)
@@ -46,6 +60,19 @@ __device__ __forceinline__ float h2f(std::uint16_t h)
 __device__ __forceinline__ std::uint16_t f2h(float f)
 {
     return __builtin_bit_cast(std::uint16_t, static_cast<_Float16>(f));
+}
+
+// LeakyReLU of an FP16 value f: fp16(f * alpha) with the product rounded to
+// FP32 first, as the reference computes it. The multiply is issued as a plain
+// v_mul_f32 so it stays a separate rounding step: left alone the compiler
+// folds multiply and narrowing into v_fma_mixlo_f16, which rounds once and
+// gives a different FP16 result when the FP32 product is an FP16 tie
+// (e.g. 0x815E * 0.01f: -3.5 ulp after the FP32 rounding -> -4, not -3).
+__device__ __forceinline__ std::uint16_t leaky_f16(float f, float alpha)
+{
+    float p;
+    asm("v_mul_f32 %0, %1, %2" : "=v"(p) : "v"(f), "v"(alpha));
+    return f2h(p);
 }
 
 }  // namespace mlvc_hip

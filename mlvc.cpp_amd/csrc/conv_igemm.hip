@@ -44,6 +44,7 @@ struct ConvArgs {
     int epi;
     float alpha;
     int tiles_x, nchunks;
+    int tiles, ocbs, nwg;  // pixel tiles per image, output-channel blocks, workgroups (tiles*ocbs*n)
 };
 
 // KC consecutive channels [c0, c0 + KC) of input pixel (iy, ix) of batch b,
@@ -113,7 +114,7 @@ __device__ __forceinline__ std::uint16_t finish(const ConvArgs& a, float acc, in
     std::uint16_t h = f2h(acc);
     if (a.epi == MLVC_EPI_LEAKY_RELU) {
         const float f = h2f(h);
-        if (f < 0.0f) h = f2h(f * a.alpha);
+        if (f < 0.0f) h = leaky_f16(f, a.alpha);
     } else if (a.epi == MLVC_EPI_RESIDUAL_ADD) {
         h = f2h(h2f(h) + h2f(a.res[(static_cast<size_t>(b * a.oc + oc) * a.oh + oy) * a.ow + ox]));
     }
@@ -185,9 +186,11 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a)
     std::uint16_t* const lds_w = lds + C::IN_LDS;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int tile = blockIdx.x;
+    // Logical work item: output-channel block fastest, then pixel tiles in
+    // row-major order, then images; each XCD runs a contiguous range of them.
+    const int item = xcd_order(blockIdx.x, a.nwg);
+    const int ocb = item % a.ocbs, tile = (item / a.ocbs) % a.tiles, b = item / (a.ocbs * a.tiles);
     const int tx0 = (tile % a.tiles_x) * C::TW, ty0 = (tile / a.tiles_x) * C::TH;
-    const int ocb = blockIdx.y, b = blockIdx.z;
     const int iy0 = ty0 * C::S - a.ph, ix0 = tx0 * C::S - a.pw;
     // First staged input column (8-aligned for the vector path).
     const int xa = C::VEC ? ix0 - (((ix0 % 8) + 8) % 8) : ix0;
@@ -357,7 +360,7 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a)
 #pragma unroll
             for (int j = 0; j < 8; ++j) {
                 const float f = h2f(h[j]);
-                if (f < 0.0f) h[j] = f2h(f * a.alpha);
+                if (f < 0.0f) h[j] = leaky_f16(f, a.alpha);
             }
         } else if (a.epi == MLVC_EPI_RESIDUAL_ADD) {
             const u32x4 rv = *reinterpret_cast<const u32x4*>(a.res + (static_cast<size_t>(b * a.oc + oc) * a.oh + oy) * a.ow + ox);
@@ -412,7 +415,7 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a)
                 std::uint16_t h = lds[ocl * C::EPI_ROW + pl];
                 if (a.epi == MLVC_EPI_LEAKY_RELU) {
                     const float f = h2f(h);
-                    if (f < 0.0f) h = f2h(f * a.alpha);
+                    if (f < 0.0f) h = leaky_f16(f, a.alpha);
                 } else if (a.epi == MLVC_EPI_RESIDUAL_ADD) {
                     h = f2h(h2f(h) + h2f(a.res[(static_cast<size_t>(b * a.oc + oc) * a.oh + oy) * a.ow + ox]));
                 }
@@ -467,6 +470,8 @@ void launch_mfma(const ConvArgs& a, dim3 grid, hipStream_t s)
 const Variant kVariants[] = {
     Variant{"direct_fp32", 0, 0, 0, 0, 0, 0, 0, nullptr, nullptr},
     // 3x3 stride 1
+    MLVC_VARIANT(32, 4, 64, 3, 3, 1, 16),
+    MLVC_VARIANT(32, 8, 32, 3, 3, 1, 16),
     MLVC_VARIANT(64, 4, 64, 3, 3, 1, 16),
     MLVC_VARIANT(64, 8, 32, 3, 3, 1, 16),
     MLVC_VARIANT(64, 16, 16, 3, 3, 1, 16),
@@ -477,11 +482,13 @@ const Variant kVariants[] = {
     MLVC_VARIANT(128, 8, 32, 3, 3, 1, 16),
     MLVC_VARIANT(128, 16, 16, 3, 3, 1, 16),
     // 3x3 stride 2
+    MLVC_VARIANT(32, 4, 64, 3, 3, 2, 16),
     MLVC_VARIANT(64, 2, 64, 3, 3, 2, 16),
     MLVC_VARIANT(64, 4, 32, 3, 3, 2, 16),
     MLVC_VARIANT(64, 8, 16, 3, 3, 2, 16),
     MLVC_VARIANT(128, 2, 64, 3, 3, 2, 16),
     // 1x1 (flattened pixels unless an unshuffle is fused)
+    MLVC_VARIANT(32, 1, 256, 1, 1, 1, 32),
     MLVC_VARIANT(64, 1, 256, 1, 1, 1, 32),
     MLVC_VARIANT(64, 1, 128, 1, 1, 1, 32),
     MLVC_VARIANT(128, 1, 128, 1, 1, 1, 32),
@@ -532,6 +539,10 @@ void validate(const mlvc_hip_conv_desc& d, bool pointers)
     if (!d.x || !d.y || !d.packed_w || !d.bias) throw std::runtime_error("conv: null tensor");
 }
 
+// A tile variant can run the geometry: kernel size and stride match, 1x1
+// variants without padding, flattened 1x1 geometry on one-row tiles only.
+bool eligible(const mlvc_hip_conv_desc& d, const Variant& k);
+
 // Geometry as the kernel sees it (1x1 convs run over flattened pixels).
 void kernel_geometry(const mlvc_hip_conv_desc& d, int& ih, int& iw, int& oh, int& ow)
 {
@@ -544,6 +555,16 @@ void kernel_geometry(const mlvc_hip_conv_desc& d, int& ih, int& iw, int& oh, int
         oh = d.oh;
         ow = d.ow;
     }
+}
+
+bool eligible(const mlvc_hip_conv_desc& d, const Variant& k)
+{
+    if (k.bm == 0 || k.kh != d.kh || k.kw != d.kw || k.s != d.stride_h || k.s != d.stride_w) return false;
+    if (d.kh == 1 && (d.pad_h || d.pad_w)) return false;
+    int ih, iw, oh, ow;
+    kernel_geometry(d, ih, iw, oh, ow);
+    const bool flat = ih == 1 && oh == 1 && d.kh == 1 && d.kw == 1;
+    return !(d.kh == 1 && flat != (k.th == 1));
 }
 
 }  // namespace
@@ -560,15 +581,12 @@ int mlvc_hip_conv_plan(mlvc_hip_conv_desc* desc)
         const mlvc_hip_conv_desc& d = *desc;
         int ih, iw, oh, ow;
         kernel_geometry(d, ih, iw, oh, ow);
-        const bool flat = ih == 1 && oh == 1 && d.kh == 1 && d.kw == 1;
         const int slots = 2 * cu_count();
         int best = 0;
         double best_cost = 0.0;
         for (int v = 1; v < kVariantCount; ++v) {
+            if (!eligible(d, kVariants[v])) continue;
             const Variant& k = kVariants[v];
-            if (k.kh != d.kh || k.kw != d.kw || k.s != d.stride_h || k.s != d.stride_w) continue;
-            if (d.kh == 1 && (d.pad_h || d.pad_w)) continue;
-            if (d.kh == 1 && flat != (k.th == 1)) continue;
             const long tiles = static_cast<long>((oh + k.th - 1) / k.th) * ((ow + k.tw - 1) / k.tw) *
                                ((d.oc + k.bm - 1) / k.bm) * d.n;
             const long rounds = (tiles + slots - 1) / slots;
@@ -583,6 +601,21 @@ int mlvc_hip_conv_plan(mlvc_hip_conv_desc* desc)
         // 16-byte row-segment staging: plain or channel-concat input whose
         // split falls on 8 channels, rows of 8-aligned width.
         desc->vector_io = best != 0 && d.in_s2d_block <= 1 && (!d.x2 || d.ic_split % 8 == 0) && iw % 8 == 0;
+    });
+}
+
+int mlvc_hip_conv_candidates(const mlvc_hip_conv_desc* desc, int* variants, int capacity, int* count)
+{
+    return guard([&] {
+        validate(*desc, false);
+        if (!count || (capacity > 0 && !variants)) throw std::runtime_error("conv: null candidate buffer");
+        int n = 0;
+        for (int v = 1; v < kVariantCount; ++v)
+            if (eligible(*desc, kVariants[v])) {
+                if (n < capacity) variants[n] = v;
+                ++n;
+            }
+        *count = n;
     });
 }
 
@@ -680,8 +713,12 @@ int mlvc_hip_conv_launch(const mlvc_hip_conv_desc* desc, mlvc_hip_stream s)
             const bool vec = d.vector_io && aligned && a.s2d <= 1 && (!a.x2 || a.ic_split % 8 == 0) && a.iw % 8 == 0;
             a.tiles_x = (a.ow + k.tw - 1) / k.tw;
             a.nchunks = (d.ic + k.kc - 1) / k.kc;
-            const unsigned tiles = static_cast<unsigned>(a.tiles_x * ((a.oh + k.th - 1) / k.th));
-            const dim3 grid(tiles, static_cast<unsigned>((d.oc + k.bm - 1) / k.bm), static_cast<unsigned>(d.n));
+            a.tiles = a.tiles_x * ((a.oh + k.th - 1) / k.th);
+            a.ocbs = (d.oc + k.bm - 1) / k.bm;
+            const long long nwg = static_cast<long long>(a.tiles) * a.ocbs * d.n;
+            if (nwg > 0x7FFFFFFF) throw std::runtime_error("conv: grid too large");
+            a.nwg = static_cast<int>(nwg);
+            const dim3 grid(static_cast<unsigned>(a.nwg));
             (vec ? k.launch_vec : k.launch_scalar)(a, grid, to_stream(s));
         }
         check(hipGetLastError(), "conv kernel launch");

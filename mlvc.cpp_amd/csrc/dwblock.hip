@@ -48,7 +48,7 @@ struct DwBlockArgs {
     const float* b1;
     const std::uint16_t* w2;
     const float* b2;
-    int h, w, tiles_x;
+    int h, w, tiles_x, tiles, nwg;  // nwg = tiles * n
     float alpha;
 };
 
@@ -86,8 +86,10 @@ __global__ __launch_bounds__(256) void dwblock_kernel(DwBlockArgs a)
     std::uint16_t* ys = reinterpret_cast<std::uint16_t*>(lds_b);
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int x0 = (blockIdx.x % a.tiles_x) * kTW, y0 = (blockIdx.x / a.tiles_x) * kTH;
-    const int b = blockIdx.y;
+    // Each XCD runs a contiguous band of tiles, so the halo rows it stages
+    // and the residual it re-reads stay in its own L2.
+    const int item = xcd_order(blockIdx.x, a.nwg), tile = item % a.tiles, b = item / a.tiles;
+    const int x0 = (tile % a.tiles_x) * kTW, y0 = (tile / a.tiles_x) * kTH;
     const size_t plane = static_cast<size_t>(a.h) * a.w;
     const std::uint16_t* xb = a.x + static_cast<size_t>(b) * C * plane;
     const u32x4* w1 = reinterpret_cast<const u32x4*>(a.w1);
@@ -253,7 +255,7 @@ __global__ __launch_bounds__(256) void dwblock_kernel(DwBlockArgs a)
             for (int i = 0; i < 4; ++i) {
                 hv[i] = f2h(acc1[m][4 * j + i]);
                 const float f = h2f(hv[i]);
-                if (f < 0.0f) hv[i] = f2h(f * a.alpha);
+                if (f < 0.0f) hv[i] = leaky_f16(f, a.alpha);
             }
             const std::uint32_t lo = hv[0] | (static_cast<std::uint32_t>(hv[1]) << 16);
             const std::uint32_t hi = hv[2] | (static_cast<std::uint32_t>(hv[3]) << 16);
@@ -350,8 +352,12 @@ int mlvc_hip_dwblock_launch(const mlvc_hip_dwblock_desc* d, mlvc_hip_stream s)
                       static_cast<const std::uint16_t*>(d->dw_w), d->dw_b,
                       static_cast<const std::uint16_t*>(d->w1), d->b1,
                       static_cast<const std::uint16_t*>(d->w2), d->b2,
-                      d->h, d->w, (d->w + kTW - 1) / kTW, d->alpha};
-        const dim3 grid(static_cast<unsigned>(a.tiles_x * ((d->h + kTH - 1) / kTH)), static_cast<unsigned>(d->n));
+                      d->h, d->w, (d->w + kTW - 1) / kTW, 0, 0, d->alpha};
+        a.tiles = a.tiles_x * ((d->h + kTH - 1) / kTH);
+        const long long nwg = static_cast<long long>(a.tiles) * d->n;
+        if (nwg > 0x7FFFFFFF) throw std::runtime_error("dwblock: grid too large");
+        a.nwg = static_cast<int>(nwg);
+        const dim3 grid(static_cast<unsigned>(a.nwg));
         if (d->c == 256 && d->e == 512) launch<256, 512>(a, grid, to_stream(s));
         else if (d->c == 128 && d->e == 256) launch<128, 256>(a, grid, to_stream(s));
         else launch<128, 512>(a, grid, to_stream(s));

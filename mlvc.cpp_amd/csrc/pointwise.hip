@@ -116,14 +116,14 @@ __global__ __launch_bounds__(kBlock) void eltwise_kernel(const std::uint16_t* __
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
             const float f = h2f(pa[j]);
-            po[j] = OP == 0 ? (f < 0.0f ? f2h(f * alpha) : pa[j]) : f2h(f + h2f(pb[j]));
+            po[j] = OP == 0 ? (f < 0.0f ? leaky_f16(f, alpha) : pa[j]) : f2h(f + h2f(pb[j]));
         }
         reinterpret_cast<uint4*>(y)[i] = out;
     }
     for (size_t i = vecs * 8 + blockIdx.x * static_cast<size_t>(kBlock) + threadIdx.x; i < count;
          i += static_cast<size_t>(gridDim.x) * kBlock) {
         const float f = h2f(a[i]);
-        y[i] = OP == 0 ? (f < 0.0f ? f2h(f * alpha) : a[i]) : f2h(f + h2f(b[i]));
+        y[i] = OP == 0 ? (f < 0.0f ? leaky_f16(f, alpha) : a[i]) : f2h(f + h2f(b[i]));
     }
 }
 
