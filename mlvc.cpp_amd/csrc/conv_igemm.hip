@@ -32,6 +32,12 @@
 namespace mlvc_hip {
 namespace {
 
+// Raw buffer resource word 3 for gfx950 (32-bit data format, no swizzle).
+constexpr int kRawBufferFlags = 0x00020000;
+// Byte offset that is past the end of every staged tensor (each < 2 GiB)
+// even after adding the largest per-load SGPR offset (7 channel planes).
+constexpr std::uint32_t kOutOfRange = 0x80000000u;
+
 struct ConvArgs {
     const std::uint16_t* x;
     const std::uint16_t* x2;
@@ -211,29 +217,45 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a)
     u32x4 vin[C::VEC ? C::UNITS_PER_T : 1][8];
     std::uint32_t in_reg[C::VEC ? 1 : C::PIX_PER_T][C::KC / 2];
     u32x4 w_reg[C::W_PER_T];
+    // Vector staging reads through raw buffer resources sized to this
+    // image's part of x (channels [0, c1)) and of x2 (the concat rest): a
+    // load past the end returns zeros, so padding rows/columns (offset set
+    // past the end) and channels past IC need no branch. The concat split
+    // falls on a chunk boundary, so each chunk reads one resource.
+    const std::uint32_t hw2 = static_cast<std::uint32_t>(hw) * 2u;
+    const std::uint16_t* x_img = a.x + static_cast<size_t>(b) * c1 * hw;
+    const std::uint16_t* x2_img = a.x2 ? a.x2 + static_cast<size_t>(b) * (a.ic - c1) * hw : x_img;
+    const __amdgpu_buffer_rsrc_t rx =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<std::uint16_t*>(x_img), 0, static_cast<int>(c1 * hw2), kRawBufferFlags);
+    const __amdgpu_buffer_rsrc_t rx2 = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<std::uint16_t*>(x2_img), 0, static_cast<int>(a.x2 ? (a.ic - c1) * hw2 : 0u), kRawBufferFlags);
+    std::uint32_t pix_off[C::VEC ? C::UNITS_PER_T : 1];
+    int unit_c8[C::VEC ? C::UNITS_PER_T : 1];
+    if constexpr (C::VEC) {
+#pragma unroll
+        for (int i = 0; i < C::UNITS_PER_T; ++i) {
+            const int u = tid + i * C::kThreads;
+            const int sg = u % C::NSEG, yi = (u / C::NSEG) % C::IH_T;
+            const int iy = iy0 + yi, ix = xa + sg * 8;
+            const bool ok = u < C::UNITS && iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw;
+            pix_off[i] = ok ? static_cast<std::uint32_t>(iy * a.iw + ix) * 2u : kOutOfRange;
+            unit_c8[i] = u / (C::NSEG * C::IH_T);
+        }
+    }
     auto fetch = [&](int chunk) {
         const int c0 = chunk * C::KC;
         if constexpr (C::VEC) {
+            const bool second = a.x2 && c0 >= c1;
+            const __amdgpu_buffer_rsrc_t r = second ? rx2 : rx;
+            const std::uint32_t cbase = static_cast<std::uint32_t>(second ? c0 - c1 : c0);
 #pragma unroll
             for (int i = 0; i < C::UNITS_PER_T; ++i) {
-                const int u = tid + i * C::kThreads;
-                if (u < C::UNITS) {
-                    const int sg = u % C::NSEG, yi = (u / C::NSEG) % C::IH_T, c8 = u / (C::NSEG * C::IH_T);
-                    const int iy = iy0 + yi, ix = xa + sg * 8;
-                    const bool ok = iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw;
-                    const size_t po = static_cast<size_t>(iy) * a.iw + ix;
+                const std::uint32_t off = pix_off[i] == kOutOfRange
+                                              ? kOutOfRange
+                                              : pix_off[i] + (cbase + static_cast<std::uint32_t>(unit_c8[i]) * 8u) * hw2;
 #pragma unroll
-                    for (int k = 0; k < 8; ++k) {
-                        const int c = c0 + c8 * 8 + k;
-                        u32x4 v = {0u, 0u, 0u, 0u};
-                        if (ok && c < a.ic) {
-                            const std::uint16_t* src = c < c1 ? a.x + (static_cast<size_t>(b) * c1 + c) * hw
-                                                              : a.x2 + (static_cast<size_t>(b) * (a.ic - c1) + c - c1) * hw;
-                            v = *reinterpret_cast<const u32x4*>(src + po);
-                        }
-                        vin[i][k] = v;
-                    }
-                }
+                for (int k = 0; k < 8; ++k)
+                    vin[i][k] = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), static_cast<int>(k * hw2), 0);
             }
         } else {
 #pragma unroll
@@ -710,7 +732,11 @@ int mlvc_hip_conv_launch(const mlvc_hip_conv_desc* desc, mlvc_hip_stream s)
             if (a.s2d > 1 && a.ih == 1 && d.ih != 1) throw std::runtime_error("conv: flattened geometry with fusion");
             const bool aligned = (reinterpret_cast<std::uintptr_t>(d.x) & 15u) == 0 &&
                                  (!d.x2 || (reinterpret_cast<std::uintptr_t>(d.x2) & 15u) == 0);
-            const bool vec = d.vector_io && aligned && a.s2d <= 1 && (!a.x2 || a.ic_split % 8 == 0) && a.iw % 8 == 0;
+            // Buffer offsets of the vector path stay below 2^31 (range check
+            // and the out-of-range marker); the concat split falls on a chunk.
+            const std::uint64_t plane_bytes = static_cast<std::uint64_t>(a.ih) * a.iw * 2;
+            const bool vec = d.vector_io && aligned && a.s2d <= 1 && (!a.x2 || a.ic_split % k.kc == 0) &&
+                             a.iw % 8 == 0 && (static_cast<std::uint64_t>(d.ic) + k.kc) * plane_bytes < (1ull << 31);
             a.tiles_x = (a.ow + k.tw - 1) / k.tw;
             a.nchunks = (d.ic + k.kc - 1) / k.kc;
             a.tiles = a.tiles_x * ((a.oh + k.th - 1) / k.th);
