@@ -50,6 +50,14 @@ bool fusion_enabled()
     return !(env && env[0] == '1' && env[1] == '\0');
 }
 
+// MLVC_HIP_CONV_VARIANT=<variant name> runs every conv that variant can
+// run with it, untuned (tests sweep the variants this way).
+std::string forced_conv_variant()
+{
+    const char* env = std::getenv("MLVC_HIP_CONV_VARIANT");
+    return env ? std::string(env) : std::string();
+}
+
 void hip_check(int rc, const char* what)
 {
     if (rc != 0) fail(std::string(what) + ": " + mlvc_hip_last_error());
@@ -107,6 +115,7 @@ struct Launch {
     DeviceMem packed, bias, packed2, bias2, packed3, bias3;
     std::vector<std::uint16_t> w_oihw;  // conv weights kept for re-packing after tuning
     std::vector<float> bias_oc;         // conv bias, unpadded
+    bool forced = false;                // variant set by MLVC_HIP_CONV_VARIANT, not tuned
     int n = 0, c = 0, ih = 0, iw = 0, oh = 0, ow = 0, kh = 0, kw = 0, sh = 1, sw = 1, ph = 0, pw = 0;
     int block = 0, ca = 0, cb = 0;
     std::size_t count = 0, hw = 0;
@@ -547,6 +556,17 @@ private:
         }
         L.y = out;
         hip_check(mlvc_hip_conv_plan(&d), "conv planning");
+        if (const std::string want = forced_conv_variant(); !want.empty()) {
+            int count = 0;
+            hip_check(mlvc_hip_conv_candidates(&d, nullptr, 0, &count), "conv candidates");
+            std::vector<int> cand(static_cast<std::size_t>(count));
+            hip_check(mlvc_hip_conv_candidates(&d, cand.data(), count, &count), "conv candidates");
+            for (int v : cand)
+                if (want == mlvc_hip_conv_variant_name(v)) {
+                    d.variant = v;
+                    L.forced = true;
+                }
+        }
         L.kind_name = std::string(mlvc_hip_conv_variant_name(d.variant)) + tags;
         // Pack weights into the variant's fragment order, widen the bias.
         L.w_oihw = weight_fp16(n.inputs[1]);
@@ -840,7 +860,7 @@ private:
         constexpr int kWarm = 2, kReps = 5;
         for (auto& lp : launches_) {
             Launch& L = *lp;
-            if (L.kind != Launch::kConv) continue;
+            if (L.kind != Launch::kConv || L.forced) continue;
             int count = 0;
             hip_check(mlvc_hip_conv_candidates(&L.conv, nullptr, 0, &count), "conv candidates");
             if (count < 2) continue;

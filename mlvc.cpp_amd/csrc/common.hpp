@@ -68,11 +68,13 @@ __device__ __forceinline__ std::uint16_t f2h(float f)
 // folds multiply and narrowing into v_fma_mixlo_f16, which rounds once and
 // gives a different FP16 result when the FP32 product is an FP16 tie
 // (e.g. 0x815E * 0.01f: -3.5 ulp after the FP32 rounding -> -4, not -3).
-__device__ __forceinline__ std::uint16_t leaky_f16(float f, float alpha)
+__device__ __forceinline__ float mul_f32(float a, float b)
 {
     float p;
-    asm("v_mul_f32 %0, %1, %2" : "=v"(p) : "v"(f), "v"(alpha));
-    return f2h(p);
+    asm("v_mul_f32 %0, %1, %2" : "=v"(p) : "v"(a), "v"(b));
+    return p;
 }
+
+__device__ __forceinline__ std::uint16_t leaky_f16(float f, float alpha) { return f2h(mul_f32(f, alpha)); }
 
 }  // namespace mlvc_hip

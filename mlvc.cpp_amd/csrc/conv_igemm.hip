@@ -34,8 +34,8 @@ namespace {
 
 // Raw buffer resource word 3 for gfx950 (32-bit data format, no swizzle).
 constexpr int kRawBufferFlags = 0x00020000;
-// Byte offset that is past the end of every staged tensor (each < 2 GiB)
-// even after adding the largest per-load SGPR offset (7 channel planes).
+// Byte offset past the end of every staged tensor (each < 2 GiB), also after
+// adding up to 7 channel planes; raw buffer loads there return zeros.
 constexpr std::uint32_t kOutOfRange = 0x80000000u;
 
 struct ConvArgs {
@@ -139,10 +139,14 @@ __device__ __forceinline__ void store_output(const ConvArgs& a, std::uint16_t h,
     }
 }
 
-template <int BM_, int TH_, int TW_, int KH_, int KW_, int S_, int KC_, bool VEC_>
+template <int BM_, int TH_, int TW_, int KH_, int KW_, int S_, int KC_, bool VEC_, bool DB_>
 struct Cfg {
     static constexpr int BM = BM_, TH = TH_, TW = TW_, KH = KH_, KW = KW_, S = S_, KC = KC_;
     static constexpr bool VEC = VEC_;  // 16-byte row-segment staging (needs W % 8 == 0)
+    // Two LDS stages: chunk k+1 is staged (weights by LDS DMA) while chunk k
+    // is multiplied, one barrier per chunk. Otherwise one stage, weights
+    // staged through registers, two barriers per chunk, half the LDS.
+    static constexpr bool DB = DB_;
     static constexpr int kThreads = 256;
     static constexpr int BN = TH * TW;
     static constexpr int TAPS = KH * KW;
@@ -170,8 +174,11 @@ struct Cfg {
     static constexpr int W_PER_T = (W_VEC + kThreads - 1) / kThreads;
     static constexpr int EPI_ROW = BN + 8;  // output staging row (one channel), halves
     static constexpr int EPI_LDS = BM * EPI_ROW;
-    static constexpr int LDS = (IN_LDS + W_LDS) > EPI_LDS ? (IN_LDS + W_LDS) : EPI_LDS;
-    static_assert(BM % 32 == 0 && WN % 32 == 0 && KC % 16 == 0 && TW % 8 == 0, "tile shape");
+    static constexpr int STAGE = IN_LDS + W_LDS;
+    static constexpr int W_INST = W_VEC / 64;  // 1 KB LDS DMA instructions per chunk
+    static constexpr int LDS = (DB ? 2 * STAGE : STAGE) > EPI_LDS ? (DB ? 2 * STAGE : STAGE) : EPI_LDS;
+    static_assert(BM % 32 == 0 && WN % 32 == 0 && KC % 16 == 0 && TW % 8 == 0 && W_VEC % 64 == 0, "tile shape");
+    static_assert(STAGE % 8 == 0, "stage alignment");
     static_assert(LDS * 2 <= 160 * 1024, "LDS budget");
 
     __device__ static constexpr int col(int x) { return S == 2 ? ((x & 1) ? IW_E + (x >> 1) : (x >> 1)) : x; }
@@ -188,8 +195,8 @@ template <class C>
 __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a)
 {
     __shared__ __attribute__((aligned(16))) std::uint16_t lds[C::LDS];
-    std::uint16_t* const lds_in = lds;
-    std::uint16_t* const lds_w = lds + C::IN_LDS;
+    auto lds_in = [&](int stage) { return lds + stage * C::STAGE; };
+    auto lds_w = [&](int stage) { return lds + stage * C::STAGE + C::IN_LDS; };
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     // Logical work item: output-channel block fastest, then pixel tiles in
@@ -216,7 +223,7 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a)
     const int c1 = a.x2 ? a.ic_split : a.ic;
     u32x4 vin[C::VEC ? C::UNITS_PER_T : 1][8];
     std::uint32_t in_reg[C::VEC ? 1 : C::PIX_PER_T][C::KC / 2];
-    u32x4 w_reg[C::W_PER_T];
+    u32x4 w_reg[C::DB ? 1 : C::W_PER_T];
     // Vector staging reads through raw buffer resources sized to this
     // image's part of x (channels [0, c1)) and of x2 (the concat rest): a
     // load past the end returns zeros, so padding rows/columns (offset set
@@ -242,7 +249,7 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a)
             unit_c8[i] = u / (C::NSEG * C::IH_T);
         }
     }
-    auto fetch = [&](int chunk) {
+    auto fetch = [&](int chunk, int stage) {
         const int c0 = chunk * C::KC;
         if constexpr (C::VEC) {
             const bool second = a.x2 && c0 >= c1;
@@ -253,9 +260,11 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a)
                 const std::uint32_t off = pix_off[i] == kOutOfRange
                                               ? kOutOfRange
                                               : pix_off[i] + (cbase + static_cast<std::uint32_t>(unit_c8[i]) * 8u) * hw2;
+                // The channel offset goes in the VGPR operand: the range check
+                // covers that operand only, so channels past the end read zeros.
 #pragma unroll
                 for (int k = 0; k < 8; ++k)
-                    vin[i][k] = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off), static_cast<int>(k * hw2), 0);
+                    vin[i][k] = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off + k * hw2), 0, 0);
             }
         } else {
 #pragma unroll
@@ -268,13 +277,27 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a)
             }
         }
         const u32x4* ws = reinterpret_cast<const u32x4*>(a.w + (static_cast<size_t>(ocb) * a.nchunks + chunk) * C::W_LDS);
+        if constexpr (C::DB) {
+            // The packed chunk is copied verbatim: LDS DMA, 1 KB per wave
+            // instruction, lane l of instruction j moving vector 64*j + l.
+            u32x4* dst = reinterpret_cast<u32x4*>(lds_w(stage));
 #pragma unroll
-        for (int i = 0; i < C::W_PER_T; ++i) {
-            const int e = tid + i * C::kThreads;
-            if (e < C::W_VEC) w_reg[i] = ws[e];
+            for (int i = 0; i < (C::W_INST + 3) / 4; ++i) {
+                const int j = wave + 4 * i;
+                if (j < C::W_INST)
+                    __builtin_amdgcn_global_load_lds(ws + j * 64 + lane,
+                                                     (__attribute__((address_space(3))) void*)(dst + j * 64), 16, 0, 0);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < C::W_PER_T; ++i) {
+                const int e = tid + i * C::kThreads;
+                if (e < C::W_VEC) w_reg[i] = ws[e];
+            }
         }
     };
-    auto commit = [&]() {
+    auto commit = [&](int stage) {
+        std::uint16_t* const in_s = lds_in(stage);
         if constexpr (C::VEC) {
             // 8x8 transpose in registers: staged pixel j of the segment gets
             // the 8 channels of the unit as one 16-byte LDS write.
@@ -289,7 +312,7 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a)
                         const int wd = j >> 1;
                         const u32x4 t = {pack_half(vin[i][0][wd], vin[i][1][wd], up), pack_half(vin[i][2][wd], vin[i][3][wd], up),
                                          pack_half(vin[i][4][wd], vin[i][5][wd], up), pack_half(vin[i][6][wd], vin[i][7][wd], up)};
-                        *reinterpret_cast<u32x4*>(&lds_in[C::at(yi, sg * 8 + j) + c8 * 8]) = t;
+                        *reinterpret_cast<u32x4*>(&in_s[C::at(yi, sg * 8 + j) + c8 * 8]) = t;
                     }
                 }
             }
@@ -299,17 +322,19 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a)
                 const int pix = tid + i * C::kThreads;
                 if (pix < C::IN_PIX) {
                     const int yi = pix / C::IW_T, xi = pix - yi * C::IW_T;
-                    u32x4* dst = reinterpret_cast<u32x4*>(&lds_in[C::at(yi, xi)]);
+                    u32x4* dst = reinterpret_cast<u32x4*>(&in_s[C::at(yi, xi)]);
 #pragma unroll
                     for (int q = 0; q < C::KC / 8; ++q)
                         dst[q] = u32x4{in_reg[i][4 * q], in_reg[i][4 * q + 1], in_reg[i][4 * q + 2], in_reg[i][4 * q + 3]};
                 }
             }
         }
+        if constexpr (!C::DB) {
 #pragma unroll
-        for (int i = 0; i < C::W_PER_T; ++i) {
-            const int e = tid + i * C::kThreads;
-            if (e < C::W_VEC) reinterpret_cast<u32x4*>(lds_w)[e] = w_reg[i];
+            for (int i = 0; i < C::W_PER_T; ++i) {
+                const int e = tid + i * C::kThreads;
+                if (e < C::W_VEC) reinterpret_cast<u32x4*>(lds_w(0))[e] = w_reg[i];
+            }
         }
     };
 
@@ -323,12 +348,9 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a)
     }
     const int koff = (lane >> 5) * 8;
 
-    fetch(0);
-    commit();
-    __syncthreads();
-    for (int chunk = 0; chunk < a.nchunks; ++chunk) {
-        const bool more = chunk + 1 < a.nchunks;
-        if (more) fetch(chunk + 1);
+    auto compute = [&](int stage) {
+        const std::uint16_t* const in_s = lds_in(stage);
+        const std::uint16_t* const w_s = lds_w(stage);
 #pragma unroll
         for (int tap = 0; tap < C::TAPS; ++tap) {
             const int ky = tap / C::KW, kx = tap % C::KW;
@@ -340,9 +362,9 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a)
                 half8 av[C::MT], bv[C::NT];
 #pragma unroll
                 for (int mt = 0; mt < C::MT; ++mt)
-                    av[mt] = *reinterpret_cast<const half8*>(&lds_w[(((tap * C::KS + ks) * C::MT + mt) * 64 + lane) * 8]);
+                    av[mt] = *reinterpret_cast<const half8*>(&w_s[(((tap * C::KS + ks) * C::MT + mt) * 64 + lane) * 8]);
 #pragma unroll
-                for (int nt = 0; nt < C::NT; ++nt) bv[nt] = *reinterpret_cast<const half8*>(&lds_in[boff[nt] + ks * 16]);
+                for (int nt = 0; nt < C::NT; ++nt) bv[nt] = *reinterpret_cast<const half8*>(&in_s[boff[nt] + ks * 16]);
 #pragma unroll
                 for (int mt = 0; mt < C::MT; ++mt)
 #pragma unroll
@@ -350,10 +372,38 @@ __global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a)
                         acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[mt], bv[nt], acc[mt][nt], 0, 0, 0);
             }
         }
+    };
+
+    if constexpr (C::DB) {
+        fetch(0, 0);
+        commit(0);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's LDS DMA has landed
         __syncthreads();
-        if (more) {
-            commit();
+        for (int chunk = 0; chunk < a.nchunks; ++chunk) {
+            const int cur = chunk & 1;
+            const bool more = chunk + 1 < a.nchunks;
+            // Stage cur^1 was last read before the previous barrier.
+            if (more) fetch(chunk + 1, cur ^ 1);
+            compute(cur);
+            if (more) {
+                commit(cur ^ 1);
+                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            }
             __syncthreads();
+        }
+    } else {
+        fetch(0, 0);
+        commit(0);
+        __syncthreads();
+        for (int chunk = 0; chunk < a.nchunks; ++chunk) {
+            const bool more = chunk + 1 < a.nchunks;
+            if (more) fetch(chunk + 1, 0);
+            compute(0);
+            __syncthreads();
+            if (more) {
+                commit(0);
+                __syncthreads();
+            }
         }
     }
 
@@ -485,9 +535,13 @@ void launch_mfma(const ConvArgs& a, dim3 grid, hipStream_t s)
     hipLaunchKernelGGL(conv_mfma_kernel<C>, grid, dim3(C::kThreads), 0, s, a);
 }
 
-#define MLVC_VARIANT(BM, TH, TW, KH, KW, S, KC)                                                       \
-    Variant{"mfma_bm" #BM "_" #TH "x" #TW "_k" #KH "x" #KW "_s" #S "_kc" #KC, BM, TH, TW, KH, KW, S, KC, \
-            &launch_mfma<Cfg<BM, TH, TW, KH, KW, S, KC, false>>, &launch_mfma<Cfg<BM, TH, TW, KH, KW, S, KC, true>>}
+#define MLVC_VARIANT(BM, TH, TW, KH, KW, S, KC)                                                              \
+    Variant{"mfma_bm" #BM "_" #TH "x" #TW "_k" #KH "x" #KW "_s" #S "_kc" #KC, BM, TH, TW, KH, KW, S, KC,        \
+            &launch_mfma<Cfg<BM, TH, TW, KH, KW, S, KC, false, false>>, &launch_mfma<Cfg<BM, TH, TW, KH, KW, S, KC, true, false>>}
+// Two-stage pipeline (vector staging only; the scalar staging path keeps the one-stage kernel).
+#define MLVC_VARIANT_DB(BM, TH, TW, KH, KW, S, KC)                                                           \
+    Variant{"mfma_bm" #BM "_" #TH "x" #TW "_k" #KH "x" #KW "_s" #S "_kc" #KC "_db", BM, TH, TW, KH, KW, S, KC,  \
+            &launch_mfma<Cfg<BM, TH, TW, KH, KW, S, KC, false, false>>, &launch_mfma<Cfg<BM, TH, TW, KH, KW, S, KC, true, true>>}
 
 const Variant kVariants[] = {
     Variant{"direct_fp32", 0, 0, 0, 0, 0, 0, 0, nullptr, nullptr},
@@ -503,6 +557,11 @@ const Variant kVariants[] = {
     MLVC_VARIANT(128, 4, 64, 3, 3, 1, 16),
     MLVC_VARIANT(128, 8, 32, 3, 3, 1, 16),
     MLVC_VARIANT(128, 16, 16, 3, 3, 1, 16),
+    MLVC_VARIANT_DB(64, 8, 32, 3, 3, 1, 16),
+    MLVC_VARIANT_DB(32, 8, 32, 3, 3, 1, 16),
+    MLVC_VARIANT_DB(128, 8, 32, 3, 3, 1, 16),
+    MLVC_VARIANT_DB(128, 4, 64, 3, 3, 1, 16),
+    MLVC_VARIANT_DB(64, 4, 64, 3, 3, 1, 16),
     // 3x3 stride 2
     MLVC_VARIANT(32, 4, 64, 3, 3, 2, 16),
     MLVC_VARIANT(64, 2, 64, 3, 3, 2, 16),

@@ -7,23 +7,28 @@
 // Same rounding points as the unfused schedule (the reference runs DW, a
 // conv with a LeakyReLU epilogue and a conv with a residual epilogue:
 // backends/cpu/src/kernels_x86_avx2.cpp:237-302, kernels_scalar.cpp:178-192),
-// but d and e never leave the chip. One workgroup (4 waves) owns a 4x8 pixel
-// tile and all channels. At 1920x1088 / 16 the grid is one workgroup per CU,
-// so the kernel is bound by how fast each CU streams the 2*C*E weight halves
-// it needs, not by MFMA issue. It is organised around that stream:
-//   * every wave runs ONE register ring of RING weight fragments (16 bytes per
-//     lane, pre-packed in A-fragment order) through both GEMMs, so W1 and then
-//     W2 are in flight from the first instruction to the last MFMA, across
-//     the depthwise stage and the barriers between stages;
-//   * the 6x24 halo tile of all C channels is staged with one batch of
-//     16-byte loads; each thread then runs the depthwise taps for two
-//     adjacent channels from registers and writes d[pixel][C + 8] as packed
-//     pairs;
+// but d and e never leave the chip. One workgroup owns a 4x8 pixel tile and
+// all channels; at 1920x1088 / 16 that is one workgroup per CU, so the
+// kernel is bound by how fast each CU streams the 2*C*E weight halves and by
+// the per-pixel VALU work, not by MFMA issue. It is organised around that:
+//   * 8 waves (2 per SIMD) for C = 256, so one wave's VALU work and waits
+//     overlap the other's MFMAs;
+//   * every wave runs ONE register ring of kRing weight fragments (16 bytes
+//     per lane, pre-packed in A-fragment order) through both GEMMs, so W1 and
+//     then W2 are in flight from the first instruction to the last MFMA,
+//     across the depthwise stage and the barriers (LDS-only fences);
+//   * the depthwise input never touches LDS: two threads per channel load
+//     their 4 halo rows with range-checked buffer loads (one dword left, 16
+//     bytes, one dword right per row) and run the taps from registers; taps
+//     outside the image are skipped, so what those loads return is unused;
 //   * accumulators are seeded with the bias (float4 loads issued at start);
+//   * LeakyReLU for 0 <= alpha <= 1 is max(fp16(v), fp16(v * alpha)) on
+//     packed halves (rounding is monotonic, so this equals the reference's
+//     select), with the product rounded to FP32 first;
 //   * the project result is rounded into LDS as [channel][pixel] and leaves
 //     as 16-byte rows with the residual added from 16-byte loads of x.
-// LDS: xs (halo tile) aliases es (expand result); ds (depthwise result)
-// aliases ys (project result). Requires W % 8 == 0 (16-byte rows).
+// LDS: d[pixel][C + 8] (later reused as y[channel][pixel]) and
+// e[pixel][E + 8]. Requires W % 8 == 0 (16-byte rows).
 
 #include "common.hpp"
 #include "mlvc_hip_device.h"
@@ -34,10 +39,26 @@ namespace mlvc_hip {
 namespace {
 
 constexpr int kTH = 4, kTW = 8, kP = kTH * kTW;  // 32 pixels per workgroup
-constexpr int kRow = 24;                          // staged halves per input row
-constexpr int kXC = (kTH + 2) * kRow + 8;         // staged halves per channel (+8: bank spread)
-constexpr int kYS = kP + 8;                       // ys row stride (halves)
+constexpr int kYS = kP + 8;                       // y staging row stride (halves)
 constexpr int kRing = 16;                         // weight fragments in flight per wave
+constexpr int kRawBufferFlags = 0x00020000;       // raw buffer resource word 3 (gfx950)
+constexpr int kOutOfRange = 0x40000000;           // byte offset past every staged tensor (< 2^30 bytes)
+
+template <int C, int E>
+struct BlockCfg {
+    static constexpr int WAVES = C >= 256 ? 8 : 4;
+    static constexpr int T = 64 * WAVES;
+    static constexpr int MT1 = E / 32 / WAVES, MT2 = C / 32 / WAVES;  // m-tiles per wave
+    static constexpr int KS1 = C / 16, KS2 = E / 16;
+    static constexpr int NF1 = MT1 * KS1, NF = NF1 + MT2 * KS2;       // fragments per wave
+    static constexpr int TPC = T / C;                                 // depthwise threads per channel
+    static constexpr int ORT = kTH / TPC;                             // depthwise output rows per thread
+    static constexpr int RV = C * kTH / T;                            // output rows (16 B) per thread
+    static constexpr int DST = C + 8, EST = E + 8;
+    static constexpr int DS_HALVES = kP * DST > C * kYS ? kP * DST : C * kYS;
+    static_assert(C % 128 == 0 && E % 128 == 0 && MT1 >= 1 && MT2 >= 1, "channel counts");
+    static_assert(TPC * ORT == kTH && C * kTH % T == 0, "thread mapping");
+};
 
 struct DwBlockArgs {
     const std::uint16_t* x;
@@ -64,29 +85,37 @@ __device__ __forceinline__ void lds_barrier()
 __device__ __forceinline__ float lo_h(std::uint32_t v) { return h2f(static_cast<std::uint16_t>(v & 0xFFFFu)); }
 __device__ __forceinline__ float hi_h(std::uint32_t v) { return h2f(static_cast<std::uint16_t>(v >> 16)); }
 
-template <int C, int E>
-__global__ __launch_bounds__(256) void dwblock_kernel(DwBlockArgs a)
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+// Two FP32 accumulators -> packed FP16 pair after LeakyReLU on the rounded
+// values (see leaky_f16): max form when 0 <= alpha <= 1, select otherwise.
+__device__ __forceinline__ std::uint32_t leaky_pair(float a0, float a1, float alpha, bool max_form)
 {
-    constexpr int DST = C + 8, EST = E + 8;
-    constexpr int MT1 = E / 32 / 4, MT2 = C / 32 / 4;  // m-tiles per wave
-    constexpr int KS1 = C / 16, KS2 = E / 16;
-    constexpr int NF1 = MT1 * KS1, NF = NF1 + MT2 * KS2;  // fragments per wave
-    constexpr int XV = C * (kTH + 2) * 3 / 256;           // staged 16-byte vectors per thread
-    constexpr int RV = C * kTH / 256;                     // residual rows per thread
-    constexpr int CP = C / 2, RPT = kTH * CP / 256;       // channel pairs, output rows per thread
-    static_assert(C % 128 == 0 && E % 128 == 0, "channel counts");
-    static_assert(C * (kTH + 2) * 3 % 256 == 0 && C * kTH % 256 == 0 && kTH * CP % 256 == 0, "thread mapping");
-    constexpr int XS_BYTES = C * kXC * 2, ES_BYTES = kP * EST * 2;
-    constexpr int DS_BYTES = kP * DST * 2, YS_BYTES = C * kYS * 2;
-    __shared__ __attribute__((aligned(16))) std::uint8_t lds_a[XS_BYTES > ES_BYTES ? XS_BYTES : ES_BYTES];
-    __shared__ __attribute__((aligned(16))) std::uint8_t lds_b[DS_BYTES > YS_BYTES ? DS_BYTES : YS_BYTES];
-    std::uint16_t* xs = reinterpret_cast<std::uint16_t*>(lds_a);
-    std::uint16_t* es = reinterpret_cast<std::uint16_t*>(lds_a);
-    std::uint16_t* ds = reinterpret_cast<std::uint16_t*>(lds_b);
-    std::uint16_t* ys = reinterpret_cast<std::uint16_t*>(lds_b);
+    const half2_t h = {static_cast<_Float16>(a0), static_cast<_Float16>(a1)};
+    if (max_form) {
+        const half2_t p = {static_cast<_Float16>(mul_f32(static_cast<float>(h[0]), alpha)),
+                           static_cast<_Float16>(mul_f32(static_cast<float>(h[1]), alpha))};
+        return __builtin_bit_cast(std::uint32_t, __builtin_elementwise_max(h, p));
+    }
+    const std::uint16_t h0 = __builtin_bit_cast(std::uint16_t, h[0]), h1 = __builtin_bit_cast(std::uint16_t, h[1]);
+    const std::uint16_t r0 = h2f(h0) < 0.0f ? leaky_f16(h2f(h0), alpha) : h0;
+    const std::uint16_t r1 = h2f(h1) < 0.0f ? leaky_f16(h2f(h1), alpha) : h1;
+    return r0 | (static_cast<std::uint32_t>(r1) << 16);
+}
+
+template <int C, int E>
+__global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArgs a)
+{
+    using B = BlockCfg<C, E>;
+    constexpr int DST = B::DST, EST = B::EST, MT1 = B::MT1, MT2 = B::MT2, KS1 = B::KS1, KS2 = B::KS2;
+    constexpr int NF1 = B::NF1, NF = B::NF, ORT = B::ORT, RV = B::RV, T = B::T;
+    __shared__ __attribute__((aligned(16))) std::uint16_t es[kP * EST];
+    __shared__ __attribute__((aligned(16))) std::uint16_t dys[B::DS_HALVES];
+    std::uint16_t* const ds = dys;  // d[pixel][C + 8]
+    std::uint16_t* const ys = dys;  // y[channel][kYS], after the expand stage
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    // Each XCD runs a contiguous band of tiles, so the halo rows it stages
+    // Each XCD runs a contiguous band of tiles, so the halo rows it loads
     // and the residual it re-reads stay in its own L2.
     const int item = xcd_order(blockIdx.x, a.nwg), tile = item % a.tiles, b = item / a.tiles;
     const int x0 = (tile % a.tiles_x) * kTW, y0 = (tile / a.tiles_x) * kTH;
@@ -104,7 +133,7 @@ __global__ __launch_bounds__(256) void dwblock_kernel(DwBlockArgs a)
     };
     u32x4 ring[kRing];
 #pragma unroll
-    for (int f = 0; f < kRing; ++f) ring[f] = frag(f);
+    for (int f = 0; f < kRing; ++f) ring[f] = f < NF ? frag(f) : u32x4{0u, 0u, 0u, 0u};
 
     // Expand accumulators seeded with b1: lane holds rows 8j + hsel + (0..3).
     floatx16 acc1[MT1];
@@ -116,105 +145,85 @@ __global__ __launch_bounds__(256) void dwblock_kernel(DwBlockArgs a)
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc1[m][4 * j + i] = bv[i];
         }
-    // The scheduler would otherwise sink every ring load down to its MFMA
-    // (minimising live registers) and serialise the stream on L2 latency;
-    // scheduling barriers keep each load in the stage that issues it.
+
+    // ---- 1. depthwise halo rows of channel c straight into registers ------
+    // Thread (c, g): output rows g*ORT .. g*ORT + ORT - 1 of the tile, input
+    // rows y0 + g*ORT - 1 .. + ORT. Per row: the dword holding columns
+    // x0-2, x0-1, the 16 bytes x0 .. x0+7 and the dword x0+8, x0+9. The
+    // whole byte offset goes in the VGPR operand: the range check applies to
+    // that operand alone, not to the SGPR offset. Rows outside the image get
+    // an offset past the end (zeros); the left/right dwords at the image edge
+    // read a neighbouring row or zeros. All of those taps are skipped.
+    const int c = tid % C, g = tid / C;
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<std::uint16_t*>(xb), 0, static_cast<int>(C * plane * 2), kRawBufferFlags);
+    const int row0 = y0 + g * ORT - 1;
+    std::uint32_t xl[ORT + 2], xr[ORT + 2];
+    u32x4 xm[ORT + 2];
+#pragma unroll
+    for (int r = 0; r < ORT + 2; ++r) {
+        const int iy = row0 + r;
+        const int off = iy >= 0 && iy < a.h ? ((c * a.h + iy) * a.w + x0) * 2 : kOutOfRange;
+        xl[r] = __builtin_amdgcn_raw_buffer_load_b32(rx, off - 4, 0, 0);
+        xm[r] = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
+        xr[r] = __builtin_amdgcn_raw_buffer_load_b32(rx, off + 16, 0, 0);
+    }
+    std::uint16_t wdw[9];
+#pragma unroll
+    for (int t = 0; t < 9; ++t) wdw[t] = a.dw_w[c * 9 + t];
+    const float bdw = a.dw_b[c];
+    // Residual rows for the output stage, loaded ahead of use.
+    u32x4 res[RV];
+#pragma unroll
+    for (int i = 0; i < RV; ++i) {
+        const int q = tid + T * i, ch = q / kTH, gy = min(y0 + q % kTH, a.h - 1);  // rows past h are not stored
+        res[i] = *reinterpret_cast<const u32x4*>(xb + ch * plane + static_cast<size_t>(gy) * a.w + x0);
+    }
+    // The scheduler would otherwise sink the ring loads down to their MFMAs
+    // (minimising live registers) and serialise the stream on L2 latency.
     __builtin_amdgcn_sched_barrier(0);
 
-    // ---- 1. stage the 6-row halo of all C channels (one batch of loads) ----
-    // Loads are unconditional (addresses clamped into the image, out-of-image
-    // vectors zeroed afterwards): a branch around a load makes the compiler
-    // wait for every load in flight, the weight ring included.
-    {
-        u32x4 v[XV];
-#pragma unroll
-        for (int i = 0; i < XV; ++i) {
-            const int q = tid + 256 * i;
-            const int seg = q % 3, row = (q / 3) % (kTH + 2), c = q / (3 * (kTH + 2));
-            const int iy = min(max(y0 - 1 + row, 0), a.h - 1), ix = min(max(x0 - 8 + seg * 8, 0), a.w - 8);
-            v[i] = *reinterpret_cast<const u32x4*>(xb + c * plane + static_cast<size_t>(iy) * a.w + ix);
-        }
-#pragma unroll
-        for (int i = 0; i < XV; ++i) {
-            const int q = tid + 256 * i;
-            const int seg = q % 3, row = (q / 3) % (kTH + 2), c = q / (3 * (kTH + 2));
-            const int iy = y0 - 1 + row, ix = x0 - 8 + seg * 8;
-            const bool in = iy >= 0 && iy < a.h && ix >= 0 && ix < a.w;
-            *reinterpret_cast<u32x4*>(&xs[c * kXC + row * kRow + seg * 8]) = in ? v[i] : u32x4{0u, 0u, 0u, 0u};
-        }
-    }
-    // Depthwise weights and bias of this thread's channel pair.
-    const int cp = tid % CP, rg = tid / CP;
-    std::uint32_t wdw[9];
-#pragma unroll
-    for (int i = 0; i < 9; ++i) wdw[i] = reinterpret_cast<const std::uint32_t*>(a.dw_w)[cp * 9 + i];
-    const float bd0 = a.dw_b[2 * cp], bd1 = a.dw_b[2 * cp + 1];
-    lds_barrier();
-
-    // ---- 2. depthwise 3x3 for channels 2cp, 2cp+1, output rows rg*RPT.. ----
     {
         const bool left = x0 > 0, right = x0 + kTW < a.w;
-        float d0[RPT][kTW], d1[RPT][kTW];
+        float d[ORT][kTW];
 #pragma unroll
-        for (int r = 0; r < RPT; ++r)
+        for (int r = 0; r < ORT; ++r)
 #pragma unroll
-            for (int px = 0; px < kTW; ++px) {
-                d0[r][px] = bd0;
-                d1[r][px] = bd1;
-            }
+            for (int px = 0; px < kTW; ++px) d[r][px] = bdw;
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const std::uint16_t* xc = xs + (2 * cp + j) * kXC;
-            float wt[9];
+        for (int r = 0; r < ORT; ++r) {
+            const int gy = y0 + g * ORT + r;
 #pragma unroll
-            for (int t = 0; t < 9; ++t) {
-                const int e = j * 9 + t;  // halves 18cp + e of the pair's weights
-                wt[t] = (e & 1) ? hi_h(wdw[e >> 1]) : lo_h(wdw[e >> 1]);
-            }
+            for (int ky = 0; ky < 3; ++ky) {
+                const int iy = gy + ky - 1;
+                if (iy < 0 || iy >= a.h) continue;
+                const int rr = r + ky;
+                float xv[kTW + 2];
+                xv[0] = hi_h(xl[rr]);
 #pragma unroll
-            for (int r = 0; r < RPT; ++r) {
-                const int orow = rg * RPT + r, gy = y0 + orow;
-#pragma unroll
-                for (int ky = 0; ky < 3; ++ky) {
-                    const int iy = gy + ky - 1;
-                    if (iy < 0 || iy >= a.h) continue;
-                    const std::uint16_t* row = xc + (orow + ky) * kRow;
-                    const std::uint32_t l = *reinterpret_cast<const std::uint32_t*>(row + 6);
-                    const u32x4 m = *reinterpret_cast<const u32x4*>(row + 8);
-                    const std::uint32_t rr = *reinterpret_cast<const std::uint32_t*>(row + 16);
-                    float xv[kTW + 2];
-                    xv[0] = hi_h(l);
-#pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        xv[1 + 2 * i] = lo_h(m[i]);
-                        xv[2 + 2 * i] = hi_h(m[i]);
-                    }
-                    xv[kTW + 1] = lo_h(rr);
-#pragma unroll
-                    for (int px = 0; px < kTW; ++px)
-#pragma unroll
-                        for (int kx = 0; kx < 3; ++kx) {
-                            if (px + kx == 0 && !left) continue;
-                            if (px + kx == kTW + 1 && !right) continue;
-                            float& acc = j ? d1[r][px] : d0[r][px];
-                            acc = fmaf(xv[px + kx], wt[ky * 3 + kx], acc);
-                        }
+                for (int i = 0; i < 4; ++i) {
+                    xv[1 + 2 * i] = lo_h(xm[rr][i]);
+                    xv[2 + 2 * i] = hi_h(xm[rr][i]);
                 }
+                xv[kTW + 1] = lo_h(xr[rr]);
+#pragma unroll
+                for (int px = 0; px < kTW; ++px)
+#pragma unroll
+                    for (int kx = 0; kx < 3; ++kx) {
+                        if (px + kx == 0 && !left) continue;
+                        if (px + kx == kTW + 1 && !right) continue;
+                        d[r][px] = fmaf(xv[px + kx], h2f(wdw[ky * 3 + kx]), d[r][px]);
+                    }
             }
         }
 #pragma unroll
-        for (int r = 0; r < RPT; ++r)
+        for (int r = 0; r < ORT; ++r)
 #pragma unroll
-            for (int px = 0; px < kTW; ++px) {
-                const int p = (rg * RPT + r) * kTW + px;
-                const std::uint32_t v = static_cast<std::uint32_t>(f2h(d0[r][px])) |
-                                        (static_cast<std::uint32_t>(f2h(d1[r][px])) << 16);
-                *reinterpret_cast<std::uint32_t*>(&ds[p * DST + 2 * cp]) = v;
-            }
+            for (int px = 0; px < kTW; ++px) ds[((g * ORT + r) * kTW + px) * DST + c] = f2h(d[r][px]);
     }
     lds_barrier();
 
-    // ---- 3. expand 1x1 C -> E, round, LeakyReLU, round -> es --------------
+    // ---- 2. expand 1x1 C -> E, round, LeakyReLU, round -> es --------------
 #pragma unroll
     for (int ks = 0; ks < KS1; ++ks) {
         const half8 bv = *reinterpret_cast<const half8*>(&ds[pl * DST + ks * 16 + koff]);
@@ -227,7 +236,7 @@ __global__ __launch_bounds__(256) void dwblock_kernel(DwBlockArgs a)
         }
         __builtin_amdgcn_sched_barrier(0);
     }
-    // Project accumulators (b2) and the residual rows, loaded ahead of use.
+    // Project accumulators seeded with b2.
     floatx16 acc2[MT2];
 #pragma unroll
     for (int m = 0; m < MT2; ++m)
@@ -237,35 +246,23 @@ __global__ __launch_bounds__(256) void dwblock_kernel(DwBlockArgs a)
 #pragma unroll
             for (int i = 0; i < 4; ++i) acc2[m][4 * j + i] = bv[i];
         }
-    u32x4 res[RV];
+    {
+        const bool max_form = a.alpha >= 0.0f && a.alpha <= 1.0f;
+        typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 #pragma unroll
-    for (int i = 0; i < RV; ++i) {
-        const int q = tid + 256 * i, ch = q / kTH, gy = min(y0 + q % kTH, a.h - 1);  // rows past h are not stored
-        res[i] = *reinterpret_cast<const u32x4*>(xb + ch * plane + static_cast<size_t>(gy) * a.w + x0);
-    }
-    // es aliases xs: every wave finished its depthwise reads before the
-    // barrier above, so the expand results may overwrite the halo tile.
+        for (int m = 0; m < MT1; ++m) {
+            const int mt = wave * MT1 + m;
 #pragma unroll
-    for (int m = 0; m < MT1; ++m) {
-        const int mt = wave * MT1 + m;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            std::uint16_t hv[4];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                hv[i] = f2h(acc1[m][4 * j + i]);
-                const float f = h2f(hv[i]);
-                if (f < 0.0f) hv[i] = leaky_f16(f, a.alpha);
+            for (int j = 0; j < 4; ++j) {
+                const std::uint32_t lo = leaky_pair(acc1[m][4 * j], acc1[m][4 * j + 1], a.alpha, max_form);
+                const std::uint32_t hi = leaky_pair(acc1[m][4 * j + 2], acc1[m][4 * j + 3], a.alpha, max_form);
+                *reinterpret_cast<u32x2*>(&es[pl * EST + mt * 32 + 8 * j + hsel]) = u32x2{lo, hi};
             }
-            const std::uint32_t lo = hv[0] | (static_cast<std::uint32_t>(hv[1]) << 16);
-            const std::uint32_t hi = hv[2] | (static_cast<std::uint32_t>(hv[3]) << 16);
-            typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
-            *reinterpret_cast<u32x2*>(&es[pl * EST + mt * 32 + 8 * j + hsel]) = u32x2{lo, hi};
         }
     }
     lds_barrier();
 
-    // ---- 4. project 1x1 E -> C, round -> ys[channel][pixel] ---------------
+    // ---- 3. project 1x1 E -> C, round -> ys[channel][pixel] ---------------
 #pragma unroll
     for (int ks = 0; ks < KS2; ++ks) {
         const half8 bv = *reinterpret_cast<const half8*>(&es[pl * EST + ks * 16 + koff]);
@@ -288,11 +285,11 @@ __global__ __launch_bounds__(256) void dwblock_kernel(DwBlockArgs a)
     }
     lds_barrier();
 
-    // ---- 5. residual add, 16-byte rows out ------------------------------
+    // ---- 4. residual add, 16-byte rows out ------------------------------
     std::uint16_t* yb = a.y + static_cast<size_t>(b) * C * plane;
 #pragma unroll
     for (int i = 0; i < RV; ++i) {
-        const int q = tid + 256 * i, ch = q / kTH, row = q % kTH, gy = y0 + row;
+        const int q = tid + T * i, ch = q / kTH, row = q % kTH, gy = y0 + row;
         if (gy >= a.h) continue;
         const u32x4 pv = *reinterpret_cast<const u32x4*>(&ys[ch * kYS + row * kTW]);
         u32x4 o;
@@ -309,7 +306,7 @@ __global__ __launch_bounds__(256) void dwblock_kernel(DwBlockArgs a)
 template <int C, int E>
 void launch(const DwBlockArgs& a, dim3 grid, hipStream_t s)
 {
-    hipLaunchKernelGGL((dwblock_kernel<C, E>), grid, dim3(256), 0, s, a);
+    hipLaunchKernelGGL((dwblock_kernel<C, E>), grid, dim3(BlockCfg<C, E>::T), 0, s, a);
 }
 
 }  // namespace
@@ -348,6 +345,8 @@ int mlvc_hip_dwblock_launch(const mlvc_hip_dwblock_desc* d, mlvc_hip_stream s)
             throw std::runtime_error("dwblock: unsupported geometry");
         if (!d->x || !d->y || !d->dw_w || !d->dw_b || !d->w1 || !d->b1 || !d->w2 || !d->b2)
             throw std::runtime_error("dwblock: null tensor");
+        if (static_cast<std::uint64_t>(d->c) * d->h * d->w * 2 + 64 >= static_cast<std::uint64_t>(kOutOfRange))
+            throw std::runtime_error("dwblock: image too large for 32-bit buffer offsets");
         DwBlockArgs a{static_cast<const std::uint16_t*>(d->x), static_cast<std::uint16_t*>(d->y),
                       static_cast<const std::uint16_t*>(d->dw_w), d->dw_b,
                       static_cast<const std::uint16_t*>(d->w1), d->b1,

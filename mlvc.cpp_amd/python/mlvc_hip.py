@@ -78,6 +78,19 @@ def device_lib() -> C.CDLL:
     return _dev
 
 
+def conv_variants() -> list[str]:
+    """Names of the conv tile variants (index order); index 0 is the direct fallback."""
+    lib = device_lib()
+    lib.mlvc_hip_conv_variant_name.restype = C.c_char_p
+    lib.mlvc_hip_conv_variant_name.argtypes = [C.c_int]
+    names = []
+    while True:
+        name = lib.mlvc_hip_conv_variant_name(len(names)).decode()
+        if name == "invalid":
+            return names
+        names.append(name)
+
+
 def _check(rc: int) -> None:
     if rc != 0:
         raise MlvcError(backend_lib().mlvc_backend_last_error().decode())

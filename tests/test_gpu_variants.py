@@ -1,0 +1,62 @@
+"""Every conv tile variant on every conv geometry of the MLVC-shaped graphs.
+
+The backend tunes the tile variant per launch at load time, so a variant that
+is wrong on some geometry could pass the other tests only because it was not
+the fastest there. Here MLVC_HIP_CONV_VARIANT forces each variant in turn;
+each result must match the oracle, and all variants of one kernel size must
+agree bit for bit (they accumulate in the same K order).
+"""
+
+import numpy as np
+import pytest
+
+import graphs
+import mlvc_hip
+import mlvc_oracle
+from conftest import assert_parity
+
+pytestmark = pytest.mark.gpu
+
+# (name, n, ic, h, w, oc, k, stride, pad, options): the convs of mlvc_s_tiny
+# (32x64), of the 1920x1088 graph at reduced size, and ragged shapes.
+CASES = [
+    ("unshuffle_in", 1, 12, 16, 32, 64, 3, 1, 1, dict(s2d=2, epilogue="lrelu")),
+    ("concat_1x1", 1, 128, 16, 32, 64, 1, 1, 0, dict(concat_ic=64, epilogue="lrelu")),
+    ("down_s2", 1, 64, 16, 32, 128, 3, 2, 1, dict(epilogue="lrelu")),
+    ("down_s2_4x8", 1, 128, 8, 16, 192, 3, 2, 1, dict(epilogue="lrelu")),
+    ("mid_4x8", 1, 192, 4, 8, 256, 3, 1, 1, dict(epilogue="lrelu")),
+    ("synth_4x8", 1, 256, 4, 8, 192, 3, 1, 1, dict(epilogue="lrelu")),
+    ("shuffle_4x8", 1, 192, 4, 8, 512, 3, 1, 1, dict(epilogue="lrelu", d2s=2)),
+    ("shuffle_8x16", 1, 128, 8, 16, 256, 3, 1, 1, dict(epilogue="lrelu", d2s=2)),
+    ("recon_16x32", 1, 64, 16, 32, 12, 3, 1, 1, dict(d2s=2)),
+    ("ragged_s1", 1, 72, 13, 27, 96, 3, 1, 1, dict(epilogue="residual")),
+    ("ragged_s2", 1, 40, 11, 26, 72, 3, 2, 1, dict()),
+    ("ragged_1x1", 2, 48, 7, 13, 80, 1, 1, 0, dict(epilogue="residual")),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_every_variant(tmp_path, monkeypatch, case):
+    name, n, ic, h, w, oc, k, s, p, opts = case
+    shapes = graphs.single_conv_graph(tmp_path, "m", n, ic, h, w, oc, k, s, p, seed=len(name), **opts)
+    rng = np.random.default_rng(5)
+    ins = [graphs.half(rng.uniform(-1, 1, sh)) for sh in shapes]
+    want = mlvc_oracle.OraclePlan(tmp_path, "m").run(ins)[0]
+    first, ran = None, []
+    for v in mlvc_hip.conv_variants()[1:]:
+        monkeypatch.setenv("MLVC_HIP_CONV_VARIANT", v)
+        gpu = mlvc_hip.Backend(tmp_path, "hip")
+        gpu.load("m")
+        kinds = [l["kind"] for l in gpu.launches()]
+        if not any(kd.startswith(v + "+") or kd == v for kd in kinds):
+            gpu.close()
+            continue  # not eligible for this geometry
+        got = gpu.run(ins)[0]
+        gpu.close()
+        assert_parity(got, want, f"{name} with {v}")
+        if first is None:
+            first = (v, got)
+        else:
+            assert (got == first[1]).all(), f"{name}: {v} differs from {first[0]}"
+        ran.append(v)
+    assert len(ran) >= 2, ran
