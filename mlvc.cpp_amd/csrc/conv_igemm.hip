@@ -192,7 +192,7 @@ __device__ __forceinline__ std::uint32_t pack_half(std::uint32_t lo_word, std::u
 }
 
 template <class C>
-__global__ __launch_bounds__(256) void conv_mfma_kernel(ConvArgs a)
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void conv_mfma_kernel(ConvArgs a)
 {
     __shared__ __attribute__((aligned(16))) std::uint16_t lds[C::LDS];
     auto lds_in = [&](int stage) { return lds + stage * C::STAGE; };
