@@ -161,9 +161,11 @@ struct Cfg {
     static constexpr int IW_S = VEC ? NSEG * 8 : IW_T;
     static constexpr int IW_E = (IW_S + 1) / 2;  // even columns (stride-2 layout)
     static constexpr int PST = KC + 8;           // LDS halves per staged pixel
-    // One extra 16-byte pad per 8 staged columns keeps both the transposed
-    // 8-pixel writes and the consecutive-pixel B reads free of bank conflicts.
-    static constexpr int ROW = IW_S * PST + ((IW_S - 1) / 8 + 1) * 8;
+    // Staged rows are padded by 16 bytes, so consecutive rows start 4 banks
+    // apart: the transposed commit writes (8 lanes = 8 consecutive rows of
+    // one pixel column) and the B reads (8 lanes = 8 consecutive pixels of a
+    // row, PST = 12 dwords apart, any alignment) are both free of conflicts.
+    static constexpr int ROW = IW_S * PST + 8;
     static constexpr int IN_LDS = IH_T * ROW;
     static constexpr int UNITS = (KC / 8) * IH_T * NSEG;  // 8 channels x 8 columns
     static constexpr int UNITS_PER_T = (UNITS + kThreads - 1) / kThreads;
@@ -183,7 +185,7 @@ struct Cfg {
 
     __device__ static constexpr int col(int x) { return S == 2 ? ((x & 1) ? IW_E + (x >> 1) : (x >> 1)) : x; }
     // LDS offset (halves) of staged pixel (row, column).
-    __device__ static constexpr int at(int row, int x) { return row * ROW + col(x) * PST + (col(x) >> 3) * 8; }
+    __device__ static constexpr int at(int row, int x) { return row * ROW + col(x) * PST; }
 };
 
 __device__ __forceinline__ std::uint32_t pack_half(std::uint32_t lo_word, std::uint32_t hi_word, bool upper)
@@ -242,11 +244,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void c
 #pragma unroll
         for (int i = 0; i < C::UNITS_PER_T; ++i) {
             const int u = tid + i * C::kThreads;
-            const int sg = u % C::NSEG, yi = (u / C::NSEG) % C::IH_T;
+            const int yi = u % C::IH_T, sg = (u / C::IH_T) % C::NSEG;
             const int iy = iy0 + yi, ix = xa + sg * 8;
             const bool ok = u < C::UNITS && iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw;
             pix_off[i] = ok ? static_cast<std::uint32_t>(iy * a.iw + ix) * 2u : kOutOfRange;
-            unit_c8[i] = u / (C::NSEG * C::IH_T);
+            unit_c8[i] = u / (C::NSEG * C::IH_T);  // units: rows fastest, then segments, then channel groups
         }
     }
     auto fetch = [&](int chunk, int stage) {
@@ -305,7 +307,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void c
             for (int i = 0; i < C::UNITS_PER_T; ++i) {
                 const int u = tid + i * C::kThreads;
                 if (u < C::UNITS) {
-                    const int sg = u % C::NSEG, yi = (u / C::NSEG) % C::IH_T, c8 = u / (C::NSEG * C::IH_T);
+                    const int yi = u % C::IH_T, sg = (u / C::IH_T) % C::NSEG, c8 = u / (C::NSEG * C::IH_T);
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
                         const bool up = j & 1;
