@@ -77,4 +77,49 @@ __device__ __forceinline__ float mul_f32(float a, float b)
 
 __device__ __forceinline__ std::uint16_t leaky_f16(float f, float alpha) { return f2h(mul_f32(f, alpha)); }
 
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float lo_f16(std::uint32_t v) { return h2f(static_cast<std::uint16_t>(v & 0xFFFFu)); }
+__device__ __forceinline__ float hi_f16(std::uint32_t v) { return h2f(static_cast<std::uint16_t>(v >> 16)); }
+
+// Two FP32 values -> packed FP16 pair (RNE), low half first.
+__device__ __forceinline__ std::uint32_t pack_f16(float a0, float a1)
+{
+    const half2_t h = {static_cast<_Float16>(a0), static_cast<_Float16>(a1)};
+    return __builtin_bit_cast(std::uint32_t, h);
+}
+
+// LeakyReLU of a packed pair of FP16 values (already rounded), as in
+// leaky_pair below.
+__device__ __forceinline__ std::uint32_t leaky_h2(std::uint32_t hv, float alpha, bool max_form)
+{
+    const half2_t h = __builtin_bit_cast(half2_t, hv);
+    if (max_form) {
+        const half2_t p = {static_cast<_Float16>(mul_f32(static_cast<float>(h[0]), alpha)),
+                           static_cast<_Float16>(mul_f32(static_cast<float>(h[1]), alpha))};
+        return __builtin_bit_cast(std::uint32_t, __builtin_elementwise_max(h, p));
+    }
+    const std::uint16_t h0 = static_cast<std::uint16_t>(hv), h1 = static_cast<std::uint16_t>(hv >> 16);
+    const std::uint16_t r0 = h2f(h0) < 0.0f ? leaky_f16(h2f(h0), alpha) : h0;
+    const std::uint16_t r1 = h2f(h1) < 0.0f ? leaky_f16(h2f(h1), alpha) : h1;
+    return r0 | (static_cast<std::uint32_t>(r1) << 16);
+}
+
+// Two FP32 accumulators -> packed FP16 pair after LeakyReLU on the rounded
+// values. For 0 <= alpha <= 1 this is max(h, fp16(h * alpha)), which equals
+// the select form because rounding is monotonic; otherwise the select form.
+__device__ __forceinline__ std::uint32_t leaky_pair(float a0, float a1, float alpha, bool max_form)
+{
+    const half2_t h = {static_cast<_Float16>(a0), static_cast<_Float16>(a1)};
+    if (max_form) {
+        const half2_t p = {static_cast<_Float16>(mul_f32(static_cast<float>(h[0]), alpha)),
+                           static_cast<_Float16>(mul_f32(static_cast<float>(h[1]), alpha))};
+        return __builtin_bit_cast(std::uint32_t, __builtin_elementwise_max(h, p));
+    }
+    const std::uint16_t h0 = __builtin_bit_cast(std::uint16_t, h[0]), h1 = __builtin_bit_cast(std::uint16_t, h[1]);
+    const std::uint16_t r0 = h2f(h0) < 0.0f ? leaky_f16(h2f(h0), alpha) : h0;
+    const std::uint16_t r1 = h2f(h1) < 0.0f ? leaky_f16(h2f(h1), alpha) : h1;
+    return r0 | (static_cast<std::uint32_t>(r1) << 16);
+}
+
 }  // namespace mlvc_hip

@@ -1,503 +1,20 @@
-// FP16 convolution (groups == 1) on gfx950 MFMA as an implicit GEMM.
-//
-//   D[oc, p] = bias[oc] + sum_k W[oc, k] * X[k, p],  k = (chunk, tap, c16)
-//
-// One workgroup (4 waves) owns BM output channels x a TH x TW output-pixel
-// tile. Per input-channel chunk of KC channels it stages
-//   * the NCHW input halo tile into LDS channel-last ([pixel][KC + 8 pad]),
-//     so the MFMA B fragment of a lane (8 consecutive channels of one pixel)
-//     is a single 16-byte LDS read for every tap; for stride 2 the even and
-//     odd input columns are stored in separate halves of an LDS row so that
-//     consecutive output pixels read consecutive LDS pixels;
-//   * the chunk's weights, pre-packed at load time in exact A-fragment order
-//     ([tap][k16][m32][lane][8]), as a contiguous 16-byte-vector copy.
-// The next chunk is fetched into registers while the current one is
-// consumed (v_mfma_f32_32x32x16_f16, FP32 accumulators seeded with the
-// bias). The epilogue rounds to FP16 (RNE), applies LeakyReLU or the
-// residual add on the rounded value exactly like the reference CPU GEMM
-// epilogue (backends/cpu/src/kernels_scalar.cpp:178-192), and stores either
-// plainly or through the DEPTH_TO_SPACE (CRD) index map.
-//
-// Reference kernels this replaces: pointwise_conv.cu:116-338 (1x1 mma.sync),
-// cutlass.cu:116-161 (1x1 EVT epilogues, spatial fprop), spatial_conv.cu:
-// 1-293 (implicit-GEMM KxK), generic_conv.cu:1-82 (fallback).
+// FP16 convolution (groups == 1): variant table, planning, weight packing
+// and launch behind the device C ABI. The MFMA kernel template is in
+// conv_kernel.hpp and its tile variants are instantiated per kernel size in
+// conv_k3s1.hip, conv_k3s2.hip and conv_k1.hip.
 
-#include "common.hpp"
-#include "mlvc_hip_device.h"
+#include "conv_kernel.hpp"
 
 #include <algorithm>
-#include <cstring>
 #include <vector>
 
 namespace mlvc_hip {
-namespace {
+namespace conv {
 
-// Raw buffer resource word 3 for gfx950 (32-bit data format, no swizzle).
-constexpr int kRawBufferFlags = 0x00020000;
-// Byte offset past the end of every staged tensor (each < 2 GiB), also after
-// adding up to 7 channel planes; raw buffer loads there return zeros.
-constexpr std::uint32_t kOutOfRange = 0x80000000u;
-
-struct ConvArgs {
-    const std::uint16_t* x;
-    const std::uint16_t* x2;
-    const std::uint16_t* w;
-    const float* bias;
-    const std::uint16_t* res;
-    std::uint16_t* y;
-    int ic_split, s2d, d2s;
-    int ic, ih, iw, oc, oh, ow, kh, kw, sh, sw, ph, pw;
-    int epi;
-    float alpha;
-    int tiles_x, nchunks;
-    int tiles, ocbs, nwg;  // pixel tiles per image, output-channel blocks, workgroups (tiles*ocbs*n)
-};
-
-// KC consecutive channels [c0, c0 + KC) of input pixel (iy, ix) of batch b,
-// packed in pairs, through the optional SPACE_TO_DEPTH / CONCAT maps. Zero
-// outside the image (padding) and for channels past IC (chunk padding).
-template <int KC>
-__device__ __forceinline__ void load_pixel(const ConvArgs& a, int b, int c0, int iy, int ix, std::uint32_t (&out)[KC / 2])
-{
-    std::uint16_t v[KC];
-#pragma unroll
-    for (int j = 0; j < KC; ++j) v[j] = 0;
-    if (iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw) {
-        if (a.s2d > 1) {
-            const int bs = a.s2d, b2 = bs * bs;
-            const int sW = a.iw * bs;
-            const size_t splane = static_cast<size_t>(a.ih) * bs * sW;
-            const std::uint16_t* p = a.x + static_cast<size_t>(b) * (a.ic / b2) * splane +
-                                     static_cast<size_t>(iy * bs) * sW + ix * bs;
-#pragma unroll
-            for (int j = 0; j < KC; ++j) {
-                const int c = c0 + j;
-                if (c < a.ic) {
-                    const int cs = c / b2, r = c - cs * b2, dy = r / bs, dx = r - dy * bs;
-                    v[j] = p[cs * splane + static_cast<size_t>(dy) * sW + dx];
-                }
-            }
-        } else {
-            const size_t hw = static_cast<size_t>(a.ih) * a.iw;
-            const size_t po = static_cast<size_t>(iy) * a.iw + ix;
-            const int c1 = a.x2 ? a.ic_split : a.ic;
-            const std::uint16_t* p = a.x + static_cast<size_t>(b) * c1 * hw + po;
-            const std::uint16_t* p2 = a.x2 ? a.x2 + static_cast<size_t>(b) * (a.ic - c1) * hw + po : nullptr;
-#pragma unroll
-            for (int j = 0; j < KC; ++j) {
-                const int c = c0 + j;
-                if (c < c1)
-                    v[j] = p[c * hw];
-                else if (c < a.ic)
-                    v[j] = p2[(c - c1) * hw];
-            }
-        }
-    }
-#pragma unroll
-    for (int j = 0; j < KC / 2; ++j) out[j] = static_cast<std::uint32_t>(v[2 * j]) | (static_cast<std::uint32_t>(v[2 * j + 1]) << 16);
-}
-
-// Single element of the conv input (used by the direct fallback).
-__device__ __forceinline__ std::uint16_t load_input(const ConvArgs& a, int b, int c, int iy, int ix)
-{
-    if (c >= a.ic || iy < 0 || iy >= a.ih || ix < 0 || ix >= a.iw) return 0;
-    if (a.s2d > 1) {
-        const int bs = a.s2d, b2 = bs * bs;
-        const int cs = c / b2, r = c - cs * b2, dy = r / bs, dx = r - dy * bs;
-        const int sc = a.ic / b2, sh = a.ih * bs, sw = a.iw * bs;
-        return a.x[(static_cast<size_t>(b * sc + cs) * sh + iy * bs + dy) * sw + ix * bs + dx];
-    }
-    if (a.x2) {
-        if (c >= a.ic_split)
-            return a.x2[(static_cast<size_t>(b * (a.ic - a.ic_split) + c - a.ic_split) * a.ih + iy) * a.iw + ix];
-        return a.x[(static_cast<size_t>(b * a.ic_split + c) * a.ih + iy) * a.iw + ix];
-    }
-    return a.x[(static_cast<size_t>(b * a.ic + c) * a.ih + iy) * a.iw + ix];
-}
-
-__device__ __forceinline__ std::uint16_t finish(const ConvArgs& a, float acc, int b, int oc, int oy, int ox)
-{
-    std::uint16_t h = f2h(acc);
-    if (a.epi == MLVC_EPI_LEAKY_RELU) {
-        const float f = h2f(h);
-        if (f < 0.0f) h = leaky_f16(f, a.alpha);
-    } else if (a.epi == MLVC_EPI_RESIDUAL_ADD) {
-        h = f2h(h2f(h) + h2f(a.res[(static_cast<size_t>(b * a.oc + oc) * a.oh + oy) * a.ow + ox]));
-    }
-    return h;
-}
-
-__device__ __forceinline__ void store_output(const ConvArgs& a, std::uint16_t h, int b, int oc, int oy, int ox)
-{
-    if (a.d2s > 1) {
-        const int bs = a.d2s, b2 = bs * bs;
-        const int c = oc / b2, r = oc - c * b2, dy = r / bs, dx = r - dy * bs;
-        const int occ = a.oc / b2, H = a.oh * bs, W = a.ow * bs;
-        a.y[(static_cast<size_t>(b * occ + c) * H + oy * bs + dy) * W + ox * bs + dx] = h;
-    } else {
-        a.y[(static_cast<size_t>(b * a.oc + oc) * a.oh + oy) * a.ow + ox] = h;
-    }
-}
-
-template <int BM_, int TH_, int TW_, int KH_, int KW_, int S_, int KC_, bool VEC_, bool DB_>
-struct Cfg {
-    static constexpr int BM = BM_, TH = TH_, TW = TW_, KH = KH_, KW = KW_, S = S_, KC = KC_;
-    static constexpr bool VEC = VEC_;  // 16-byte row-segment staging (needs W % 8 == 0)
-    // Two LDS stages: chunk k+1 is staged (weights by LDS DMA) while chunk k
-    // is multiplied, one barrier per chunk. Otherwise one stage, weights
-    // staged through registers, two barriers per chunk, half the LDS.
-    static constexpr bool DB = DB_;
-    static constexpr int kThreads = 256;
-    static constexpr int BN = TH * TW;
-    static constexpr int TAPS = KH * KW;
-    static constexpr int KS = KC / 16;  // 16-deep MFMA K steps per tap
-    static constexpr int MT = BM / 32;
-    static constexpr int WN = BN / 4;
-    static constexpr int NT = WN / 32;
-    static constexpr int IH_T = (TH - 1) * S + KH;
-    static constexpr int IW_T = (TW - 1) * S + KW;
-    // Vector staging covers input columns [floor8(ix0), floor8(ix0) + IW_S).
-    static constexpr int NSEG = (IW_T + 14) / 8;
-    static constexpr int IW_S = VEC ? NSEG * 8 : IW_T;
-    static constexpr int IW_E = (IW_S + 1) / 2;  // even columns (stride-2 layout)
-    static constexpr int PST = KC + 8;           // LDS halves per staged pixel
-    // Staged rows are padded by 16 bytes, so consecutive rows start 4 banks
-    // apart: the transposed commit writes (8 lanes = 8 consecutive rows of
-    // one pixel column) and the B reads (8 lanes = 8 consecutive pixels of a
-    // row, PST = 12 dwords apart, any alignment) are both free of conflicts.
-    static constexpr int ROW = IW_S * PST + 8;
-    static constexpr int IN_LDS = IH_T * ROW;
-    static constexpr int UNITS = (KC / 8) * IH_T * NSEG;  // 8 channels x 8 columns
-    static constexpr int UNITS_PER_T = (UNITS + kThreads - 1) / kThreads;
-    static constexpr int IN_PIX = IH_T * IW_T;
-    static constexpr int PIX_PER_T = (IN_PIX + kThreads - 1) / kThreads;
-    static constexpr int W_LDS = TAPS * KS * MT * 64 * 8;  // halves per chunk
-    static constexpr int W_VEC = W_LDS / 8;
-    static constexpr int W_PER_T = (W_VEC + kThreads - 1) / kThreads;
-    static constexpr int EPI_ROW = BN + 8;  // output staging row (one channel), halves
-    static constexpr int EPI_LDS = BM * EPI_ROW;
-    static constexpr int STAGE = IN_LDS + W_LDS;
-    static constexpr int W_INST = W_VEC / 64;  // 1 KB LDS DMA instructions per chunk
-    static constexpr int LDS = (DB ? 2 * STAGE : STAGE) > EPI_LDS ? (DB ? 2 * STAGE : STAGE) : EPI_LDS;
-    static_assert(BM % 32 == 0 && WN % 32 == 0 && KC % 16 == 0 && TW % 8 == 0 && W_VEC % 64 == 0, "tile shape");
-    static_assert(STAGE % 8 == 0, "stage alignment");
-    static_assert(LDS * 2 <= 160 * 1024, "LDS budget");
-
-    __device__ static constexpr int col(int x) { return S == 2 ? ((x & 1) ? IW_E + (x >> 1) : (x >> 1)) : x; }
-    // LDS offset (halves) of staged pixel (row, column).
-    __device__ static constexpr int at(int row, int x) { return row * ROW + col(x) * PST; }
-};
-
-__device__ __forceinline__ std::uint32_t pack_half(std::uint32_t lo_word, std::uint32_t hi_word, bool upper)
-{
-    return upper ? ((lo_word >> 16) | (hi_word & 0xFFFF0000u)) : ((lo_word & 0xFFFFu) | (hi_word << 16));
-}
-
-template <class C>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void conv_mfma_kernel(ConvArgs a)
-{
-    __shared__ __attribute__((aligned(16))) std::uint16_t lds[C::LDS];
-    auto lds_in = [&](int stage) { return lds + stage * C::STAGE; };
-    auto lds_w = [&](int stage) { return lds + stage * C::STAGE + C::IN_LDS; };
-
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    // Logical work item: output-channel block fastest, then pixel tiles in
-    // row-major order, then images; each XCD runs a contiguous range of them.
-    const int item = xcd_order(blockIdx.x, a.nwg);
-    const int ocb = item % a.ocbs, tile = (item / a.ocbs) % a.tiles, b = item / (a.ocbs * a.tiles);
-    const int tx0 = (tile % a.tiles_x) * C::TW, ty0 = (tile / a.tiles_x) * C::TH;
-    const int iy0 = ty0 * C::S - a.ph, ix0 = tx0 * C::S - a.pw;
-    // First staged input column (8-aligned for the vector path).
-    const int xa = C::VEC ? ix0 - (((ix0 % 8) + 8) % 8) : ix0;
-    const int col_off = ix0 - xa;
-
-    floatx16 acc[C::MT][C::NT];
-#pragma unroll
-    for (int mt = 0; mt < C::MT; ++mt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            const float bv = a.bias[ocb * C::BM + mt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)];
-#pragma unroll
-            for (int nt = 0; nt < C::NT; ++nt) acc[mt][nt][r] = bv;
-        }
-
-    const size_t hw = static_cast<size_t>(a.ih) * a.iw;
-    const int c1 = a.x2 ? a.ic_split : a.ic;
-    u32x4 vin[C::VEC ? C::UNITS_PER_T : 1][8];
-    std::uint32_t in_reg[C::VEC ? 1 : C::PIX_PER_T][C::KC / 2];
-    u32x4 w_reg[C::DB ? 1 : C::W_PER_T];
-    // Vector staging reads through raw buffer resources sized to this
-    // image's part of x (channels [0, c1)) and of x2 (the concat rest): a
-    // load past the end returns zeros, so padding rows/columns (offset set
-    // past the end) and channels past IC need no branch. The concat split
-    // falls on a chunk boundary, so each chunk reads one resource.
-    const std::uint32_t hw2 = static_cast<std::uint32_t>(hw) * 2u;
-    const std::uint16_t* x_img = a.x + static_cast<size_t>(b) * c1 * hw;
-    const std::uint16_t* x2_img = a.x2 ? a.x2 + static_cast<size_t>(b) * (a.ic - c1) * hw : x_img;
-    const __amdgpu_buffer_rsrc_t rx =
-        __builtin_amdgcn_make_buffer_rsrc(const_cast<std::uint16_t*>(x_img), 0, static_cast<int>(c1 * hw2), kRawBufferFlags);
-    const __amdgpu_buffer_rsrc_t rx2 = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<std::uint16_t*>(x2_img), 0, static_cast<int>(a.x2 ? (a.ic - c1) * hw2 : 0u), kRawBufferFlags);
-    std::uint32_t pix_off[C::VEC ? C::UNITS_PER_T : 1];
-    int unit_c8[C::VEC ? C::UNITS_PER_T : 1];
-    if constexpr (C::VEC) {
-#pragma unroll
-        for (int i = 0; i < C::UNITS_PER_T; ++i) {
-            const int u = tid + i * C::kThreads;
-            const int yi = u % C::IH_T, sg = (u / C::IH_T) % C::NSEG;
-            const int iy = iy0 + yi, ix = xa + sg * 8;
-            const bool ok = u < C::UNITS && iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw;
-            pix_off[i] = ok ? static_cast<std::uint32_t>(iy * a.iw + ix) * 2u : kOutOfRange;
-            unit_c8[i] = u / (C::NSEG * C::IH_T);  // units: rows fastest, then segments, then channel groups
-        }
-    }
-    auto fetch = [&](int chunk, int stage) {
-        const int c0 = chunk * C::KC;
-        if constexpr (C::VEC) {
-            const bool second = a.x2 && c0 >= c1;
-            const __amdgpu_buffer_rsrc_t r = second ? rx2 : rx;
-            const std::uint32_t cbase = static_cast<std::uint32_t>(second ? c0 - c1 : c0);
-#pragma unroll
-            for (int i = 0; i < C::UNITS_PER_T; ++i) {
-                const std::uint32_t off = pix_off[i] == kOutOfRange
-                                              ? kOutOfRange
-                                              : pix_off[i] + (cbase + static_cast<std::uint32_t>(unit_c8[i]) * 8u) * hw2;
-                // The channel offset goes in the VGPR operand: the range check
-                // covers that operand only, so channels past the end read zeros.
-#pragma unroll
-                for (int k = 0; k < 8; ++k)
-                    vin[i][k] = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(off + k * hw2), 0, 0);
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < C::PIX_PER_T; ++i) {
-                const int pix = tid + i * C::kThreads;
-                if (pix < C::IN_PIX) {
-                    const int yi = pix / C::IW_T, xi = pix - yi * C::IW_T;
-                    load_pixel<C::KC>(a, b, c0, iy0 + yi, ix0 + xi, in_reg[i]);
-                }
-            }
-        }
-        const u32x4* ws = reinterpret_cast<const u32x4*>(a.w + (static_cast<size_t>(ocb) * a.nchunks + chunk) * C::W_LDS);
-        if constexpr (C::DB) {
-            // The packed chunk is copied verbatim: LDS DMA, 1 KB per wave
-            // instruction, lane l of instruction j moving vector 64*j + l.
-            u32x4* dst = reinterpret_cast<u32x4*>(lds_w(stage));
-#pragma unroll
-            for (int i = 0; i < (C::W_INST + 3) / 4; ++i) {
-                const int j = wave + 4 * i;
-                if (j < C::W_INST)
-                    __builtin_amdgcn_global_load_lds(ws + j * 64 + lane,
-                                                     (__attribute__((address_space(3))) void*)(dst + j * 64), 16, 0, 0);
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < C::W_PER_T; ++i) {
-                const int e = tid + i * C::kThreads;
-                if (e < C::W_VEC) w_reg[i] = ws[e];
-            }
-        }
-    };
-    auto commit = [&](int stage) {
-        std::uint16_t* const in_s = lds_in(stage);
-        if constexpr (C::VEC) {
-            // 8x8 transpose in registers: staged pixel j of the segment gets
-            // the 8 channels of the unit as one 16-byte LDS write.
-#pragma unroll
-            for (int i = 0; i < C::UNITS_PER_T; ++i) {
-                const int u = tid + i * C::kThreads;
-                if (u < C::UNITS) {
-                    const int yi = u % C::IH_T, sg = (u / C::IH_T) % C::NSEG, c8 = u / (C::NSEG * C::IH_T);
-#pragma unroll
-                    for (int j = 0; j < 8; ++j) {
-                        const bool up = j & 1;
-                        const int wd = j >> 1;
-                        const u32x4 t = {pack_half(vin[i][0][wd], vin[i][1][wd], up), pack_half(vin[i][2][wd], vin[i][3][wd], up),
-                                         pack_half(vin[i][4][wd], vin[i][5][wd], up), pack_half(vin[i][6][wd], vin[i][7][wd], up)};
-                        *reinterpret_cast<u32x4*>(&in_s[C::at(yi, sg * 8 + j) + c8 * 8]) = t;
-                    }
-                }
-            }
-        } else {
-#pragma unroll
-            for (int i = 0; i < C::PIX_PER_T; ++i) {
-                const int pix = tid + i * C::kThreads;
-                if (pix < C::IN_PIX) {
-                    const int yi = pix / C::IW_T, xi = pix - yi * C::IW_T;
-                    u32x4* dst = reinterpret_cast<u32x4*>(&in_s[C::at(yi, xi)]);
-#pragma unroll
-                    for (int q = 0; q < C::KC / 8; ++q)
-                        dst[q] = u32x4{in_reg[i][4 * q], in_reg[i][4 * q + 1], in_reg[i][4 * q + 2], in_reg[i][4 * q + 3]};
-                }
-            }
-        }
-        if constexpr (!C::DB) {
-#pragma unroll
-            for (int i = 0; i < C::W_PER_T; ++i) {
-                const int e = tid + i * C::kThreads;
-                if (e < C::W_VEC) reinterpret_cast<u32x4*>(lds_w(0))[e] = w_reg[i];
-            }
-        }
-    };
-
-    // Per-lane output pixel of each 32-wide N block, in tile coordinates.
-    int pyi[C::NT], pxi[C::NT];
-#pragma unroll
-    for (int nt = 0; nt < C::NT; ++nt) {
-        const int p = wave * C::WN + nt * 32 + (lane & 31);
-        pyi[nt] = (p / C::TW) * C::S;
-        pxi[nt] = (p % C::TW) * C::S + col_off;
-    }
-    const int koff = (lane >> 5) * 8;
-
-    auto compute = [&](int stage) {
-        const std::uint16_t* const in_s = lds_in(stage);
-        const std::uint16_t* const w_s = lds_w(stage);
-#pragma unroll
-        for (int tap = 0; tap < C::TAPS; ++tap) {
-            const int ky = tap / C::KW, kx = tap % C::KW;
-            int boff[C::NT];
-#pragma unroll
-            for (int nt = 0; nt < C::NT; ++nt) boff[nt] = C::at(pyi[nt] + ky, pxi[nt] + kx) + koff;
-#pragma unroll
-            for (int ks = 0; ks < C::KS; ++ks) {
-                half8 av[C::MT], bv[C::NT];
-#pragma unroll
-                for (int mt = 0; mt < C::MT; ++mt)
-                    av[mt] = *reinterpret_cast<const half8*>(&w_s[(((tap * C::KS + ks) * C::MT + mt) * 64 + lane) * 8]);
-#pragma unroll
-                for (int nt = 0; nt < C::NT; ++nt) bv[nt] = *reinterpret_cast<const half8*>(&in_s[boff[nt] + ks * 16]);
-#pragma unroll
-                for (int mt = 0; mt < C::MT; ++mt)
-#pragma unroll
-                    for (int nt = 0; nt < C::NT; ++nt)
-                        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[mt], bv[nt], acc[mt][nt], 0, 0, 0);
-            }
-        }
-    };
-
-    if constexpr (C::DB) {
-        fetch(0, 0);
-        commit(0);
-        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's LDS DMA has landed
-        __syncthreads();
-        for (int chunk = 0; chunk < a.nchunks; ++chunk) {
-            const int cur = chunk & 1;
-            const bool more = chunk + 1 < a.nchunks;
-            // Stage cur^1 was last read before the previous barrier.
-            if (more) fetch(chunk + 1, cur ^ 1);
-            compute(cur);
-            if (more) {
-                commit(cur ^ 1);
-                asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            }
-            __syncthreads();
-        }
-    } else {
-        fetch(0, 0);
-        commit(0);
-        __syncthreads();
-        for (int chunk = 0; chunk < a.nchunks; ++chunk) {
-            const bool more = chunk + 1 < a.nchunks;
-            if (more) fetch(chunk + 1, 0);
-            compute(0);
-            __syncthreads();
-            if (more) {
-                commit(0);
-                __syncthreads();
-            }
-        }
-    }
-
-    // Epilogue, stage 1: each lane writes its FP16-rounded accumulators into
-    // an LDS tile [oc][pixel] (all indices static, so nothing spills).
-    // The main loop ended with a barrier, so the staging buffers are free.
-#pragma unroll
-    for (int mt = 0; mt < C::MT; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < C::NT; ++nt)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-                const int ocl = mt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                const int pl = wave * C::WN + nt * 32 + (lane & 31);
-                lds[ocl * C::EPI_ROW + pl] = f2h(acc[mt][nt][r]);
-            }
-    __syncthreads();
-
-    // Stage 2: the epilogue acts on the rounded value. Vector path: 8
-    // consecutive pixels of a channel per thread, 16-byte stores; with a
-    // fused DEPTH_TO_SPACE(2) the two dx channels of one (c, dy) are
-    // interleaved into 16 contiguous output pixels.
-    constexpr int GROUPS = C::BN / 8;
-    auto epi8 = [&](std::uint16_t (&h)[8], int oc, int oy, int ox) {
-        if (a.epi == MLVC_EPI_LEAKY_RELU) {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const float f = h2f(h[j]);
-                if (f < 0.0f) h[j] = leaky_f16(f, a.alpha);
-            }
-        } else if (a.epi == MLVC_EPI_RESIDUAL_ADD) {
-            const u32x4 rv = *reinterpret_cast<const u32x4*>(a.res + (static_cast<size_t>(b * a.oc + oc) * a.oh + oy) * a.ow + ox);
-            const std::uint16_t* r = reinterpret_cast<const std::uint16_t*>(&rv);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) h[j] = f2h(h2f(h[j]) + h2f(r[j]));
-        }
-    };
-    if (a.ow % 8 == 0 && (a.d2s <= 1 || a.d2s == 2)) {
-        const bool d2s2 = a.d2s == 2;
-        const int units = d2s2 ? (C::BM / 4) * 2 * GROUPS : C::BM * GROUPS;
-        for (int u = tid; u < units; u += C::kThreads) {
-            const int g = u % GROUPS;
-            const int pl = g * 8;
-            const int oy = ty0 + pl / C::TW, ox = tx0 + pl % C::TW;
-            if (oy >= a.oh || ox >= a.ow) continue;
-            if (d2s2) {
-                const int dy = (u / GROUPS) & 1, cq = u / (2 * GROUPS);
-                const int ocl = cq * 4 + dy * 2, oc = ocb * C::BM + ocl;
-                if (oc >= a.oc) continue;
-                std::uint16_t h0[8], h1[8];
-                *reinterpret_cast<u32x4*>(h0) = *reinterpret_cast<const u32x4*>(&lds[ocl * C::EPI_ROW + pl]);
-                *reinterpret_cast<u32x4*>(h1) = *reinterpret_cast<const u32x4*>(&lds[(ocl + 1) * C::EPI_ROW + pl]);
-                epi8(h0, oc, oy, ox);
-                epi8(h1, oc + 1, oy, ox);
-                std::uint16_t o[16];
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    o[2 * j] = h0[j];
-                    o[2 * j + 1] = h1[j];
-                }
-                const int W2 = a.ow * 2;
-                std::uint16_t* dst = a.y + (static_cast<size_t>(b * (a.oc / 4) + oc / 4) * (a.oh * 2) + oy * 2 + dy) * W2 + ox * 2;
-                reinterpret_cast<u32x4*>(dst)[0] = *reinterpret_cast<const u32x4*>(o);
-                reinterpret_cast<u32x4*>(dst)[1] = *reinterpret_cast<const u32x4*>(o + 8);
-            } else {
-                const int ocl = u / GROUPS, oc = ocb * C::BM + ocl;
-                if (oc >= a.oc) continue;
-                std::uint16_t h[8];
-                *reinterpret_cast<u32x4*>(h) = *reinterpret_cast<const u32x4*>(&lds[ocl * C::EPI_ROW + pl]);
-                epi8(h, oc, oy, ox);
-                *reinterpret_cast<u32x4*>(a.y + (static_cast<size_t>(b * a.oc + oc) * a.oh + oy) * a.ow + ox) =
-                    *reinterpret_cast<const u32x4*>(h);
-            }
-        }
-    } else {
-        for (int e = tid; e < C::BM * C::BN; e += C::kThreads) {
-            const int ocl = e / C::BN, pl = e - ocl * C::BN;
-            const int oc = ocb * C::BM + ocl;
-            const int oy = ty0 + pl / C::TW, ox = tx0 + pl % C::TW;
-            if (oc < a.oc && oy < a.oh && ox < a.ow) {
-                std::uint16_t h = lds[ocl * C::EPI_ROW + pl];
-                if (a.epi == MLVC_EPI_LEAKY_RELU) {
-                    const float f = h2f(h);
-                    if (f < 0.0f) h = leaky_f16(f, a.alpha);
-                } else if (a.epi == MLVC_EPI_RESIDUAL_ADD) {
-                    h = f2h(h2f(h) + h2f(a.res[(static_cast<size_t>(b * a.oc + oc) * a.oh + oy) * a.ow + ox]));
-                }
-                store_output(a, h, b, oc, oy, ox);
-            }
-        }
-    }
-}
+// Host-side tables of the per-size files (count returned through n).
+const Variant* variants_k3s1(int* n);
+const Variant* variants_k3s2(int* n);
+const Variant* variants_k1(int* n);
 
 // Generic fallback: one thread per output, FP32 fused multiply-add in
 // (ic, ky, kx) order. Used only for shapes without an MFMA variant.
@@ -524,61 +41,29 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(ConvArgs a, int n)
 }
 
 // ---------------------------------------------------------------- variants
-struct Variant {
-    const char* name;
-    int bm, th, tw, kh, kw, s, kc;  // bm == 0: direct fallback
-    void (*launch_scalar)(const ConvArgs&, dim3, hipStream_t);
-    void (*launch_vec)(const ConvArgs&, dim3, hipStream_t);
-};
 
-template <class C>
-void launch_mfma(const ConvArgs& a, dim3 grid, hipStream_t s)
+}  // namespace conv
+
+namespace {
+
+using namespace conv;
+
+// Variant 0 is the direct fallback, then the MFMA tile variants.
+const std::vector<Variant>& variants()
 {
-    hipLaunchKernelGGL(conv_mfma_kernel<C>, grid, dim3(C::kThreads), 0, s, a);
+    static const std::vector<Variant> table = [] {
+        std::vector<Variant> t{Variant{"direct_fp32", 0, 0, 0, 0, 0, 0, 0, nullptr, nullptr, nullptr}};
+        for (auto family : {variants_k3s1, variants_k3s2, variants_k1}) {
+            int n = 0;
+            const Variant* v = family(&n);
+            t.insert(t.end(), v, v + n);
+        }
+        return t;
+    }();
+    return table;
 }
 
-#define MLVC_VARIANT(BM, TH, TW, KH, KW, S, KC)                                                              \
-    Variant{"mfma_bm" #BM "_" #TH "x" #TW "_k" #KH "x" #KW "_s" #S "_kc" #KC, BM, TH, TW, KH, KW, S, KC,        \
-            &launch_mfma<Cfg<BM, TH, TW, KH, KW, S, KC, false, false>>, &launch_mfma<Cfg<BM, TH, TW, KH, KW, S, KC, true, false>>}
-// Two-stage pipeline (vector staging only; the scalar staging path keeps the one-stage kernel).
-#define MLVC_VARIANT_DB(BM, TH, TW, KH, KW, S, KC)                                                           \
-    Variant{"mfma_bm" #BM "_" #TH "x" #TW "_k" #KH "x" #KW "_s" #S "_kc" #KC "_db", BM, TH, TW, KH, KW, S, KC,  \
-            &launch_mfma<Cfg<BM, TH, TW, KH, KW, S, KC, false, false>>, &launch_mfma<Cfg<BM, TH, TW, KH, KW, S, KC, true, true>>}
-
-const Variant kVariants[] = {
-    Variant{"direct_fp32", 0, 0, 0, 0, 0, 0, 0, nullptr, nullptr},
-    // 3x3 stride 1
-    MLVC_VARIANT(32, 4, 64, 3, 3, 1, 16),
-    MLVC_VARIANT(32, 8, 32, 3, 3, 1, 16),
-    MLVC_VARIANT(64, 4, 64, 3, 3, 1, 16),
-    MLVC_VARIANT(64, 8, 32, 3, 3, 1, 16),
-    MLVC_VARIANT(64, 16, 16, 3, 3, 1, 16),
-    MLVC_VARIANT(64, 2, 64, 3, 3, 1, 16),
-    MLVC_VARIANT(64, 4, 32, 3, 3, 1, 16),
-    MLVC_VARIANT(64, 8, 16, 3, 3, 1, 16),
-    MLVC_VARIANT(128, 4, 64, 3, 3, 1, 16),
-    MLVC_VARIANT(128, 8, 32, 3, 3, 1, 16),
-    MLVC_VARIANT(128, 16, 16, 3, 3, 1, 16),
-    MLVC_VARIANT_DB(64, 8, 32, 3, 3, 1, 16),
-    MLVC_VARIANT_DB(32, 8, 32, 3, 3, 1, 16),
-    MLVC_VARIANT_DB(128, 8, 32, 3, 3, 1, 16),
-    MLVC_VARIANT_DB(128, 4, 64, 3, 3, 1, 16),
-    MLVC_VARIANT_DB(64, 4, 64, 3, 3, 1, 16),
-    // 3x3 stride 2
-    MLVC_VARIANT(32, 4, 64, 3, 3, 2, 16),
-    MLVC_VARIANT(64, 2, 64, 3, 3, 2, 16),
-    MLVC_VARIANT(64, 4, 32, 3, 3, 2, 16),
-    MLVC_VARIANT(64, 8, 16, 3, 3, 2, 16),
-    MLVC_VARIANT(128, 2, 64, 3, 3, 2, 16),
-    // 1x1 (flattened pixels unless an unshuffle is fused)
-    MLVC_VARIANT(32, 1, 256, 1, 1, 1, 32),
-    MLVC_VARIANT(64, 1, 256, 1, 1, 1, 32),
-    MLVC_VARIANT(64, 1, 128, 1, 1, 1, 32),
-    MLVC_VARIANT(128, 1, 128, 1, 1, 1, 32),
-    MLVC_VARIANT(64, 2, 64, 1, 1, 1, 32),
-    MLVC_VARIANT(64, 4, 32, 1, 1, 1, 32),
-};
-constexpr int kVariantCount = static_cast<int>(sizeof(kVariants) / sizeof(kVariants[0]));
+int variant_count() { return static_cast<int>(variants().size()); }
 
 int cu_count()
 {
@@ -600,8 +85,8 @@ bool flat_1x1(const mlvc_hip_conv_desc& d)
 
 const Variant& variant_of(const mlvc_hip_conv_desc& d)
 {
-    if (d.variant < 0 || d.variant >= kVariantCount) throw std::runtime_error("conv: invalid variant");
-    return kVariants[d.variant];
+    if (d.variant < 0 || d.variant >= variant_count()) throw std::runtime_error("conv: invalid variant");
+    return variants()[d.variant];
 }
 
 // Geometry and fusion checks (planning and launch); pointers at launch only.
@@ -667,9 +152,9 @@ int mlvc_hip_conv_plan(mlvc_hip_conv_desc* desc)
         const int slots = 2 * cu_count();
         int best = 0;
         double best_cost = 0.0;
-        for (int v = 1; v < kVariantCount; ++v) {
-            if (!eligible(d, kVariants[v])) continue;
-            const Variant& k = kVariants[v];
+        for (int v = 1; v < variant_count(); ++v) {
+            if (!eligible(d, variants()[v])) continue;
+            const Variant& k = variants()[v];
             const long tiles = static_cast<long>((oh + k.th - 1) / k.th) * ((ow + k.tw - 1) / k.tw) *
                                ((d.oc + k.bm - 1) / k.bm) * d.n;
             const long rounds = (tiles + slots - 1) / slots;
@@ -687,15 +172,15 @@ int mlvc_hip_conv_plan(mlvc_hip_conv_desc* desc)
     });
 }
 
-int mlvc_hip_conv_candidates(const mlvc_hip_conv_desc* desc, int* variants, int capacity, int* count)
+int mlvc_hip_conv_candidates(const mlvc_hip_conv_desc* desc, int* out, int capacity, int* count)
 {
     return guard([&] {
         validate(*desc, false);
-        if (!count || (capacity > 0 && !variants)) throw std::runtime_error("conv: null candidate buffer");
+        if (!count || (capacity > 0 && !out)) throw std::runtime_error("conv: null candidate buffer");
         int n = 0;
-        for (int v = 1; v < kVariantCount; ++v)
-            if (eligible(*desc, kVariants[v])) {
-                if (n < capacity) variants[n] = v;
+        for (int v = 1; v < variant_count(); ++v)
+            if (eligible(*desc, variants()[v])) {
+                if (n < capacity) out[n] = v;
                 ++n;
             }
         *count = n;
@@ -704,7 +189,7 @@ int mlvc_hip_conv_candidates(const mlvc_hip_conv_desc* desc, int* variants, int 
 
 const char* mlvc_hip_conv_variant_name(int variant)
 {
-    return variant >= 0 && variant < kVariantCount ? kVariants[variant].name : "invalid";
+    return variant >= 0 && variant < variant_count() ? variants()[variant].name : "invalid";
 }
 
 size_t mlvc_hip_conv_bias_len(const mlvc_hip_conv_desc* desc)
@@ -806,7 +291,12 @@ int mlvc_hip_conv_launch(const mlvc_hip_conv_desc* desc, mlvc_hip_stream s)
             if (nwg > 0x7FFFFFFF) throw std::runtime_error("conv: grid too large");
             a.nwg = static_cast<int>(nwg);
             const dim3 grid(static_cast<unsigned>(a.nwg));
-            (vec ? k.launch_vec : k.launch_scalar)(a, grid, to_stream(s));
+            // SPACE_TO_DEPTH(2) vector staging: 32-byte aligned source rows
+            // and offsets (up to KC/4 channel planes past the end) < 2^31.
+            const std::uint64_t src_plane = static_cast<std::uint64_t>(a.ih) * a.iw * 4 * 2;
+            const bool s2d_vec = k.launch_s2d && a.s2d == 2 && (reinterpret_cast<std::uintptr_t>(d.x) & 15u) == 0 &&
+                                 a.iw % 8 == 0 && (static_cast<std::uint64_t>(d.ic / 4) + k.kc / 4 + 1) * src_plane < (1ull << 31);
+            (s2d_vec ? k.launch_s2d : vec ? k.launch_vec : k.launch_scalar)(a, grid, to_stream(s));
         }
         check(hipGetLastError(), "conv kernel launch");
     });

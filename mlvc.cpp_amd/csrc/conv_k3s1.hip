@@ -1,0 +1,40 @@
+// 3x3 stride-1 tile variants of the MFMA conv kernel (conv_kernel.hpp).
+
+#include "conv_kernel.hpp"
+
+namespace mlvc_hip {
+namespace conv {
+
+namespace {
+const Variant kTable[] = {
+    MLVC_VARIANT_S2D(32, 4, 64, 3, 3, 1, 16),
+    MLVC_VARIANT_S2D(32, 8, 32, 3, 3, 1, 16),
+    MLVC_VARIANT_S2D(64, 4, 64, 3, 3, 1, 16),
+    MLVC_VARIANT_S2D(64, 8, 32, 3, 3, 1, 16),
+    MLVC_VARIANT(64, 16, 16, 3, 3, 1, 16),
+    MLVC_VARIANT(64, 2, 64, 3, 3, 1, 16),
+    MLVC_VARIANT_S2D(64, 4, 32, 3, 3, 1, 16),
+    MLVC_VARIANT_S2D(64, 8, 16, 3, 3, 1, 16),
+    MLVC_VARIANT(128, 4, 64, 3, 3, 1, 16),
+    MLVC_VARIANT(128, 8, 32, 3, 3, 1, 16),
+    MLVC_VARIANT(128, 16, 16, 3, 3, 1, 16),
+    MLVC_VARIANT(32, 8, 32, 3, 3, 1, 32),
+    MLVC_VARIANT(64, 8, 32, 3, 3, 1, 32),
+    MLVC_VARIANT(64, 4, 64, 3, 3, 1, 32),
+    MLVC_VARIANT(64, 8, 16, 3, 3, 1, 32),
+    MLVC_VARIANT_DB(64, 8, 32, 3, 3, 1, 16),
+    MLVC_VARIANT_DB(32, 8, 32, 3, 3, 1, 16),
+    MLVC_VARIANT_DB(128, 8, 32, 3, 3, 1, 16),
+    MLVC_VARIANT_DB(128, 4, 64, 3, 3, 1, 16),
+    MLVC_VARIANT_DB(64, 4, 64, 3, 3, 1, 16),
+};
+}  // namespace
+
+const Variant* variants_k3s1(int* n)
+{
+    *n = static_cast<int>(sizeof(kTable) / sizeof(kTable[0]));
+    return kTable;
+}
+
+}  // namespace conv
+}  // namespace mlvc_hip

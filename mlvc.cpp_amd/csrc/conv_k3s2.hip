@@ -1,0 +1,27 @@
+// 3x3 stride-2 tile variants of the MFMA conv kernel (conv_kernel.hpp).
+
+#include "conv_kernel.hpp"
+
+namespace mlvc_hip {
+namespace conv {
+
+namespace {
+const Variant kTable[] = {
+    MLVC_VARIANT(32, 4, 64, 3, 3, 2, 16),
+    MLVC_VARIANT(64, 2, 64, 3, 3, 2, 16),
+    MLVC_VARIANT(64, 4, 32, 3, 3, 2, 16),
+    MLVC_VARIANT(64, 8, 16, 3, 3, 2, 16),
+    MLVC_VARIANT(128, 2, 64, 3, 3, 2, 16),
+    MLVC_VARIANT(64, 4, 32, 3, 3, 2, 32),
+    MLVC_VARIANT(64, 8, 16, 3, 3, 2, 32),
+};
+}  // namespace
+
+const Variant* variants_k3s2(int* n)
+{
+    *n = static_cast<int>(sizeof(kTable) / sizeof(kTable[0]));
+    return kTable;
+}
+
+}  // namespace conv
+}  // namespace mlvc_hip

@@ -85,24 +85,6 @@ __device__ __forceinline__ void lds_barrier()
 __device__ __forceinline__ float lo_h(std::uint32_t v) { return h2f(static_cast<std::uint16_t>(v & 0xFFFFu)); }
 __device__ __forceinline__ float hi_h(std::uint32_t v) { return h2f(static_cast<std::uint16_t>(v >> 16)); }
 
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
-
-// Two FP32 accumulators -> packed FP16 pair after LeakyReLU on the rounded
-// values (see leaky_f16): max form when 0 <= alpha <= 1, select otherwise.
-__device__ __forceinline__ std::uint32_t leaky_pair(float a0, float a1, float alpha, bool max_form)
-{
-    const half2_t h = {static_cast<_Float16>(a0), static_cast<_Float16>(a1)};
-    if (max_form) {
-        const half2_t p = {static_cast<_Float16>(mul_f32(static_cast<float>(h[0]), alpha)),
-                           static_cast<_Float16>(mul_f32(static_cast<float>(h[1]), alpha))};
-        return __builtin_bit_cast(std::uint32_t, __builtin_elementwise_max(h, p));
-    }
-    const std::uint16_t h0 = __builtin_bit_cast(std::uint16_t, h[0]), h1 = __builtin_bit_cast(std::uint16_t, h[1]);
-    const std::uint16_t r0 = h2f(h0) < 0.0f ? leaky_f16(h2f(h0), alpha) : h0;
-    const std::uint16_t r1 = h2f(h1) < 0.0f ? leaky_f16(h2f(h1), alpha) : h1;
-    return r0 | (static_cast<std::uint32_t>(r1) << 16);
-}
-
 template <int C, int E>
 __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArgs a)
 {

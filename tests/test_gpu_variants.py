@@ -32,6 +32,8 @@ CASES = [
     ("ragged_s1", 1, 72, 13, 27, 96, 3, 1, 1, dict(epilogue="residual")),
     ("ragged_s2", 1, 40, 11, 26, 72, 3, 2, 1, dict()),
     ("ragged_1x1", 2, 48, 7, 13, 80, 1, 1, 0, dict(epilogue="residual")),
+    ("d2s3_fallback", 1, 32, 9, 12, 18, 3, 1, 1, dict(epilogue="lrelu", d2s=3)),
+    ("residual_d2s", 1, 64, 6, 16, 64, 3, 1, 1, dict(epilogue="residual", d2s=2)),
 ]
 
 
