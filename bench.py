@@ -142,6 +142,8 @@ def main() -> int:
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--api-frames", type=int, default=30,
+                    help="frames timed through run() (host frame in, host reconstruction out)")
     ap.add_argument("--pmc-pass", default=None, metavar="I,J,...",
                     help="counter-collection mode for rocprofv3 --pmc: run the calibration stream kernel, then "
                          "launches I,J,... of the graph, PMC_REPS times each; no timing, no JSON line")
@@ -198,6 +200,15 @@ def main() -> int:
         log(f"sum of isolated kernel times {sum_kernel_ms:.3f} ms/frame; graph replay {gpu_ms / args.steps:.3f} ms/frame "
             f"(events), {wall * 1e3 / args.steps:.3f} ms/frame (wall); {conv_flops / 1e9:.1f} GFLOP and "
             f"{frame_bytes / 1e6:.0f} MB algorithmic per frame")
+        # Through the plain run() API instead: the frame is copied in from
+        # host memory and the reconstruction copied back every frame (pinned
+        # staging, PCIe). Reported beside the value, never as it.
+        x0 = mlvc_hip.synth_input(CONFIG, 0, 0, shape)
+        gpu.run([x0])
+        t1 = time.perf_counter()
+        for _ in range(args.api_frames):
+            gpu.run([x0])
+        api_fps = args.api_frames / (time.perf_counter() - t1)
         base = None
         if not args.no_cpu_baseline and rank == 0:
             base = cpu_baseline(d, bindings, shape, args.cpu_seconds)
@@ -225,6 +236,7 @@ def main() -> int:
         "conv_tflops": conv_tflops,
         "conv_mfma_peak_frac": conv_tflops / PEAK_MFMA_TFLOPS,
         "gpu_event_ms_per_step": gpu_ms / args.steps,
+        "run_api_frames_per_s": api_fps,
         "roofline": roof,
         "cpu_baseline": base,
     }
