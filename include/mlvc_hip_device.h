@@ -152,6 +152,42 @@ size_t mlvc_hip_dwblock_packed_bytes(int m, int k);
 int mlvc_hip_dwblock_pack(const uint16_t* w_mk, int m, int k, void* dst_host);
 int mlvc_hip_dwblock_launch(const mlvc_hip_dwblock_desc* desc, mlvc_hip_stream s);
 
+/* ---- fused conv pair: 3x3 conv -> channel CONCAT -> 1x1 conv ----
+ * y = epi_b(fp16(Wb [t ; r] + bb)),  t = epi_a(fp16(Wa * x + ba))
+ * with t never leaving the chip: one kernel for what the reference runs as a
+ * spatial conv (spatial_conv.cu / cutlass.cu fprop), a channel concat
+ * (tensor_ops.cu concat copy) and a 1x1 conv (pointwise_conv.cu), or the
+ * CPU plan's two GEMM steps (execution_plan.cpp); rounding points and K
+ * order are those of the unfused kernels, so the results are identical.
+ * x: [n, ica, h, w], or with in_s2d_block == 2 the SPACE_TO_DEPTH source
+ * [n, ica/4, 2h, 2w]; r: [n, cr, h, w]; y: [n, ocb, h, w]. Wa is OIHW
+ * [oca, ica, 3, 3] (stride 1, pad 1), Wb is [ocb, oca + cr]; both packed
+ * by mlvc_hip_convpair_pack. Biases are FP32. */
+typedef struct mlvc_hip_convpair_desc {
+    int n, ica, h, w, in_s2d_block;
+    int oca, cr, ocb;
+    const void* x;
+    const void* r;
+    const void* wa;
+    const float* ba;
+    int epi_a;
+    float alpha_a;
+    const void* wb;
+    const float* bb;
+    int epi_b;
+    float alpha_b;
+    void* y;
+} mlvc_hip_convpair_desc;
+
+/* 1 when the geometry has a fused kernel (oca = cr = ocb = 64, w % 8 == 0,
+ * epilogues none or LeakyReLU), else 0. */
+int mlvc_hip_convpair_supported(const mlvc_hip_convpair_desc* desc);
+size_t mlvc_hip_convpair_packed_a_bytes(const mlvc_hip_convpair_desc* desc);
+size_t mlvc_hip_convpair_packed_b_bytes(const mlvc_hip_convpair_desc* desc);
+int mlvc_hip_convpair_pack(const mlvc_hip_convpair_desc* desc, const uint16_t* wa_oihw, const uint16_t* wb_oi,
+                           void* dst_a_host, void* dst_b_host);
+int mlvc_hip_convpair_launch(const mlvc_hip_convpair_desc* desc, mlvc_hip_stream s);
+
 /* ---- pixel layout, CRD (tensor_ops.cu:62-116, mode 1) ----
  * DEPTH_TO_SPACE: in [n, c*b*b, h, w] -> out [n, c, h*b, w*b].
  * SPACE_TO_DEPTH: in [n, c, h, w] -> out [n, c*b*b, h/b, w/b]. */

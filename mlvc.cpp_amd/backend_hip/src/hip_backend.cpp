@@ -107,11 +107,12 @@ struct HostMem {
 };
 
 struct Launch {
-    enum Kind { kConv, kDepthwise, kDwBlock, kLeaky, kAdd, kD2S, kS2D, kConcat } kind = kConv;
+    enum Kind { kConv, kDepthwise, kDwBlock, kPair, kLeaky, kAdd, kD2S, kS2D, kConcat } kind = kConv;
     std::string name, kind_name;
     TensorId x = 0, x2 = 0, res = 0, y = 0;  // tensors read (x, x2, res) and written (y)
     mlvc_hip_conv_desc conv{};
     mlvc_hip_dwblock_desc blk{};
+    mlvc_hip_convpair_desc pair{};
     DeviceMem packed, bias, packed2, bias2, packed3, bias3;
     std::vector<std::uint16_t> w_oihw;  // conv weights kept for re-packing after tuning
     std::vector<float> bias_oc;         // conv bias, unpadded
@@ -362,7 +363,8 @@ private:
             switch (n.op) {
             case Op::CONV:
                 if (n.conv().groups == 1) {
-                    lower_conv(*L, n, producer, folded, done, internal_single, first_consumer, fuse);
+                    if (!(fuse && lower_pair(*L, n, producer, folded, done, internal_single, first_consumer)))
+                        lower_conv(*L, n, producer, folded, done, internal_single, first_consumer, fuse);
                 } else if (!(fuse && lower_dwblock(*L, n, done, internal_single, first_consumer))) {
                     lower_depthwise(*L, n);
                 }
@@ -576,6 +578,107 @@ private:
         L.flops = 2.0 * d.n * d.oc * d.oh * d.ow * static_cast<double>(d.ic) * d.kh * d.kw;
         L.bytes = 2.0 * (static_cast<double>(d.n) * d.ic * d.ih * d.iw + static_cast<double>(d.oc) * d.ic * d.kh * d.kw + d.oc +
                          static_cast<double>(d.n) * d.oc * d.oh * d.ow * (L.res ? 2.0 : 1.0));
+    }
+
+    // 3x3 s1 p1 conv (input plain or a folded SPACE_TO_DEPTH(2)) [-> LEAKY_RELU]
+    // -> CONCAT(t, r) -> 1x1 conv [-> LEAKY_RELU], every intermediate with
+    // one consumer and not a graph output: one fused launch, t stays on chip.
+    template <typename SingleFn>
+    bool lower_pair(Launch& L, const aot::Node& n, std::map<TensorId, std::size_t>& producer, const std::vector<bool>& folded,
+                    std::vector<bool>& done, SingleFn internal_single, std::map<TensorId, std::size_t>& first_consumer)
+    {
+        const auto& ns = nodes();
+        const auto& ws = desc(n.inputs[1]).shape;
+        if (ws.size() != 4 || ws[2] != 3 || ws[3] != 3 || n.conv().strides != std::array<int, 2>{1, 1} ||
+            n.conv().pads != std::array<int, 4>{1, 1, 1, 1} || !is_weight(n.inputs[1]))
+            return false;
+        TensorId x = n.inputs[0];
+        int s2d = 0;
+        if (producer.count(x) && folded[producer[x]]) {
+            const aot::Node& pn = ns[producer[x]];
+            if (pn.op != Op::SPACE_TO_DEPTH || pn.block_size() != 2) return false;
+            x = pn.inputs[0];
+            s2d = 2;
+        }
+        auto next = [&](TensorId id) -> const aot::Node* {
+            if (!internal_single(id)) return nullptr;
+            return &ns[first_consumer[id]];
+        };
+        TensorId t = n.outputs[0];
+        const aot::Node* act_a = nullptr;
+        const aot::Node* c = next(t);
+        if (c && c->op == Op::LEAKY_RELU && c->inputs[0] == t) {
+            act_a = c;
+            t = c->outputs[0];
+            c = next(t);
+        }
+        if (!c || c->op != Op::CONCAT || c->inputs.size() != 2 || c->inputs[0] != t) return false;
+        const int axis = c->axis() < 0 ? c->axis() + 4 : c->axis();
+        const TensorId r = c->inputs[1];
+        if (axis != 1 || is_weight(r) || desc(r).dtype != aot::DataType::FP16 || desc(r).shape.size() != 4) return false;
+        const aot::Node* m = next(c->outputs[0]);
+        if (!m || m->op != Op::CONV || m->inputs[0] != c->outputs[0] || m->conv().groups != 1 || !is_weight(m->inputs[1]))
+            return false;
+        const auto& wm = desc(m->inputs[1]).shape;
+        if (wm.size() != 4 || wm[2] != 1 || wm[3] != 1 || m->conv().strides != std::array<int, 2>{1, 1} ||
+            m->conv().pads != std::array<int, 4>{0, 0, 0, 0})
+            return false;
+        TensorId y = m->outputs[0];
+        const aot::Node* act_b = nullptr;
+        if (const aot::Node* nb = next(y); nb && nb->op == Op::LEAKY_RELU && nb->inputs[0] == y) {
+            act_b = nb;
+            y = nb->outputs[0];
+        }
+        const auto& ts = desc(n.outputs[0]).shape;
+        const auto& rs = desc(r).shape;
+        const auto& ys = desc(y).shape;
+        mlvc_hip_convpair_desc& d = L.pair;
+        d = mlvc_hip_convpair_desc{};
+        d.n = static_cast<int>(ts[0]);
+        d.ica = static_cast<int>(ws[1]);
+        d.h = static_cast<int>(ts[2]);
+        d.w = static_cast<int>(ts[3]);
+        d.in_s2d_block = s2d;
+        d.oca = static_cast<int>(ts[1]);
+        d.cr = static_cast<int>(rs[1]);
+        d.ocb = static_cast<int>(wm[0]);
+        d.epi_a = act_a ? MLVC_EPI_LEAKY_RELU : MLVC_EPI_NONE;
+        d.alpha_a = act_a ? act_a->alpha() : 0.0F;
+        d.epi_b = act_b ? MLVC_EPI_LEAKY_RELU : MLVC_EPI_NONE;
+        d.alpha_b = act_b ? act_b->alpha() : 0.0F;
+        if (rs[0] != ts[0] || rs[2] != ts[2] || rs[3] != ts[3] || wm[1] != d.oca + d.cr || ys[1] != d.ocb ||
+            ys[2] != ts[2] || ys[3] != ts[3] || !mlvc_hip_convpair_supported(&d))
+            return false;
+        L.kind = Launch::kPair;
+        L.kind_name = std::string("convpair_3x3_1x1") + (s2d ? "+s2d" : "") + "+concat";
+        L.name = desc(y).name;
+        L.x = x;
+        L.x2 = r;
+        L.y = y;
+        const auto wa = weight_fp16(n.inputs[1]);
+        const auto wb = weight_fp16(m->inputs[1]);
+        std::vector<std::uint8_t> pa(mlvc_hip_convpair_packed_a_bytes(&d)), pb(mlvc_hip_convpair_packed_b_bytes(&d));
+        hip_check(mlvc_hip_convpair_pack(&d, wa.data(), wb.data(), pa.data(), pb.data()), "pair weight packing");
+        auto upload = [&](DeviceMem& dst, std::vector<std::uint8_t> bytes) {
+            dst = DeviceMem(bytes.size());
+            pending_uploads_.push_back({dst.ptr, std::move(bytes)});
+        };
+        auto f32_bytes = [](const std::vector<float>& v) {
+            std::vector<std::uint8_t> b(v.size() * 4);
+            std::memcpy(b.data(), v.data(), b.size());
+            return b;
+        };
+        upload(L.packed, std::move(pa));
+        upload(L.bias, f32_bytes(bias_f32(n, d.oca, static_cast<std::size_t>(d.oca))));
+        upload(L.packed2, std::move(pb));
+        upload(L.bias2, f32_bytes(bias_f32(*m, d.ocb, static_cast<std::size_t>(d.ocb))));
+        for (const aot::Node* q : {act_a, c, m, act_b})
+            if (q) done[q->index] = true;
+        const double px = static_cast<double>(d.n) * d.h * d.w;
+        L.flops = 2.0 * px * d.oca * d.ica * 9 + 2.0 * px * d.ocb * (d.oca + d.cr);
+        L.bytes = 2.0 * (px * d.ica + px * d.cr + px * d.ocb + 9.0 * d.oca * d.ica + static_cast<double>(d.ocb) * (d.oca + d.cr)) +
+                  4.0 * (d.oca + d.ocb);
+        return true;
     }
 
     // DW3x3 s1 p1 -> 1x1 C->E -> LEAKY_RELU -> 1x1 E->C -> ADD(block input),
@@ -823,6 +926,18 @@ private:
             d.w2 = l.packed3.ptr;
             d.b2 = static_cast<const float*>(l.bias3.ptr);
             hip_check(mlvc_hip_dwblock_launch(&d, stream_), "dwblock launch");
+            break;
+        }
+        case Launch::kPair: {
+            mlvc_hip_convpair_desc d = l.pair;
+            d.x = ptr(l.x, parity);
+            d.r = ptr(l.x2, parity);
+            d.y = ptr(l.y, parity);
+            d.wa = l.packed.ptr;
+            d.ba = static_cast<const float*>(l.bias.ptr);
+            d.wb = l.packed2.ptr;
+            d.bb = static_cast<const float*>(l.bias2.ptr);
+            hip_check(mlvc_hip_convpair_launch(&d, stream_), "convpair launch");
             break;
         }
         case Launch::kLeaky:

@@ -17,6 +17,12 @@ const Variant kTable[] = {
     MLVC_VARIANT_S2D(64, 8, 16, 3, 3, 1, 16),
     MLVC_VARIANT(128, 4, 64, 3, 3, 1, 16),
     MLVC_VARIANT(128, 8, 32, 3, 3, 1, 16),
+    MLVC_VARIANT_W(128, 16, 32, 3, 3, 1, 16, 1, 8),
+    MLVC_VARIANT_W(128, 8, 64, 3, 3, 1, 16, 1, 8),
+    MLVC_VARIANT_W(256, 8, 32, 3, 3, 1, 16, 2, 4),
+    MLVC_VARIANT_W(256, 4, 64, 3, 3, 1, 16, 2, 4),
+    MLVC_VARIANT_W(64, 16, 32, 3, 3, 1, 16, 1, 8),
+    MLVC_VARIANT_W(128, 16, 16, 3, 3, 1, 16, 2, 4),
     MLVC_VARIANT(128, 16, 16, 3, 3, 1, 16),
     MLVC_VARIANT(32, 8, 32, 3, 3, 1, 32),
     MLVC_VARIANT(64, 8, 32, 3, 3, 1, 32),

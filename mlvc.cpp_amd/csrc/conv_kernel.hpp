@@ -145,7 +145,7 @@ __device__ __forceinline__ void store_output(const ConvArgs& a, std::uint16_t h,
     }
 }
 
-template <int BM_, int TH_, int TW_, int KH_, int KW_, int S_, int KC_, int STG_, bool DB_>
+template <int BM_, int TH_, int TW_, int KH_, int KW_, int S_, int KC_, int STG_, bool DB_, int WM_ = 1, int WNW_ = 4>
 struct Cfg {
     static constexpr int BM = BM_, TH = TH_, TW = TW_, KH = KH_, KW = KW_, S = S_, KC = KC_;
     // Input staging: 0 = per-pixel loads through the SPACE_TO_DEPTH / CONCAT
@@ -159,12 +159,16 @@ struct Cfg {
     // is multiplied, one barrier per chunk. Otherwise one stage, weights
     // staged through registers, two barriers per chunk, half the LDS.
     static constexpr bool DB = DB_;
-    static constexpr int kThreads = 256;
+    // Waves: WM along the output channels x WNW along the pixels; each wave
+    // computes (BM / WM) channels x (BN / WNW) pixels.
+    static constexpr int WM = WM_, WNW = WNW_, WAVES = WM_ * WNW_;
+    static constexpr int kThreads = 64 * WAVES;
     static constexpr int BN = TH * TW;
     static constexpr int TAPS = KH * KW;
     static constexpr int KS = KC / 16;  // 16-deep MFMA K steps per tap
-    static constexpr int MT = BM / 32;
-    static constexpr int WN = BN / 4;
+    static constexpr int MTT = BM / 32;  // m-tiles of the workgroup (weight layout)
+    static constexpr int MT = MTT / WM;  // m-tiles per wave
+    static constexpr int WN = BN / WNW;  // pixels per wave
     static constexpr int NT = WN / 32;
     static constexpr int IH_T = (TH - 1) * S + KH;
     static constexpr int IW_T = (TW - 1) * S + KW;
@@ -185,7 +189,7 @@ struct Cfg {
     static constexpr int UNITS2_PER_T = (UNITS2 + kThreads - 1) / kThreads;
     static constexpr int IN_PIX = IH_T * IW_T;
     static constexpr int PIX_PER_T = (IN_PIX + kThreads - 1) / kThreads;
-    static constexpr int W_LDS = TAPS * KS * MT * 64 * 8;  // halves per chunk
+    static constexpr int W_LDS = TAPS * KS * MTT * 64 * 8;  // halves per chunk
     static constexpr int W_VEC = W_LDS / 8;
     static constexpr int W_PER_T = (W_VEC + kThreads - 1) / kThreads;
     static constexpr int EPI_ROW = BN + 8;  // output staging row (one channel), halves
@@ -193,7 +197,9 @@ struct Cfg {
     static constexpr int STAGE = IN_LDS + W_LDS;
     static constexpr int W_INST = W_VEC / 64;  // 1 KB LDS DMA instructions per chunk
     static constexpr int LDS = (DB ? 2 * STAGE : STAGE) > EPI_LDS ? (DB ? 2 * STAGE : STAGE) : EPI_LDS;
-    static_assert(BM % 32 == 0 && WN % 32 == 0 && KC % 16 == 0 && TW % 8 == 0 && W_VEC % 64 == 0, "tile shape");
+    static_assert(BM % 32 == 0 && MTT % WM == 0 && WN % 32 == 0 && BN % WNW == 0 && KC % 16 == 0 && TW % 8 == 0 &&
+                      W_VEC % 64 == 0,
+                  "tile shape");
     static_assert(STAGE % 8 == 0, "stage alignment");
     static_assert(LDS * 2 <= 160 * 1024, "LDS budget");
 
@@ -208,13 +214,15 @@ __device__ __forceinline__ std::uint32_t pack_half(std::uint32_t lo_word, std::u
 }
 
 template <class C>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void conv_mfma_kernel(ConvArgs a)
+__global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(2))) void conv_mfma_kernel(ConvArgs a)
 {
     __shared__ __attribute__((aligned(16))) std::uint16_t lds[C::LDS];
     auto lds_in = [&](int stage) { return lds + stage * C::STAGE; };
     auto lds_w = [&](int stage) { return lds + stage * C::STAGE + C::IN_LDS; };
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / C::WNW, wn = wave % C::WNW;  // this wave's channel and pixel slices
+    const int mt0 = wm * C::MT;                        // first m-tile of this wave
     // Logical work item: output-channel block fastest, then pixel tiles in
     // row-major order, then images; each XCD runs a contiguous range of them.
     const int item = xcd_order(blockIdx.x, a.nwg);
@@ -230,7 +238,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void c
     for (int mt = 0; mt < C::MT; ++mt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const float bv = a.bias[ocb * C::BM + mt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)];
+            const float bv = a.bias[ocb * C::BM + (mt0 + mt) * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)];
 #pragma unroll
             for (int nt = 0; nt < C::NT; ++nt) acc[mt][nt][r] = bv;
         }
@@ -336,8 +344,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void c
             // instruction, lane l of instruction j moving vector 64*j + l.
             u32x4* dst = reinterpret_cast<u32x4*>(lds_w(stage));
 #pragma unroll
-            for (int i = 0; i < (C::W_INST + 3) / 4; ++i) {
-                const int j = wave + 4 * i;
+            for (int i = 0; i < (C::W_INST + C::WAVES - 1) / C::WAVES; ++i) {
+                const int j = wave + C::WAVES * i;
                 if (j < C::W_INST)
                     __builtin_amdgcn_global_load_lds(ws + j * 64 + lane,
                                                      (__attribute__((address_space(3))) void*)(dst + j * 64), 16, 0, 0);
@@ -416,7 +424,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void c
     int pyi[C::NT], pxi[C::NT];
 #pragma unroll
     for (int nt = 0; nt < C::NT; ++nt) {
-        const int p = wave * C::WN + nt * 32 + (lane & 31);
+        const int p = wn * C::WN + nt * 32 + (lane & 31);
         pyi[nt] = (p / C::TW) * C::S;
         pxi[nt] = (p % C::TW) * C::S + col_off;
     }
@@ -436,7 +444,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void c
                 half8 av[C::MT], bv[C::NT];
 #pragma unroll
                 for (int mt = 0; mt < C::MT; ++mt)
-                    av[mt] = *reinterpret_cast<const half8*>(&w_s[(((tap * C::KS + ks) * C::MT + mt) * 64 + lane) * 8]);
+                    av[mt] = *reinterpret_cast<const half8*>(&w_s[(((tap * C::KS + ks) * C::MTT + mt0 + mt) * 64 + lane) * 8]);
 #pragma unroll
                 for (int nt = 0; nt < C::NT; ++nt)
                     bv[nt] = *reinterpret_cast<const half8*>(&in_s[C::at(pyi[nt] + ky, pxi[nt] + kx) + koff + ks * 16]);
@@ -482,8 +490,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void c
     }
 
     // Epilogue. Lane l of accumulator (mt, nt) holds output channels oc0 + i,
-    // oc0 = ocb*BM + mt*32 + 8j + 4*(l/32) (j, i = 0..3), of tile pixel
-    // wave*WN + nt*32 + l%32: 32 lanes hold 32 consecutive pixels of each
+    // oc0 = ocb*BM + (mt0 + mt)*32 + 8j + 4*(l/32) (j, i = 0..3), of tile pixel
+    // wn*WN + nt*32 + l%32: 32 lanes hold 32 consecutive pixels of each
     // channel. Values are rounded to FP16 first and the epilogue acts on the
     // rounded value. With a fused DEPTH_TO_SPACE(2) the 4 channels of a lane
     // are the (dy, dx) block of output channel oc0/4, so the stores go
@@ -496,12 +504,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void c
         for (int mt = 0; mt < C::MT; ++mt)
 #pragma unroll
             for (int nt = 0; nt < C::NT; ++nt) {
-                const int p = wave * C::WN + nt * 32 + (lane & 31);
+                const int p = wn * C::WN + nt * 32 + (lane & 31);
                 const int oy = ty0 + (p / C::TW), ox = tx0 + (p % C::TW);
                 const bool inside = oy < a.oh && ox < a.ow;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    const int oc0 = ocb * C::BM + mt * 32 + 8 * j + 4 * (lane >> 5);
+                    const int oc0 = ocb * C::BM + (mt0 + mt) * 32 + 8 * j + 4 * (lane >> 5);
                     const float v[4] = {acc[mt][nt][4 * j], acc[mt][nt][4 * j + 1], acc[mt][nt][4 * j + 2],
                                         acc[mt][nt][4 * j + 3]};
                     std::uint32_t h01, h23;
@@ -540,8 +548,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void c
         for (int nt = 0; nt < C::NT; ++nt)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-                const int ocl = mt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-                const int pl = wave * C::WN + nt * 32 + (lane & 31);
+                const int ocl = (mt0 + mt) * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                const int pl = wn * C::WN + nt * 32 + (lane & 31);
                 lds[ocl * C::EPI_ROW + pl] = f2h(acc[mt][nt][r]);
             }
     __syncthreads();
@@ -604,6 +612,11 @@ void launch_mfma(const ConvArgs& a, dim3 grid, hipStream_t s)
 #define MLVC_VARIANT(BM, TH, TW, KH, KW, S, KC)                                                              \
     Variant{"mfma_bm" #BM "_" #TH "x" #TW "_k" #KH "x" #KW "_s" #S "_kc" #KC, BM, TH, TW, KH, KW, S, KC,        \
             &launch_mfma<Cfg<BM, TH, TW, KH, KW, S, KC, 0, false>>, &launch_mfma<Cfg<BM, TH, TW, KH, KW, S, KC, 1, false>>, nullptr}
+// 8-wave (or other) workgroups: WM waves along the channels x WNW along the pixels.
+#define MLVC_VARIANT_W(BM, TH, TW, KH, KW, S, KC, WM, WNW)                                                      \
+    Variant{"mfma_bm" #BM "_" #TH "x" #TW "_k" #KH "x" #KW "_s" #S "_kc" #KC "_w" #WM "x" #WNW, BM, TH, TW, KH, KW, S, \
+            KC, &launch_mfma<Cfg<BM, TH, TW, KH, KW, S, KC, 0, false, WM, WNW>>,                                      \
+            &launch_mfma<Cfg<BM, TH, TW, KH, KW, S, KC, 1, false, WM, WNW>>, nullptr}
 // With SPACE_TO_DEPTH(2) vector staging.
 #define MLVC_VARIANT_S2D(BM, TH, TW, KH, KW, S, KC)                                                          \
     Variant{"mfma_bm" #BM "_" #TH "x" #TW "_k" #KH "x" #KW "_s" #S "_kc" #KC, BM, TH, TW, KH, KW, S, KC,        \

@@ -139,3 +139,47 @@ def test_standalone_layout_and_eltwise(tmp_path, rng):
     assert kinds == ["add", "leaky_relu", "space_to_depth", "depth_to_space", "concat"], kinds
     for i, (gg, ww) in enumerate(zip(got, want)):
         assert (gg == ww).all(), f"output {i} differs"  # one rounding per op on both sides
+
+
+@pytest.mark.parametrize("s2d,ica,h,w,acts", [(2, 12, 14, 40, (True, True)), (0, 16, 9, 24, (True, False)),
+                                              (0, 40, 6, 16, (False, True)), (2, 24, 5, 8, (True, True))])
+def test_fused_conv_pair(tmp_path, monkeypatch, s2d, ica, h, w, acts):
+    """3x3 conv [+LeakyReLU] -> CONCAT(t, r) -> 1x1 [+LeakyReLU] runs as one
+    launch, matches the oracle and equals the unfused schedule bit for bit."""
+    rng = np.random.default_rng(ica + h)
+    g = graphs.Graph()
+    if s2d:
+        x0 = g.input("x", [1, ica // 4, 2 * h, 2 * w])
+        x = g.pixel("SPACE_TO_DEPTH", "xs", x0, 2)
+    else:
+        x = g.input("x", [1, ica, h, w])
+    r = g.input("r", [1, 64, h, w])
+    wa = g.weight_fp16("wa", rng.normal(0, 1 / np.sqrt(9 * ica), (64, ica, 3, 3)))
+    ba = g.weight_fp16("ba", rng.normal(0, 0.1, (64,)))
+    t = g.conv("t", x, wa, ba, (1, 1), (1, 1, 1, 1))
+    if acts[0]:
+        t = g.leaky_relu("ta", t, 0.1)
+    c = g.concat("cat", [t, r], 1)
+    wb = g.weight_fp16("wb", rng.normal(0, 1 / np.sqrt(128), (64, 128, 1, 1)))
+    bb = g.weight_fp16("bb", rng.normal(0, 0.1, (64,)))
+    y = g.conv("y", c, wb, bb)
+    if acts[1]:
+        y = g.leaky_relu("ya", y, 0.2)
+    g.output(y)
+    g.write(tmp_path, "m")
+    ins = [graphs.half(rng.uniform(-1, 1, s)) for s in ([1, ica // 4, 2 * h, 2 * w] if s2d else [1, ica, h, w],
+                                                        [1, 64, h, w])]
+    want = mlvc_oracle.OraclePlan(tmp_path, "m").run(ins)[0]
+    fused = mlvc_hip.Backend(tmp_path, "hip")
+    fused.load("m")
+    kinds = [l["kind"] for l in fused.launches()]
+    assert len(kinds) == 1 and kinds[0].startswith("convpair"), kinds
+    got = fused.run(ins)[0]
+    fused.close()
+    assert_parity(got, want, f"conv pair s2d={s2d} ica={ica} {h}x{w}")
+    monkeypatch.setenv("MLVC_HIP_DISABLE_FUSION", "1")
+    plain = mlvc_hip.Backend(tmp_path, "hip")
+    plain.load("m")
+    ref = plain.run(ins)[0]
+    plain.close()
+    assert (got == ref).all()
