@@ -7,6 +7,9 @@ namespace conv {
 
 namespace {
 const Variant kTable[] = {
+    MLVC_VARIANT_OCC(32, 4, 64, 3, 3, 1, 16, 4),
+    MLVC_VARIANT_OCC(32, 8, 32, 3, 3, 1, 16, 4),
+    MLVC_VARIANT_OCC(64, 4, 32, 3, 3, 1, 16, 4),
     MLVC_VARIANT_S2D(32, 4, 64, 3, 3, 1, 16),
     MLVC_VARIANT_S2D(32, 8, 32, 3, 3, 1, 16),
     MLVC_VARIANT_S2D(64, 4, 64, 3, 3, 1, 16),

@@ -7,6 +7,10 @@ namespace conv {
 
 namespace {
 const Variant kTable[] = {
+    MLVC_VARIANT_OCC(64, 4, 32, 3, 3, 2, 16, 4),
+    MLVC_VARIANT_OCC(64, 8, 16, 3, 3, 2, 16, 4),
+    MLVC_VARIANT_OCC(64, 2, 64, 3, 3, 2, 16, 4),
+    MLVC_VARIANT_OCC(32, 4, 64, 3, 3, 2, 16, 4),
     MLVC_VARIANT(32, 4, 64, 3, 3, 2, 16),
     MLVC_VARIANT(64, 2, 64, 3, 3, 2, 16),
     MLVC_VARIANT(64, 4, 32, 3, 3, 2, 16),

@@ -145,7 +145,8 @@ __device__ __forceinline__ void store_output(const ConvArgs& a, std::uint16_t h,
     }
 }
 
-template <int BM_, int TH_, int TW_, int KH_, int KW_, int S_, int KC_, int STG_, bool DB_, int WM_ = 1, int WNW_ = 4>
+template <int BM_, int TH_, int TW_, int KH_, int KW_, int S_, int KC_, int STG_, bool DB_, int WM_ = 1, int WNW_ = 4,
+          int OCC_ = 2>
 struct Cfg {
     static constexpr int BM = BM_, TH = TH_, TW = TW_, KH = KH_, KW = KW_, S = S_, KC = KC_;
     // Input staging: 0 = per-pixel loads through the SPACE_TO_DEPTH / CONCAT
@@ -162,6 +163,10 @@ struct Cfg {
     // Waves: WM along the output channels x WNW along the pixels; each wave
     // computes (BM / WM) channels x (BN / WNW) pixels.
     static constexpr int WM = WM_, WNW = WNW_, WAVES = WM_ * WNW_;
+    // Register budget: at least OCC waves per SIMD (2 leaves up to 256
+    // registers for the large tiles; short-K layers want more waves to hide
+    // their per-tile load latency).
+    static constexpr int OCC = OCC_;
     static constexpr int kThreads = 64 * WAVES;
     static constexpr int BN = TH * TW;
     static constexpr int TAPS = KH * KW;
@@ -214,7 +219,7 @@ __device__ __forceinline__ std::uint32_t pack_half(std::uint32_t lo_word, std::u
 }
 
 template <class C>
-__global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(2))) void conv_mfma_kernel(ConvArgs a)
+__global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::OCC))) void conv_mfma_kernel(ConvArgs a)
 {
     __shared__ __attribute__((aligned(16))) std::uint16_t lds[C::LDS];
     auto lds_in = [&](int stage) { return lds + stage * C::STAGE; };
@@ -617,6 +622,11 @@ void launch_mfma(const ConvArgs& a, dim3 grid, hipStream_t s)
     Variant{"mfma_bm" #BM "_" #TH "x" #TW "_k" #KH "x" #KW "_s" #S "_kc" #KC "_w" #WM "x" #WNW, BM, TH, TW, KH, KW, S, \
             KC, &launch_mfma<Cfg<BM, TH, TW, KH, KW, S, KC, 0, false, WM, WNW>>,                                      \
             &launch_mfma<Cfg<BM, TH, TW, KH, KW, S, KC, 1, false, WM, WNW>>, nullptr}
+// Higher-occupancy build (register budget for OCC waves per SIMD).
+#define MLVC_VARIANT_OCC(BM, TH, TW, KH, KW, S, KC, OCC)                                                          \
+    Variant{"mfma_bm" #BM "_" #TH "x" #TW "_k" #KH "x" #KW "_s" #S "_kc" #KC "_occ" #OCC, BM, TH, TW, KH, KW, S, KC,  \
+            &launch_mfma<Cfg<BM, TH, TW, KH, KW, S, KC, 0, false, 1, 4, OCC>>,                                      \
+            &launch_mfma<Cfg<BM, TH, TW, KH, KW, S, KC, 1, false, 1, 4, OCC>>, nullptr}
 // With SPACE_TO_DEPTH(2) vector staging.
 #define MLVC_VARIANT_S2D(BM, TH, TW, KH, KW, S, KC)                                                          \
     Variant{"mfma_bm" #BM "_" #TH "x" #TW "_k" #KH "x" #KW "_s" #S "_kc" #KC, BM, TH, TW, KH, KW, S, KC,        \
