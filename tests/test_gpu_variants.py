@@ -34,6 +34,13 @@ CASES = [
     ("ragged_1x1", 2, 48, 7, 13, 80, 1, 1, 0, dict(epilogue="residual")),
     ("d2s3_fallback", 1, 32, 9, 12, 18, 3, 1, 1, dict(epilogue="lrelu", d2s=3)),
     ("residual_d2s", 1, 64, 6, 16, 64, 3, 1, 1, dict(epilogue="residual", d2s=2)),
+    # More tiles than the device holds workgroups at once: each workgroup
+    # walks several tiles (next tile staged under the current one's last
+    # chunk), across output-channel blocks and both images.
+    ("many_tiles_s1", 2, 32, 256, 1024, 64, 3, 1, 1, dict(epilogue="lrelu")),
+    ("many_tiles_d2s", 1, 32, 384, 768, 128, 3, 1, 1, dict(epilogue="lrelu", d2s=2)),
+    ("many_tiles_s2", 2, 24, 600, 1000, 64, 3, 2, 1, dict(epilogue="residual")),
+    ("many_tiles_1x1", 1, 128, 512, 512, 64, 1, 1, 0, dict(concat_ic=64, epilogue="lrelu")),
 ]
 
 
