@@ -46,16 +46,57 @@ int mlvc_backend_io_count(mlvc_backend* backend, int is_output, int* count);
 int mlvc_backend_io_shape(mlvc_backend* backend, int is_output, int index, int64_t* shape4, int* rank);
 /* InferenceBackend::run(inputs) -> outputs (host buffers, sizes implied by
  * the shapes above). */
-int mlvc_backend_run(mlvc_backend* backend, const uint16_t* const* inputs, uint16_t* const* outputs);
+int mlvc_backend_run(mlvc_backend* backend, const void* const* inputs, uint16_t* const* outputs);
+/* Element type of external input/output `index`: 0 FP16, 1 INT32 (control
+ * inputs such as q_index_shifted; outputs are FP16). */
+int mlvc_backend_io_dtype(mlvc_backend* backend, int is_output, int index, int* dtype);
 /* InferenceBackend::reset_state() */
 int mlvc_backend_reset_state(mlvc_backend* backend);
 /* Names of the registered backends, comma-separated (available_backends()). */
 int mlvc_backend_available(char* buf, size_t len);
 
+/* ---- BufferedCodecBackend (backend.hpp:64-96), for backends that have it
+ *      (-1 "backend has no buffered codec I/O" otherwise) ----
+ * configure_codec_io(CodecIoConfig{width, height, model_width, model_height,
+ * pixel_range, FramePadding{left, right, top, bottom, rotated}, slots}); the
+ * graph must be MLVCEncoder or MLVCDecoder with an INT32 [1]
+ * q_index_shifted input and an FP16 [1, 3, model_height, model_width] x
+ * input (encoder) or x_hat output (decoder): backends/cpu/src/
+ * execution_plan.cpp:1386-1486, backends/driver_cubin/src/
+ * cuda_graph_executor.cpp:205-236. */
+int mlvc_backend_configure_codec_io(mlvc_backend* backend, int width, int height, int model_width, int model_height,
+                                    float pixel_range, int pad_left, int pad_right, int pad_top, int pad_bottom,
+                                    int rotated, size_t slots);
+int mlvc_backend_codec_slot_count(mlvc_backend* backend, size_t* count);
+/* encoder_input_yuv(slot): the slot's pinned I420 planes, writable until the
+ * slot is submitted (cuda_graph_executor.cpp:243-259). */
+int mlvc_backend_encoder_input_yuv(mlvc_backend* backend, size_t slot, uint8_t** y, uint8_t** u, uint8_t** v);
+/* submit_encoder(slot, shifted_q): frame upload, conversion, frame graph,
+ * output download, in stream order (cuda_graph_executor.cpp:261-290). */
+int mlvc_backend_submit_encoder(mlvc_backend* backend, size_t slot, int shifted_q);
+/* encoder_outputs(slot)[index] / decoder_inputs(slot)[index]: pinned host
+ * bytes of the external outputs / of the external inputs other than
+ * q_index_shifted, in graph order (cuda_graph_executor.cpp:292-334). */
+int mlvc_backend_codec_tensor_count(mlvc_backend* backend, size_t slot, int is_decoder, int* count);
+int mlvc_backend_encoder_output(mlvc_backend* backend, size_t slot, int index, const void** data, size_t* bytes);
+int mlvc_backend_decoder_input(mlvc_backend* backend, size_t slot, int index, void** data, size_t* bytes);
+/* submit_decoder(slot, shifted_q): input uploads, frame graph, conversion,
+ * frame download (cuda_graph_executor.cpp:336-373). */
+int mlvc_backend_submit_decoder(mlvc_backend* backend, size_t slot, int shifted_q);
+int mlvc_backend_decoder_output_yuv(mlvc_backend* backend, size_t slot, const uint8_t** y, const uint8_t** u,
+                                    const uint8_t** v);
+/* wait_codec_slot(slot) (cuda_graph_executor.cpp:393-400). A submitted slot
+ * must be waited before its views are used again; touching it earlier
+ * fails with "codec slot is pending". */
+int mlvc_backend_wait_codec_slot(mlvc_backend* backend, size_t slot);
+/* frame_padding(width, height, model_width, model_height) of core/src/
+ * yuv.cpp:325-337: pad5 = {left, right, top, bottom, rotated}. */
+int mlvc_frame_padding(int width, int height, int model_width, int model_height, int* pad5);
+
 /* ---- "hip" backend extras for measurement (no reference counterpart:
  *      the reference times whole run() calls only) ---- */
 /* Uploads external inputs once; later frames reuse them in HBM. */
-int mlvc_hip_backend_upload_inputs(mlvc_backend* backend, const uint16_t* const* inputs);
+int mlvc_hip_backend_upload_inputs(mlvc_backend* backend, const void* const* inputs);
 /* Replays `frames` per-frame hipGraphs back to back (device-resident, no
  * host copies) and returns the elapsed GPU time between events recorded on
  * the backend's stream around them. */

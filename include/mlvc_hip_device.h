@@ -196,6 +196,21 @@ int mlvc_hip_space_to_depth(const void* x, void* y, int n, int in_c, int h, int 
 
 /* ---- elementwise (elementwise.cu:1-80): y = fp16(op(fp32 inputs)) ---- */
 int mlvc_hip_leaky_relu(const void* x, void* y, size_t count, float alpha, mlvc_hip_stream s);
+
+/* ---- Codec I/O around the encoder / decoder graphs ----
+ * Frames are I420 bytes (Y w*h, then U and V (w/2)*(h/2)); the model image
+ * is FP16 [3, mh, mw]. Replace the driver backend's mlvc_yuv420_to_nchw_fp16
+ * and mlvc_nchw_to_yuv420 (backends/driver_cubin/kernels/codec_io.cu:31-107)
+ * with the CPU backend's values (backends/cpu/src/execution_plan.cpp:
+ * 1044-1322): lut holds 256 FP16 values float_to_half(v / 255 * pixel_range)
+ * in device memory; the frame sits at model (0, 0) with its last column/row
+ * repeated, transposed when rotated. The model -> frame direction reads the
+ * active area at (pad_top, pad_left), divides by pixel_range, averages chroma
+ * over 2x2 and rounds v * 255 half to even after clamping to [0, 1]. */
+int mlvc_hip_yuv420_to_model(const uint8_t* yuv, const uint16_t* lut, void* out, int w, int h, int mw, int mh,
+                             int rotated, mlvc_hip_stream s);
+int mlvc_hip_model_to_yuv420(const void* x, uint8_t* yuv, int w, int h, int mw, int mh, int pad_left, int pad_top,
+                             int rotated, float pixel_range, mlvc_hip_stream s);
 int mlvc_hip_add(const void* a, const void* b, void* y, size_t count, mlvc_hip_stream s);
 /* Channel concat of two NCHW tensors (tensor_ops.cu concat copy, axis 1). */
 int mlvc_hip_concat_channels(const void* a, int ca, const void* b, int cb, void* y, int n, size_t hw,

@@ -40,6 +40,15 @@ mlvc::hip_backend::HipBackend& hip(mlvc_backend* b)
     return *h;
 }
 
+// The buffered codec path, as the reference's callers find it
+// (codec/src/pipeline.cpp:826, 906: dynamic_cast to BufferedCodecBackend).
+mlvc::BufferedCodecBackend& buffered(mlvc_backend* b)
+{
+    auto* c = dynamic_cast<mlvc::BufferedCodecBackend*>(b->impl.get());
+    if (!c) throw std::runtime_error(b->name + ": backend has no buffered codec I/O");
+    return *c;
+}
+
 std::vector<std::vector<std::int64_t>> shapes(mlvc_backend* b, bool outputs)
 {
     return hip(b).io_shapes(outputs);
@@ -115,17 +124,32 @@ int mlvc_backend_io_shape(mlvc_backend* backend, int is_output, int index, int64
     });
 }
 
-int mlvc_backend_run(mlvc_backend* backend, const uint16_t* const* inputs, uint16_t* const* outputs)
+int mlvc_backend_io_dtype(mlvc_backend* backend, int is_output, int index, int* dtype)
+{
+    return guard([&] {
+        const auto t = hip(backend).io_dtypes(is_output != 0).at(static_cast<std::size_t>(index));
+        *dtype = t == mlvc::TensorDataType::kInt32 ? 1 : 0;
+    });
+}
+
+int mlvc_backend_run(mlvc_backend* backend, const void* const* inputs, uint16_t* const* outputs)
 {
     return guard([&] {
         const auto ins = shapes(backend, false);
+        const auto types = hip(backend).io_dtypes(false);
         std::vector<mlvc::Tensor> ts;
         for (std::size_t i = 0; i < ins.size(); ++i) {
             mlvc::Tensor t;
             t.shape = ins[i];
             std::size_t n = 1;
             for (auto d : t.shape) n *= static_cast<std::size_t>(d);
-            t.data = std::vector<mlvc::Float16Storage>(inputs[i], inputs[i] + n);
+            if (types[i] == mlvc::TensorDataType::kInt32) {
+                const auto* p = static_cast<const std::int32_t*>(inputs[i]);
+                t.data = std::vector<std::int32_t>(p, p + n);
+            } else {
+                const auto* p = static_cast<const mlvc::Float16Storage*>(inputs[i]);
+                t.data = std::vector<mlvc::Float16Storage>(p, p + n);
+            }
             ts.push_back(std::move(t));
         }
         const auto outs = backend->impl->run(ts);
@@ -147,11 +171,109 @@ int mlvc_backend_available(char* buf, size_t len)
     });
 }
 
-int mlvc_hip_backend_upload_inputs(mlvc_backend* backend, const uint16_t* const* inputs)
+int mlvc_hip_backend_upload_inputs(mlvc_backend* backend, const void* const* inputs)
 {
     return guard([&] {
         const std::size_t n = shapes(backend, false).size();
-        hip(backend).upload_inputs(std::vector<const std::uint16_t*>(inputs, inputs + n));
+        hip(backend).upload_inputs(std::vector<const void*>(inputs, inputs + n));
+    });
+}
+
+// ---- BufferedCodecBackend ----------------------------------------------
+
+int mlvc_backend_configure_codec_io(mlvc_backend* backend, int width, int height, int model_width, int model_height,
+                                    float pixel_range, int pad_left, int pad_right, int pad_top, int pad_bottom,
+                                    int rotated, size_t slots)
+{
+    return guard([&] {
+        mlvc::CodecIoConfig c;
+        c.width = width;
+        c.height = height;
+        c.model_width = model_width;
+        c.model_height = model_height;
+        c.pixel_range = pixel_range;
+        c.padding = mlvc::FramePadding{pad_left, pad_right, pad_top, pad_bottom, rotated != 0};
+        c.slots = slots;
+        buffered(backend).configure_codec_io(c);
+    });
+}
+
+int mlvc_backend_codec_slot_count(mlvc_backend* backend, size_t* count)
+{
+    return guard([&] { *count = buffered(backend).codec_slot_count(); });
+}
+
+int mlvc_backend_encoder_input_yuv(mlvc_backend* backend, size_t slot, uint8_t** y, uint8_t** u, uint8_t** v)
+{
+    return guard([&] {
+        const auto f = buffered(backend).encoder_input_yuv(slot);
+        *y = f.y().data();
+        *u = f.u().data();
+        *v = f.v().data();
+    });
+}
+
+int mlvc_backend_submit_encoder(mlvc_backend* backend, size_t slot, int shifted_q)
+{
+    return guard([&] { buffered(backend).submit_encoder(slot, shifted_q); });
+}
+
+int mlvc_backend_encoder_output(mlvc_backend* backend, size_t slot, int index, const void** data, size_t* bytes)
+{
+    return guard([&] {
+        const auto v = buffered(backend).encoder_outputs(slot).at(static_cast<std::size_t>(index));
+        *data = v.raw_data();
+        *bytes = v.byte_size();
+    });
+}
+
+int mlvc_backend_decoder_input(mlvc_backend* backend, size_t slot, int index, void** data, size_t* bytes)
+{
+    return guard([&] {
+        const auto v = buffered(backend).decoder_inputs(slot).at(static_cast<std::size_t>(index));
+        *data = v.raw_data();
+        *bytes = v.byte_size();
+    });
+}
+
+int mlvc_backend_codec_tensor_count(mlvc_backend* backend, size_t slot, int is_decoder, int* count)
+{
+    return guard([&] {
+        auto& b = buffered(backend);
+        *count = static_cast<int>(is_decoder ? b.decoder_inputs(slot).size() : b.encoder_outputs(slot).size());
+    });
+}
+
+int mlvc_backend_submit_decoder(mlvc_backend* backend, size_t slot, int shifted_q)
+{
+    return guard([&] { buffered(backend).submit_decoder(slot, shifted_q); });
+}
+
+int mlvc_backend_decoder_output_yuv(mlvc_backend* backend, size_t slot, const uint8_t** y, const uint8_t** u,
+                                    const uint8_t** v)
+{
+    return guard([&] {
+        const auto f = buffered(backend).decoder_output_yuv(slot);
+        *y = f.y().data();
+        *u = f.u().data();
+        *v = f.v().data();
+    });
+}
+
+int mlvc_backend_wait_codec_slot(mlvc_backend* backend, size_t slot)
+{
+    return guard([&] { buffered(backend).wait_codec_slot(slot); });
+}
+
+int mlvc_frame_padding(int width, int height, int model_width, int model_height, int* pad5)
+{
+    return guard([&] {
+        const auto p = mlvc::frame_padding(width, height, model_width, model_height);
+        pad5[0] = p.left;
+        pad5[1] = p.right;
+        pad5[2] = p.top;
+        pad5[3] = p.bottom;
+        pad5[4] = p.rotated ? 1 : 0;
     });
 }
 
@@ -216,7 +338,7 @@ int mlvc_synth_write(const char* config, const char* out_dir, uint64_t seed)
     return guard([&] {
         mlvc::synth::SyntheticModel info;
         const auto g = mlvc::synth::build_synthetic(config, seed, &info);
-        g.write_directory(out_dir, info.model_name, std::string("synthetic/") + config);
+        g.write_directory(out_dir, info.model_name, info.profile);
     });
 }
 

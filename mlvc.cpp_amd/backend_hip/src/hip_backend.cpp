@@ -26,6 +26,7 @@
 #include "mlvc_hip_device.h"
 
 #include <algorithm>
+#include <cmath>
 #include <cstdlib>
 #include <cstring>
 #include <map>
@@ -129,7 +130,7 @@ struct Launch {
 class Plan {
 public:
     Plan(const BackendOptions& options, const std::string& model, const ModelExecutionConfig& config)
-        : device_(options.device_id)
+        : device_(options.device_id), model_(model)
     {
         int count = 0;
         hip_check(mlvc_hip_device_count(&count), "device query");
@@ -152,6 +153,11 @@ public:
 
     ~Plan()
     {
+        // Pending codec slots and any queued work finish before buffers go.
+        mlvc_hip_set_device(device_);
+        mlvc_hip_stream_synchronize(stream_);
+        for (auto& sl : slots_)
+            if (sl.done) mlvc_hip_event_destroy(sl.done);
         for (auto g : graphs_) mlvc_hip_graph_destroy(g);
         mlvc_hip_event_destroy(ev0_);
         mlvc_hip_event_destroy(ev1_);
@@ -163,6 +169,188 @@ public:
         std::vector<std::vector<std::int64_t>> s;
         for (TensorId id : outputs ? ext_out_ : ext_in_) s.push_back(desc(id).shape);
         return s;
+    }
+
+    std::vector<TensorDataType> io_dtypes(bool outputs) const
+    {
+        std::vector<TensorDataType> t;
+        for (TensorId id : outputs ? ext_out_ : ext_in_)
+            t.push_back(desc(id).dtype == aot::DataType::INT32 ? TensorDataType::kInt32 : TensorDataType::kFloat16);
+        return t;
+    }
+
+    // ------------------------------------------------------- codec I/O
+    // The buffered path of the reference's GPU backend
+    // (backends/driver_cubin/src/cuda_graph_executor.cpp:156-400) with the
+    // checks of the CPU backend's configure_codec_io
+    // (backends/cpu/src/execution_plan.cpp:1386-1486): per slot a pinned
+    // frame, pinned copies of the graph's external outputs (encoder) or
+    // inputs (decoder) and an event; submits run upload -> conversion kernel
+    // -> frame graph -> download on the backend's stream.
+    void configure_codec_io(const CodecIoConfig& cfg)
+    {
+        if (codec_on_) fail("codec I/O is already configured");
+        if (model_ != "MLVCEncoder" && model_ != "MLVCDecoder") fail("unsupported codec graph");
+        if (cfg.slots == 0U) fail("codec slot count must be positive");
+        if (!std::isfinite(cfg.pixel_range) || cfg.pixel_range <= 0.0F) fail("pixel range must be finite and positive");
+        const FramePadding& pad = cfg.padding;
+        if (pad.left < 0 || pad.right < 0 || pad.top < 0 || pad.bottom < 0) fail("codec frame padding must be non-negative");
+        std::size_t frame_bytes = 0;
+        try {
+            frame_bytes = yuv420_frame_bytes(cfg.width, cfg.height);
+        } catch (const std::exception& e) {
+            fail(std::string("codec I/O: ") + e.what());
+        }
+        const int active_w = pad.rotated ? cfg.height : cfg.width;
+        const int active_h = pad.rotated ? cfg.width : cfg.height;
+        if (static_cast<long long>(active_w) + pad.left + pad.right != cfg.model_width ||
+            static_cast<long long>(active_h) + pad.top + pad.bottom != cfg.model_height)
+            fail("codec I/O padded dimensions do not match model dimensions");
+        const bool encoder = model_ == "MLVCEncoder";
+        const std::vector<std::int64_t> image{1, 3, cfg.model_height, cfg.model_width};
+        int q = -1, img = -1;
+        for (std::size_t i = 0; i < ext_in_.size(); ++i) {
+            const auto& d = desc(ext_in_[i]);
+            if (d.name == "q_index_shifted") {
+                if (d.dtype != aot::DataType::INT32 || d.shape != std::vector<std::int64_t>{1})
+                    fail("invalid q_index_shifted input");
+                q = static_cast<int>(i);
+            } else if (encoder && d.name == "x") {
+                if (d.dtype != aot::DataType::FP16 || d.shape != image) fail("codec I/O model dimensions do not match graph");
+                img = static_cast<int>(i);
+            }
+        }
+        if (!encoder)
+            for (std::size_t i = 0; i < ext_out_.size(); ++i) {
+                const auto& d = desc(ext_out_[i]);
+                if (d.name != "x_hat") continue;
+                if (d.dtype != aot::DataType::FP16 || d.shape != image) fail("codec I/O model dimensions do not match graph");
+                img = static_cast<int>(i);
+                break;
+            }
+        if (q < 0 || img < 0) fail("missing required codec I/O tensors");
+
+        select();
+        codec_frame_ = DeviceMem(frame_bytes);
+        if (encoder) {
+            std::uint16_t lut[256];
+            for (int v = 0; v < 256; ++v) lut[v] = float_to_half((static_cast<float>(v) / 255.0F) * cfg.pixel_range);
+            codec_lut_ = DeviceMem(sizeof(lut));
+            hip_check(mlvc_hip_memcpy_h2d(codec_lut_.ptr, lut, sizeof(lut), stream_), "codec LUT upload");
+            hip_check(mlvc_hip_stream_synchronize(stream_), "stream sync");
+        }
+        std::vector<CodecSlot> slots(cfg.slots);
+        for (CodecSlot& sl : slots) {
+            sl.frame = HostMem(frame_bytes);
+            std::memset(sl.frame.ptr, 0, frame_bytes);
+            sl.q = HostMem(sizeof(std::int32_t));
+            const auto& ids = encoder ? ext_out_ : ext_in_;
+            sl.io.resize(ids.size());
+            for (std::size_t i = 0; i < ids.size(); ++i)
+                if (encoder || static_cast<int>(i) != q) {
+                    sl.io[i] = HostMem(aot::tensor_bytes(desc(ids[i])));
+                    std::memset(sl.io[i].ptr, 0, aot::tensor_bytes(desc(ids[i])));
+                }
+            hip_check(mlvc_hip_event_create(&sl.done), "event creation");
+        }
+        slots_ = std::move(slots);
+        codec_ = cfg;
+        codec_frame_bytes_ = frame_bytes;
+        codec_q_ = q;
+        codec_img_ = img;
+        codec_encoder_ = encoder;
+        codec_on_ = true;
+    }
+
+    std::size_t codec_slot_count() const noexcept { return codec_on_ ? slots_.size() : 0U; }
+
+    MutableYuv420FrameView encoder_input_yuv(std::size_t index)
+    {
+        CodecSlot& sl = idle_slot(index, true, "encoder");
+        return frame_view(sl);
+    }
+
+    void submit_encoder(std::size_t index, int shifted_q)
+    {
+        CodecSlot& sl = idle_slot(index, true, "encoder");
+        if (!initialized_) fail("reset_state() must be called before submit_encoder()");
+        select();
+        hip_check(mlvc_hip_memcpy_h2d(codec_frame_.ptr, sl.frame.ptr, codec_frame_bytes_, stream_), "frame upload");
+        const FramePadding& pad = codec_.padding;
+        hip_check(mlvc_hip_yuv420_to_model(static_cast<const std::uint8_t*>(codec_frame_.ptr),
+                                           static_cast<const std::uint16_t*>(codec_lut_.ptr),
+                                           input_buf_.at(ext_in_[static_cast<std::size_t>(codec_img_)]).ptr, codec_.width,
+                                           codec_.height, codec_.model_width, codec_.model_height, pad.rotated ? 1 : 0,
+                                           stream_),
+                  "frame conversion");
+        enqueue_q(sl, shifted_q);
+        hip_check(mlvc_hip_graph_launch(graphs_[static_cast<std::size_t>(parity_)], stream_), "graph launch");
+        for (std::size_t i = 0; i < ext_out_.size(); ++i)
+            hip_check(mlvc_hip_memcpy_d2h(sl.io[i].ptr, ptr(ext_out_[i], parity_), aot::tensor_bytes(desc(ext_out_[i])), stream_),
+                      "output download");
+        finish_submit(sl);
+    }
+
+    std::vector<TensorView> encoder_outputs(std::size_t index) const
+    {
+        const CodecSlot& sl = idle_slot(index, true, "encoder");
+        std::vector<TensorView> v;
+        for (std::size_t i = 0; i < ext_out_.size(); ++i) {
+            const auto& d = desc(ext_out_[i]);
+            v.push_back(TensorView::from_raw(d.name, d.shape, public_dtype(d.dtype), sl.io[i].ptr, aot::tensor_bytes(d)));
+        }
+        return v;
+    }
+
+    std::vector<MutableTensorView> decoder_inputs(std::size_t index)
+    {
+        CodecSlot& sl = idle_slot(index, false, "decoder");
+        std::vector<MutableTensorView> v;
+        for (std::size_t i = 0; i < ext_in_.size(); ++i) {
+            if (static_cast<int>(i) == codec_q_) continue;
+            const auto& d = desc(ext_in_[i]);
+            v.push_back(MutableTensorView::from_raw(d.name, d.shape, public_dtype(d.dtype), sl.io[i].ptr, aot::tensor_bytes(d)));
+        }
+        return v;
+    }
+
+    void submit_decoder(std::size_t index, int shifted_q)
+    {
+        CodecSlot& sl = idle_slot(index, false, "decoder");
+        if (!initialized_) fail("reset_state() must be called before submit_decoder()");
+        select();
+        for (std::size_t i = 0; i < ext_in_.size(); ++i) {
+            if (static_cast<int>(i) == codec_q_) continue;
+            hip_check(mlvc_hip_memcpy_h2d(input_buf_.at(ext_in_[i]).ptr, sl.io[i].ptr, aot::tensor_bytes(desc(ext_in_[i])), stream_),
+                      "input upload");
+        }
+        enqueue_q(sl, shifted_q);
+        hip_check(mlvc_hip_graph_launch(graphs_[static_cast<std::size_t>(parity_)], stream_), "graph launch");
+        const FramePadding& pad = codec_.padding;
+        hip_check(mlvc_hip_model_to_yuv420(ptr(ext_out_[static_cast<std::size_t>(codec_img_)], parity_),
+                                           static_cast<std::uint8_t*>(codec_frame_.ptr), codec_.width, codec_.height,
+                                           codec_.model_width, codec_.model_height, pad.left, pad.top,
+                                           pad.rotated ? 1 : 0, codec_.pixel_range, stream_),
+                  "frame conversion");
+        hip_check(mlvc_hip_memcpy_d2h(sl.frame.ptr, codec_frame_.ptr, codec_frame_bytes_, stream_), "frame download");
+        finish_submit(sl);
+    }
+
+    Yuv420FrameView decoder_output_yuv(std::size_t index) const
+    {
+        const CodecSlot& sl = idle_slot(index, false, "decoder");
+        return frame_view(sl);
+    }
+
+    void wait_codec_slot(std::size_t index)
+    {
+        if (!codec_on_) fail("codec I/O is unavailable");
+        if (index >= slots_.size()) fail("codec slot is out of range");
+        CodecSlot& sl = slots_[index];
+        if (!sl.pending) return;
+        select();
+        hip_check(mlvc_hip_event_synchronize(sl.done), "codec slot wait");
+        sl.pending = false;
     }
 
     void reset_state()
@@ -184,7 +372,7 @@ public:
             const Tensor& t = inputs[i];
             t.validate();
             const auto& d = desc(ext_in_[i]);
-            if (t.shape != d.shape || t.data_type() != TensorDataType::kFloat16 || t.byte_size() != aot::tensor_bytes(d))
+            if (t.shape != d.shape || t.data_type() != public_dtype(d.dtype) || t.byte_size() != aot::tensor_bytes(d))
                 fail("graph input shape, dtype, or byte size mismatch");
             std::memcpy(in_stage_[i].ptr, t.raw_data(), t.byte_size());
             hip_check(mlvc_hip_memcpy_h2d(input_buf_.at(ext_in_[i]).ptr, in_stage_[i].ptr, t.byte_size(), stream_), "input upload");
@@ -207,7 +395,7 @@ public:
         return out;
     }
 
-    void upload_inputs(const std::vector<const std::uint16_t*>& inputs)
+    void upload_inputs(const std::vector<const void*>& inputs)
     {
         if (inputs.size() != ext_in_.size()) fail("graph input count mismatch");
         select();
@@ -305,8 +493,13 @@ private:
             state_in_[in] = bindings_.size() - 1;
             state_out_[out] = bindings_.size() - 1;
         }
+        // FP16 activations, plus INT32 control inputs such as q_index_shifted
+        // (consumed by no kernel on this path; an operator reading one is
+        // rejected when the graph is lowered).
         for (TensorId id : g.inputs) {
-            if (desc(id).dtype != aot::DataType::FP16) fail("only FP16 graph inputs are on this path");
+            const auto dt = desc(id).dtype;
+            if (dt != aot::DataType::FP16 && !(dt == aot::DataType::INT32 && !state_in_.count(id)))
+                fail("only FP16 activations and INT32 control inputs are on this path");
             if (!state_in_.count(id)) ext_in_.push_back(id);
         }
         for (TensorId id : g.outputs) {
@@ -1051,7 +1244,60 @@ private:
                       "output download");
     }
 
+    struct CodecSlot {
+        HostMem frame;            // encoder input / decoder output frame (I420)
+        std::vector<HostMem> io;  // encoder: external outputs; decoder: external inputs (not q)
+        HostMem q;                // q_index_shifted staging
+        mlvc_hip_event done = nullptr;
+        bool pending = false;
+    };
+
+    static TensorDataType public_dtype(aot::DataType t)
+    {
+        return t == aot::DataType::INT32 ? TensorDataType::kInt32 : TensorDataType::kFloat16;
+    }
+
+    CodecSlot& idle_slot(std::size_t index, bool encoder, const char* side)
+    {
+        return const_cast<CodecSlot&>(static_cast<const Plan*>(this)->idle_slot(index, encoder, side));
+    }
+
+    const CodecSlot& idle_slot(std::size_t index, bool encoder, const char* side) const
+    {
+        if (!codec_on_ || codec_encoder_ != encoder) fail(std::string(side) + " codec I/O is unavailable");
+        if (index >= slots_.size()) fail("codec slot is out of range");
+        const CodecSlot& sl = slots_[index];
+        if (sl.pending) fail(std::string(side) + " codec slot is pending");
+        return sl;
+    }
+
+    MutableYuv420FrameView frame_view(CodecSlot& sl) const
+    {
+        auto* b = static_cast<std::uint8_t*>(sl.frame.ptr);
+        const std::size_t ysz = static_cast<std::size_t>(codec_.width) * codec_.height, uvsz = ysz / 4;
+        return MutableYuv420FrameView(codec_.width, codec_.height, std::span<std::uint8_t>(b, ysz),
+                                      std::span<std::uint8_t>(b + ysz, uvsz), std::span<std::uint8_t>(b + ysz + uvsz, uvsz));
+    }
+
+    Yuv420FrameView frame_view(const CodecSlot& sl) const { return frame_view(const_cast<CodecSlot&>(sl)); }
+
+    void enqueue_q(CodecSlot& sl, int shifted_q)
+    {
+        const std::int32_t q32 = static_cast<std::int32_t>(shifted_q);
+        std::memcpy(sl.q.ptr, &q32, sizeof(q32));
+        hip_check(mlvc_hip_memcpy_h2d(input_buf_.at(ext_in_[static_cast<std::size_t>(codec_q_)]).ptr, sl.q.ptr, sizeof(q32), stream_),
+                  "q upload");
+    }
+
+    void finish_submit(CodecSlot& sl)
+    {
+        advance();
+        hip_check(mlvc_hip_event_record(sl.done, stream_), "event record");
+        sl.pending = true;
+    }
+
     int device_;
+    std::string model_;
     aot::LoadedGraph graph_;
     mlvc_hip_stream stream_ = nullptr;
     mlvc_hip_event ev0_ = nullptr, ev1_ = nullptr;
@@ -1068,6 +1314,13 @@ private:
     std::vector<mlvc_hip_graph> graphs_;
     int parity_ = 0;
     bool initialized_ = false;
+    // codec I/O
+    bool codec_on_ = false, codec_encoder_ = false;
+    CodecIoConfig codec_{};
+    std::size_t codec_frame_bytes_ = 0;
+    int codec_q_ = -1, codec_img_ = -1;  // external input index of q; of x (encoder) / output index of x_hat (decoder)
+    DeviceMem codec_frame_, codec_lut_;
+    std::vector<CodecSlot> slots_;
 };
 
 HipBackend::HipBackend(BackendOptions options) : options_(std::move(options))
@@ -1094,7 +1347,17 @@ void HipBackend::load(const std::string& model_name, const ModelExecutionConfig&
 std::vector<Tensor> HipBackend::run(const std::vector<Tensor>& inputs) { return require_plan("run()").run(inputs); }
 void HipBackend::reset_state() { require_plan("reset_state()").reset_state(); }
 std::vector<std::vector<std::int64_t>> HipBackend::io_shapes(bool outputs) const { return require_plan("io_shapes()").io_shapes(outputs); }
-void HipBackend::upload_inputs(const std::vector<const std::uint16_t*>& inputs) { require_plan("upload_inputs()").upload_inputs(inputs); }
+void HipBackend::upload_inputs(const std::vector<const void*>& inputs) { require_plan("upload_inputs()").upload_inputs(inputs); }
+std::vector<TensorDataType> HipBackend::io_dtypes(bool outputs) const { return require_plan("io_dtypes()").io_dtypes(outputs); }
+void HipBackend::configure_codec_io(const CodecIoConfig& config) { require_plan("configure_codec_io()").configure_codec_io(config); }
+std::size_t HipBackend::codec_slot_count() const noexcept { return plan_ ? plan_->codec_slot_count() : 0U; }
+MutableYuv420FrameView HipBackend::encoder_input_yuv(std::size_t slot) { return require_plan("encoder_input_yuv()").encoder_input_yuv(slot); }
+void HipBackend::submit_encoder(std::size_t slot, int q) { require_plan("submit_encoder()").submit_encoder(slot, q); }
+std::vector<TensorView> HipBackend::encoder_outputs(std::size_t slot) const { return require_plan("encoder_outputs()").encoder_outputs(slot); }
+std::vector<MutableTensorView> HipBackend::decoder_inputs(std::size_t slot) { return require_plan("decoder_inputs()").decoder_inputs(slot); }
+void HipBackend::submit_decoder(std::size_t slot, int q) { require_plan("submit_decoder()").submit_decoder(slot, q); }
+Yuv420FrameView HipBackend::decoder_output_yuv(std::size_t slot) const { return require_plan("decoder_output_yuv()").decoder_output_yuv(slot); }
+void HipBackend::wait_codec_slot(std::size_t slot) { require_plan("wait_codec_slot()").wait_codec_slot(slot); }
 float HipBackend::time_frames(int frames) { return require_plan("time_frames()").time_frames(frames); }
 void HipBackend::download_outputs(const std::vector<std::uint16_t*>& outputs) { require_plan("download_outputs()").download_outputs(outputs); }
 std::size_t HipBackend::launch_count() const { return require_plan("launch_count()").launch_count(); }

@@ -26,7 +26,7 @@ struct LaunchInfo {
 
 class Plan;
 
-class HipBackend final : public InferenceBackend {
+class HipBackend final : public InferenceBackend, public BufferedCodecBackend {
 public:
     explicit HipBackend(BackendOptions options);
     ~HipBackend() override;
@@ -36,11 +36,24 @@ public:
     std::vector<Tensor> run(const std::vector<Tensor>& inputs) override;
     void reset_state() override;
 
+    // BufferedCodecBackend: pinned slots, GPU frame conversions around the
+    // MLVCEncoder / MLVCDecoder graphs, stream-ordered submits.
+    void configure_codec_io(const CodecIoConfig& config) override;
+    std::size_t codec_slot_count() const noexcept override;
+    MutableYuv420FrameView encoder_input_yuv(std::size_t slot) override;
+    void submit_encoder(std::size_t slot, int shifted_q) override;
+    std::vector<TensorView> encoder_outputs(std::size_t slot) const override;
+    std::vector<MutableTensorView> decoder_inputs(std::size_t slot) override;
+    void submit_decoder(std::size_t slot, int shifted_q) override;
+    Yuv420FrameView decoder_output_yuv(std::size_t slot) const override;
+    void wait_codec_slot(std::size_t slot) override;
+
     // External (non-state) graph inputs / outputs in graph order.
     std::vector<std::vector<std::int64_t>> io_shapes(bool outputs) const;
+    std::vector<TensorDataType> io_dtypes(bool outputs) const;
 
-    // Device-resident measurement helpers.
-    void upload_inputs(const std::vector<const std::uint16_t*>& inputs);
+    // Device-resident measurement helpers (inputs as raw host bytes).
+    void upload_inputs(const std::vector<const void*>& inputs);
     float time_frames(int frames);
     void download_outputs(const std::vector<std::uint16_t*>& outputs);
     std::size_t launch_count() const;

@@ -50,10 +50,26 @@ def backend_lib() -> C.CDLL:
         lib.mlvc_backend_load.argtypes = [C.c_void_p, C.c_char_p, _i64p, C.c_int]
         lib.mlvc_backend_io_count.argtypes = [C.c_void_p, C.c_int, C.POINTER(C.c_int)]
         lib.mlvc_backend_io_shape.argtypes = [C.c_void_p, C.c_int, C.c_int, _i64p, C.POINTER(C.c_int)]
-        lib.mlvc_backend_run.argtypes = [C.c_void_p, C.POINTER(_u16p), C.POINTER(_u16p)]
+        lib.mlvc_backend_run.argtypes = [C.c_void_p, C.POINTER(C.c_void_p), C.POINTER(_u16p)]
+        lib.mlvc_backend_io_dtype.argtypes = [C.c_void_p, C.c_int, C.c_int, C.POINTER(C.c_int)]
+        _u8pp = C.POINTER(C.POINTER(C.c_uint8))
+        lib.mlvc_backend_configure_codec_io.argtypes = [C.c_void_p] + [C.c_int] * 4 + [C.c_float] + [C.c_int] * 5 + [
+            C.c_size_t]
+        lib.mlvc_backend_codec_slot_count.argtypes = [C.c_void_p, C.POINTER(C.c_size_t)]
+        lib.mlvc_backend_encoder_input_yuv.argtypes = [C.c_void_p, C.c_size_t, _u8pp, _u8pp, _u8pp]
+        lib.mlvc_backend_decoder_output_yuv.argtypes = [C.c_void_p, C.c_size_t, _u8pp, _u8pp, _u8pp]
+        lib.mlvc_backend_submit_encoder.argtypes = [C.c_void_p, C.c_size_t, C.c_int]
+        lib.mlvc_backend_submit_decoder.argtypes = [C.c_void_p, C.c_size_t, C.c_int]
+        lib.mlvc_backend_codec_tensor_count.argtypes = [C.c_void_p, C.c_size_t, C.c_int, C.POINTER(C.c_int)]
+        lib.mlvc_backend_encoder_output.argtypes = [C.c_void_p, C.c_size_t, C.c_int, C.POINTER(C.c_void_p),
+                                                    C.POINTER(C.c_size_t)]
+        lib.mlvc_backend_decoder_input.argtypes = [C.c_void_p, C.c_size_t, C.c_int, C.POINTER(C.c_void_p),
+                                                   C.POINTER(C.c_size_t)]
+        lib.mlvc_backend_wait_codec_slot.argtypes = [C.c_void_p, C.c_size_t]
+        lib.mlvc_frame_padding.argtypes = [C.c_int] * 4 + [C.POINTER(C.c_int)]
         lib.mlvc_backend_reset_state.argtypes = [C.c_void_p]
         lib.mlvc_backend_available.argtypes = [C.c_char_p, C.c_size_t]
-        lib.mlvc_hip_backend_upload_inputs.argtypes = [C.c_void_p, C.POINTER(_u16p)]
+        lib.mlvc_hip_backend_upload_inputs.argtypes = [C.c_void_p, C.POINTER(C.c_void_p)]
         lib.mlvc_hip_backend_time_frames.argtypes = [C.c_void_p, C.c_int, C.POINTER(C.c_float)]
         lib.mlvc_hip_backend_download_outputs.argtypes = [C.c_void_p, C.POINTER(_u16p)]
         lib.mlvc_hip_backend_launch_count.argtypes = [C.c_void_p, C.POINTER(C.c_int)]
@@ -101,6 +117,24 @@ def _ptrs(arrays):
     for i, a in enumerate(arrays):
         arr[i] = a.ctypes.data_as(_u16p)
     return arr
+
+
+def _vptrs(arrays):
+    arr = (C.c_void_p * len(arrays))()
+    for i, a in enumerate(arrays):
+        arr[i] = a.ctypes.data
+    return arr
+
+
+def frame_padding(width: int, height: int, model_width: int, model_height: int) -> tuple:
+    """(left, right, top, bottom, rotated): frame_padding of core/src/yuv.cpp:325-337."""
+    pad = (C.c_int * 5)()
+    _check(backend_lib().mlvc_frame_padding(width, height, model_width, model_height, pad))
+    return tuple(pad)
+
+
+def yuv_frame_bytes(width: int, height: int) -> int:
+    return width * height + 2 * (width // 2) * (height // 2)
 
 
 def available_backends() -> list[str]:
@@ -159,13 +193,19 @@ class Backend:
         _check(self._lib.mlvc_backend_load(self._h, model_name.encode(), flat, len(bindings)))
         self.in_shapes = self._shapes(0)
         self.out_shapes = self._shapes(1)
+        self.in_dtypes = []
+        for i in range(len(self.in_shapes)):
+            t = C.c_int()
+            _check(self._lib.mlvc_backend_io_dtype(self._h, 0, i, C.byref(t)))
+            self.in_dtypes.append(np.int32 if t.value == 1 else np.uint16)
 
     def _check_inputs(self, inputs):
+        """FP16 inputs as uint16 bit patterns; INT32 control inputs as int32."""
         if len(inputs) != len(self.in_shapes):
             raise MlvcError("graph input count mismatch")
         arrs = []
-        for a, s in zip(inputs, self.in_shapes):
-            a = np.ascontiguousarray(a, dtype=np.uint16)
+        for a, s, t in zip(inputs, self.in_shapes, self.in_dtypes):
+            a = np.ascontiguousarray(a, dtype=t)
             if a.size != int(np.prod(s)):
                 raise MlvcError("graph input shape mismatch")
             arrs.append(a)
@@ -174,8 +214,70 @@ class Backend:
     def run(self, inputs) -> list[np.ndarray]:
         arrs = self._check_inputs(inputs)
         outs = [np.empty(s, dtype=np.uint16) for s in self.out_shapes]
-        _check(self._lib.mlvc_backend_run(self._h, _ptrs(arrs), _ptrs(outs)))
+        _check(self._lib.mlvc_backend_run(self._h, _vptrs(arrs), _ptrs(outs)))
         return outs
+
+    # ---- BufferedCodecBackend (backend.hpp:64-96) ----
+    def configure_codec_io(self, width: int, height: int, model_width: int, model_height: int,
+                           pixel_range: float = 1.0, padding=None, slots: int = 2) -> tuple:
+        """padding = (left, right, top, bottom, rotated); default frame_padding()."""
+        pad = padding if padding is not None else frame_padding(width, height, model_width, model_height)
+        _check(self._lib.mlvc_backend_configure_codec_io(self._h, width, height, model_width, model_height,
+                                                         pixel_range, *[int(v) for v in pad], slots))
+        self.codec = (width, height)
+        return pad
+
+    def codec_slot_count(self) -> int:
+        n = C.c_size_t()
+        _check(self._lib.mlvc_backend_codec_slot_count(self._h, C.byref(n)))
+        return n.value
+
+    def _frame(self, fn, slot: int, writable: bool) -> np.ndarray:
+        y, u, v = (C.POINTER(C.c_uint8)(), C.POINTER(C.c_uint8)(), C.POINTER(C.c_uint8)())
+        _check(fn(self._h, slot, C.byref(y), C.byref(u), C.byref(v)))
+        w, h = self.codec
+        n = yuv_frame_bytes(w, h)
+        # The three planes are contiguous in the slot's pinned buffer.
+        a = np.ctypeslib.as_array(y, shape=(n,))
+        a.flags.writeable = writable
+        return a
+
+    def encoder_input_yuv(self, slot: int) -> np.ndarray:
+        """Writable view of the slot's pinned I420 frame (Y, U, V back to back)."""
+        return self._frame(self._lib.mlvc_backend_encoder_input_yuv, slot, True)
+
+    def decoder_output_yuv(self, slot: int) -> np.ndarray:
+        return self._frame(self._lib.mlvc_backend_decoder_output_yuv, slot, False)
+
+    def submit_encoder(self, slot: int, shifted_q: int) -> None:
+        _check(self._lib.mlvc_backend_submit_encoder(self._h, slot, shifted_q))
+
+    def submit_decoder(self, slot: int, shifted_q: int) -> None:
+        _check(self._lib.mlvc_backend_submit_decoder(self._h, slot, shifted_q))
+
+    def wait_codec_slot(self, slot: int) -> None:
+        _check(self._lib.mlvc_backend_wait_codec_slot(self._h, slot))
+
+    def _tensors(self, slot: int, decoder: bool) -> list[np.ndarray]:
+        n = C.c_int()
+        _check(self._lib.mlvc_backend_codec_tensor_count(self._h, slot, int(decoder), C.byref(n)))
+        fn = self._lib.mlvc_backend_decoder_input if decoder else self._lib.mlvc_backend_encoder_output
+        out = []
+        for i in range(n.value):
+            p, nb = C.c_void_p(), C.c_size_t()
+            _check(fn(self._h, slot, i, C.byref(p), C.byref(nb)))
+            a = np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_uint16)), shape=(nb.value // 2,))
+            a.flags.writeable = decoder
+            out.append(a)
+        return out
+
+    def encoder_outputs(self, slot: int) -> list[np.ndarray]:
+        """Views of the slot's pinned external outputs (FP16 bits, flat, graph order)."""
+        return self._tensors(slot, False)
+
+    def decoder_inputs(self, slot: int) -> list[np.ndarray]:
+        """Writable views of the slot's pinned external inputs other than q_index_shifted."""
+        return self._tensors(slot, True)
 
     def reset_state(self) -> None:
         _check(self._lib.mlvc_backend_reset_state(self._h))
@@ -183,7 +285,7 @@ class Backend:
     # ---- device-resident measurement helpers ("hip" backend only) ----
     def upload_inputs(self, inputs) -> None:
         arrs = self._check_inputs(inputs)
-        _check(self._lib.mlvc_hip_backend_upload_inputs(self._h, _ptrs(arrs)))
+        _check(self._lib.mlvc_hip_backend_upload_inputs(self._h, _vptrs(arrs)))
 
     def time_frames(self, frames: int) -> float:
         ms = C.c_float()

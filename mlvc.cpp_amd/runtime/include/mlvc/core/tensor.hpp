@@ -11,6 +11,7 @@
 #include <span>
 #include <stdexcept>
 #include <string>
+#include <string_view>
 #include <type_traits>
 #include <variant>
 #include <vector>
@@ -80,5 +81,46 @@ struct Tensor {
             throw std::runtime_error("tensor shape does not match its storage");
     }
 };
+
+// Non-owning views over host tensor storage (shape span and data must
+// outlive the view), as returned by the buffered codec slots. Contract of
+// the reference's core/include/mlvc/core/tensor.hpp:104-200: the element
+// count must match the shape, and from_raw checks the byte size.
+template <bool Mutable>
+class BasicTensorView {
+public:
+    using Pointer = std::conditional_t<Mutable, void*, const void*>;
+
+    static BasicTensorView from_raw(std::string_view name, std::span<const std::int64_t> shape, TensorDataType type,
+                                    Pointer data, std::size_t bytes)
+    {
+        const std::size_t count = checked_tensor_element_count(shape);
+        if (data == nullptr || bytes != count * tensor_data_type_size(type))
+            throw std::runtime_error("tensor view shape does not match its storage");
+        return BasicTensorView(name, shape, type, data, count);
+    }
+
+    std::string_view name() const noexcept { return name_; }
+    std::span<const std::int64_t> shape() const noexcept { return shape_; }
+    TensorDataType data_type() const noexcept { return type_; }
+    Pointer raw_data() const noexcept { return data_; }
+    std::size_t element_count() const noexcept { return count_; }
+    std::size_t byte_size() const noexcept { return count_ * tensor_data_type_size(type_); }
+
+private:
+    BasicTensorView(std::string_view name, std::span<const std::int64_t> shape, TensorDataType type, Pointer data,
+                    std::size_t count)
+        : name_(name), shape_(shape), type_(type), data_(data), count_(count)
+    {
+    }
+    std::string_view name_;
+    std::span<const std::int64_t> shape_;
+    TensorDataType type_;
+    Pointer data_;
+    std::size_t count_;
+};
+
+using TensorView = BasicTensorView<false>;
+using MutableTensorView = BasicTensorView<true>;
 
 }  // namespace mlvc

@@ -114,6 +114,7 @@ private:
 // scaled-down "mlvc_s_tiny" (same topology at 64x32) used for quick parity.
 struct SyntheticModel {
     std::string model_name;
+    std::string profile;  // metadata checkpoint id; graphs of one model directory share it
     std::vector<StateTensorBinding> state_bindings;
     std::vector<std::vector<std::int64_t>> external_inputs;  // graph order, bound state removed
     std::vector<std::string> external_input_names;

@@ -15,6 +15,8 @@
 //                        of y1); W,b ~ N(0,0.02)
 //   mlvc_s_640x368       MLVC-S-shaped per-frame graph, 8 frames (below)
 //   mlvc_1920x1088       the same topology widened to 1/16, 32 frames
+//   codec_{enc,dec}_*    the MLVCEncoder / MLVCDecoder pair of the buffered
+//                        codec path (build_codec below)
 //
 // MLVC-shaped topology (frame x[1,3,H,W] U[0,1], state ref[1,64,H/2,W/2]):
 //   SPACE_TO_DEPTH 2 -> 3x3 12->64 + LReLU -> CONCAT(ref) -> 1x1 128->64 +
@@ -187,6 +189,82 @@ void build_mlvc(GraphBuilder& g, Rng& rng, SyntheticModel& info, int h, int w, i
     info.frames = frames;
 }
 
+// Encoder / decoder pair of the buffered codec path (graph names
+// MLVCEncoder / MLVCDecoder, as the reference's codec bundles use), built
+// from the MLVC-shaped topology above at 1/16:
+//   MLVCEncoder(x[1,3,h,w], q_index_shifted INT32[1], ref_in) ->
+//     (y = analysis latent [1,256,h/16,w/16], ref_out)
+//   MLVCDecoder(y, q_index_shifted, ref_in) -> (x_hat[1,3,h,w], ref_out)
+// Analysis: SPACE_TO_DEPTH 2 -> 3x3 12->64 + LReLU -> CONCAT(ref_in) -> 1x1
+// 128->64 + LReLU -> 3x3 s2 64->128->192->256 + LReLU -> B depthwise-separable
+// residual blocks = y. Synthesis (both graphs, the same weights from their
+// own Rng stream): 3x3 256->768, 192->512, 128->256 (+ LReLU, each followed by
+// DEPTH_TO_SPACE 2) -> CONCAT(ref_in) -> 1x1 128->64 + LReLU = ref_out (the
+// state, carried frame to frame); the decoder adds 3x3 64->12 -> DEPTH_TO_SPACE
+// 2 = x_hat. The encoder runs the synthesis state path too, so its ref_out
+// equals the decoder's for the same y and ref_in. q_index_shifted is the
+// graphs' INT32 control input: no operator of this path reads it (the real
+// models look up quantisation scales with it).
+void build_codec(GraphBuilder& g, Rng& rng, SyntheticModel& info, int h, int w, int blocks, int frames, bool encoder)
+{
+    Ctx c{g, rng};
+    const Id lead = encoder ? g.input("x", {1, 3, h, w}) : g.input("y", {1, 256, h / 16, w / 16});
+    g.input("q_index_shifted", {1}, aot::DataType::INT32);
+    const Id ref = g.input("ref_in", {1, 64, h / 2, w / 2});
+    Id y = lead;
+    if (encoder) {
+        Id t = g.pixel(Op::SPACE_TO_DEPTH, c.next("unshuffle"), lead, 2);
+        t = c.conv_act(t, 64, 3, 1);
+        t = g.concat(c.next("concat_ref"), {t, ref}, 1);
+        t = c.conv_act(t, 64, 1, 1);
+        t = c.conv_act(t, 128, 3, 2);
+        t = c.conv_act(t, 192, 3, 2);
+        t = c.conv_act(t, 256, 3, 2);
+        for (int b = 0; b < blocks; ++b) {
+            const std::string base = c.next("dw");
+            const Id wd = g.weight_fp16(base + ".w", {256, 1, 3, 3}, normal_fp16(rng, 256 * 9, 1.0 / 3.0));
+            const Id bd = g.weight_fp16(base + ".b", {256}, normal_fp16(rng, 256, 0.01));
+            const Id d = g.conv(base, t, wd, bd, {1, 1}, {1, 1}, 256);
+            const Id e = c.conv_act(d, 512, 1, 1);
+            const Id f = c.conv_lin(e, 256, 1, 1, 0.1);
+            t = g.binary(Op::ADD, b + 1 == blocks ? std::string("y") : c.next("residual"), f, t);
+        }
+        y = t;
+    }
+    Rng syn_rng(0x5EEDC0DEC0DEULL);
+    Ctx s{g, syn_rng, 1000};
+    auto conv_shuffle = [&](Id in, int oc, bool act, const std::string& what) {
+        const Id t = act ? s.conv_act(in, oc, 3, 1) : s.conv_lin(in, oc, 3, 1);
+        return g.pixel(Op::DEPTH_TO_SPACE, s.next(what), t, 2);
+    };
+    Id t = conv_shuffle(y, 768, true, "shuffle");   // 192 @1/8
+    t = conv_shuffle(t, 512, true, "shuffle");       // 128 @1/4
+    t = conv_shuffle(t, 256, true, "shuffle");       // 64 @1/2
+    t = g.concat(s.next("concat_ref"), {t, ref}, 1);
+    const Id state = s.conv_act(t, 64, 1, 1);        // next reference
+    if (encoder) {
+        g.output(y);
+        g.output(state);
+        info.external_inputs = {{1, 3, h, w}, {1}};
+        info.external_input_names = {"x", "q_index_shifted"};
+        info.input_lo = {0.0, 0.0};
+        info.input_hi = {1.0, 0.0};
+    } else {
+        const Id rec = s.conv_lin(state, 12, 3, 1);
+        const Id xh = g.pixel(Op::DEPTH_TO_SPACE, "x_hat", rec, 2);
+        g.output(xh);
+        g.output(state);
+        info.external_inputs = {{1, 256, h / 16, w / 16}, {1}};
+        info.external_input_names = {"y", "q_index_shifted"};
+        info.input_lo = {-1.0, 0.0};
+        info.input_hi = {1.0, 0.0};
+    }
+    info.model_name = encoder ? "MLVCEncoder" : "MLVCDecoder";
+    info.profile = "synthetic/codec_" + std::to_string(w) + "x" + std::to_string(h);
+    info.state_bindings = {StateTensorBinding{2, 1, TensorDataType::kFloat16, {1, 64, h / 2, w / 2}}};
+    info.frames = frames;
+}
+
 struct ConfigEntry {
     const char* name;
     std::function<void(GraphBuilder&, Rng&, SyntheticModel&)> make;
@@ -204,6 +282,10 @@ const std::vector<ConfigEntry>& registry()
         {"mlvc_1920x1088", [](GraphBuilder& g, Rng& r, SyntheticModel& i) { build_mlvc(g, r, i, 1088, 1920, 4, 12, 32); }},
         {"mlvc_s_tiny", [](GraphBuilder& g, Rng& r, SyntheticModel& i) { build_mlvc(g, r, i, 32, 64, 3, 2, 4); }},
         {"mlvc_tiny", [](GraphBuilder& g, Rng& r, SyntheticModel& i) { build_mlvc(g, r, i, 64, 128, 4, 2, 4); }},
+        {"codec_enc_1920x1088", [](GraphBuilder& g, Rng& r, SyntheticModel& i) { build_codec(g, r, i, 1088, 1920, 12, 32, true); }},
+        {"codec_dec_1920x1088", [](GraphBuilder& g, Rng& r, SyntheticModel& i) { build_codec(g, r, i, 1088, 1920, 12, 32, false); }},
+        {"codec_enc_tiny", [](GraphBuilder& g, Rng& r, SyntheticModel& i) { build_codec(g, r, i, 64, 128, 2, 4, true); }},
+        {"codec_dec_tiny", [](GraphBuilder& g, Rng& r, SyntheticModel& i) { build_codec(g, r, i, 64, 128, 2, 4, false); }},
     };
     return entries;
 }
@@ -230,7 +312,8 @@ GraphBuilder build_synthetic(const std::string& config, std::uint64_t seed, Synt
     Rng rng(seed);
     SyntheticModel local;
     find(config).make(g, rng, local);
-    local.model_name = config;
+    if (local.model_name.empty()) local.model_name = config;
+    if (local.profile.empty()) local.profile = "synthetic/" + config;
     if (info) *info = local;
     return g;
 }
@@ -259,6 +342,8 @@ std::vector<Float16Storage> synthetic_input(const std::string& config, std::size
     Rng rng(seed ^ (0xA5A5A5A5ULL + 0x1000193ULL * (input_index + 1)) ^
             (static_cast<std::uint64_t>(frame + 1) * 0x9E3779B97F4A7C15ULL));
     const double lo = info.input_lo[input_index], hi = info.input_hi[input_index];
+    if (info.external_input_names[input_index] == "q_index_shifted")
+        throw std::runtime_error("q_index_shifted is an INT32 control input; pass it directly");
     std::vector<Float16Storage> v(n);
     for (auto& x : v) x = float_to_half(static_cast<float>(lo + (hi - lo) * rng.uniform()));
     return v;

@@ -1,6 +1,7 @@
 #!/usr/bin/env bash
 # Builds oracle/_ref/libmlvc_ref_kernels.so from the reference CPU kernel
-# sources where they lie (default /root/reference) plus oracle/ref_harness.cpp.
+# sources and core/src/yuv.cpp where they lie (default /root/reference) plus
+# oracle/ref_harness.cpp.
 # Test infrastructure only; the output stays out of git history.
 # Flags follow the reference's backends/cpu/CMakeLists.txt: the AVX2 file is
 # built with -mavx2 -mfma -mf16c, the scalar file without (so its multiply
@@ -21,6 +22,7 @@ $CXX -c "$REF/backends/cpu/src/kernels_scalar.cpp" -o "$OUT/obj/kernels_scalar.o
 $CXX -mavx2 -mfma -mf16c -c "$REF/backends/cpu/src/kernels_x86_avx2.cpp" -o "$OUT/obj/kernels_x86_avx2.o" & pids+=($!)
 $CXX -c "$REF/backends/cpu/src/thread_pool.cpp" -o "$OUT/obj/thread_pool.o" & pids+=($!)
 $CXX -c "$REF/backends/cpu/src/cpu_features.cpp" -o "$OUT/obj/cpu_features.o" & pids+=($!)
+$CXX -c "$REF/core/src/yuv.cpp" -o "$OUT/obj/yuv.o" & pids+=($!)
 $CXX -c "$HERE/ref_harness.cpp" -o "$OUT/obj/ref_harness.o" & pids+=($!)
 for p in "${pids[@]}"; do wait "$p"; done
 g++ -shared -o "$OUT/libmlvc_ref_kernels.so" "$OUT"/obj/*.o -lpthread

@@ -26,6 +26,9 @@
 //   * LeakyReLU / ADD: kernels_x86_avx2.cpp:304-322,382-398 and scalar
 //     :244-268. Pixel shuffle/unshuffle (CRD): kernels_scalar.cpp:954-1026.
 //     Channel CONCAT: kernels_scalar.cpp:893-928 (axis 1 case).
+//   * Codec I/O around the encoder/decoder graphs: frame -> model input and
+//     model output -> frame conversions, execution_plan.cpp:1044-1322, and
+//     frame_padding, core/src/yuv.cpp:325-337.
 //   * Plan: NHWC re-layout of 4-D FP16 tensors with C > 1 and H*W > 1
 //     (execution_plan.cpp:78-82, 639-665, 1324-1358), conv classification
 //     (:410-462), state bindings (:349-369, 806-816, 1033-1042), run()
@@ -726,8 +729,13 @@ public:
         for (std::size_t id = 1; id < g_.t.size(); ++id) {
             const GTensor& t = g_.t[id];
             if (t.name.empty()) continue;
-            if (t.dtype != 1 && !t.weight) throw std::runtime_error("oracle: only FP16 activations are on this path");
+            // FP16 activations; INT32 graph inputs (q_index_shifted, which no
+            // operator of this path reads) are carried as raw bytes.
+            const bool int32_input = t.dtype == 2 && in_pos_.count(static_cast<std::uint32_t>(id));
+            if (t.dtype != 1 && !t.weight && !int32_input)
+                throw std::runtime_error("oracle: only FP16 activations are on this path");
             if (t.dtype == 1) bufs_[id].assign(elems(t.shape), 0);
+            if (int32_input) bufs_[id].assign(2 * elems(t.shape), 0);
         }
         for (std::size_t id = 1; id < g_.t.size(); ++id) {
             const GTensor& t = g_.t[id];
@@ -1002,6 +1010,114 @@ Pool& kernel_pool(int threads)
 
 }  // namespace
 
+// ---- codec I/O conversions around the encoder / decoder graphs ----------
+// Frames are I420: Y plane w*h bytes, then U and V planes of (w/2)*(h/2).
+
+// Byte -> FP16 input value: float_to_half((v / 255) * pixel_range),
+// execution_plan.cpp:1452-1458 (the same table as yuv.cpp:350-354).
+void byte_lut(float range, u16* lut)
+{
+    for (int v = 0; v < 256; ++v) lut[v] = f2h((static_cast<float>(v) / 255.0F) * range);
+}
+
+// Frame -> model input [3, mh, mw]: write_yuv420_to_nhwc_fp16,
+// execution_plan.cpp:1052-1150, in NCHW order. The frame sits at model
+// (0, 0); columns past it repeat its last column (:1101-1114) and rows past
+// it its last row (:1116-1124). A rotated frame is transposed into the model
+// (:1128-1149). Chroma samples cover 2x2 luma pixels.
+void yuv_to_model(const std::uint8_t* yuv, int w, int h, int mw, int mh, int rotated, float range, u16* out)
+{
+    u16 lut[256];
+    byte_lut(range, lut);
+    const std::size_t ysz = static_cast<std::size_t>(w) * h, uvsz = ysz / 4;
+    const std::uint8_t* pu = yuv + ysz;
+    const std::uint8_t* pv = pu + uvsz;
+    const std::size_t plane = static_cast<std::size_t>(mw) * mh;
+    for (int y = 0; y < mh; ++y)
+        for (int x = 0; x < mw; ++x) {
+            int sy, sx;
+            if (rotated) {
+                sx = std::min(y, w - 1);
+                sy = std::min(x, h - 1);
+            } else {
+                sy = std::min(y, h - 1);
+                sx = std::min(x, w - 1);
+            }
+            const std::size_t o = static_cast<std::size_t>(y) * mw + x;
+            const std::size_t uv = static_cast<std::size_t>(sy / 2) * (w / 2) + sx / 2;
+            out[o] = lut[yuv[static_cast<std::size_t>(sy) * w + sx]];
+            out[plane + o] = lut[pu[uv]];
+            out[2 * plane + o] = lut[pv[uv]];
+        }
+}
+
+// clamp to [0, 1], then nearbyint(v * 255) (round half to even):
+// execution_plan.cpp:1046-1050.
+std::uint8_t quantize_byte(float v)
+{
+    const float c = std::clamp(v, 0.0F, 1.0F);
+    return static_cast<std::uint8_t>(std::nearbyint(c * 255.0F));
+}
+
+// Model output [3, mh, mw] -> frame: read_nhwc_fp16_to_yuv420,
+// execution_plan.cpp:1211-1322. The active region starts at (pad_top,
+// pad_left); each value is divided by pixel_range; chroma is the mean of
+// its 2x2 block summed as ((s00 + s01) + s10) + s11 then scaled by 0.25
+// (:1280-1291); a rotated frame reads the model transposed (:1296-1321).
+void model_to_yuv(const u16* x, int w, int h, int mw, int mh, int pad_left, int pad_top, int rotated, float range,
+                  std::uint8_t* yuv)
+{
+    const std::size_t ysz = static_cast<std::size_t>(w) * h, uvsz = ysz / 4;
+    const std::size_t plane = static_cast<std::size_t>(mw) * mh;
+    std::uint8_t* yo = yuv;
+    std::uint8_t* uo = yuv + ysz;
+    std::uint8_t* vo = uo + uvsz;
+    auto sample = [&](int c, int y, int xx) {
+        const int my = rotated ? xx + pad_top : y + pad_top;
+        const int mx = rotated ? y + pad_left : xx + pad_left;
+        return h2f(x[c * plane + static_cast<std::size_t>(my) * mw + mx]) / range;
+    };
+    for (int y = 0; y < h; ++y)
+        for (int xx = 0; xx < w; ++xx) yo[static_cast<std::size_t>(y) * w + xx] = quantize_byte(sample(0, y, xx));
+    for (int uy = 0; uy < h / 2; ++uy)
+        for (int ux = 0; ux < w / 2; ++ux) {
+            const std::size_t o = static_cast<std::size_t>(uy) * (w / 2) + ux;
+            float su, sv;
+            if (rotated) {
+                su = 0.0F;
+                sv = 0.0F;
+                for (int dy = 0; dy < 2; ++dy)
+                    for (int dx = 0; dx < 2; ++dx) {
+                        su += sample(1, 2 * uy + dy, 2 * ux + dx);
+                        sv += sample(2, 2 * uy + dy, 2 * ux + dx);
+                    }
+            } else {
+                su = sample(1, 2 * uy, 2 * ux) + sample(1, 2 * uy, 2 * ux + 1) + sample(1, 2 * uy + 1, 2 * ux) +
+                     sample(1, 2 * uy + 1, 2 * ux + 1);
+                sv = sample(2, 2 * uy, 2 * ux) + sample(2, 2 * uy, 2 * ux + 1) + sample(2, 2 * uy + 1, 2 * ux) +
+                     sample(2, 2 * uy + 1, 2 * ux + 1);
+            }
+            uo[o] = quantize_byte(su * 0.25F);
+            vo[o] = quantize_byte(sv * 0.25F);
+        }
+}
+
+// frame_padding, yuv.cpp:325-337: the frame fits as is, or transposed.
+void frame_padding(int w, int h, int mw, int mh, int* pad)
+{
+    auto bad = [](int a, int b) { return a <= 0 || b <= 0 || a % 2 || b % 2; };
+    if (bad(w, h) || bad(mw, mh)) throw std::runtime_error("YUV420 dimensions must be positive and even");
+    const bool native = w <= mw && h <= mh;
+    const bool rotated = h <= mw && w <= mh;
+    if (!native && !rotated) throw std::runtime_error("input frame is larger than the model dimensions");
+    const int aw = native ? w : h, ah = native ? h : w;
+    pad[0] = 0;
+    pad[1] = mw - aw;
+    pad[2] = 0;
+    pad[3] = mh - ah;
+    pad[4] = native ? 0 : 1;
+}
+
 extern "C" {
 
 const char* oracle_last_error(void) { return g_error.c_str(); }
@@ -1128,6 +1244,23 @@ int oracle_nchw_to_nhwc(const uint16_t* in, uint16_t* out, size_t n, size_t c, s
 int oracle_nhwc_to_nchw(const uint16_t* in, uint16_t* out, size_t n, size_t hw, size_t c)
 {
     return guard([&] { nhwc_to_nchw(in, out, n, hw, c); });
+}
+
+int oracle_yuv420_to_model(const uint8_t* yuv, int w, int h, int mw, int mh, int rotated, float pixel_range,
+                           uint16_t* out)
+{
+    return guard([&] { yuv_to_model(yuv, w, h, mw, mh, rotated, pixel_range, out); });
+}
+
+int oracle_model_to_yuv420(const uint16_t* x, int w, int h, int mw, int mh, int pad_left, int pad_top, int rotated,
+                           float pixel_range, uint8_t* yuv)
+{
+    return guard([&] { model_to_yuv(x, w, h, mw, mh, pad_left, pad_top, rotated, pixel_range, yuv); });
+}
+
+int oracle_frame_padding(int w, int h, int mw, int mh, int* pad5)
+{
+    return guard([&] { frame_padding(w, h, mw, mh, pad5); });
 }
 
 uint16_t oracle_float_to_half(float f) { return f2h(f); }

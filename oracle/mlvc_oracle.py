@@ -18,6 +18,7 @@ ORACLE_LIB = HERE / "liboracle.so"
 REF_LIB = HERE / "_ref" / "libmlvc_ref_kernels.so"
 
 _u16p = C.POINTER(C.c_uint16)
+_u8p = C.POINTER(C.c_uint8)
 _i64p = C.POINTER(C.c_int64)
 
 
@@ -70,6 +71,9 @@ def oracle_lib() -> C.CDLL:
         lib.oracle_io_count.argtypes = [C.c_void_p, C.c_int]
         lib.oracle_io_shape.argtypes = [C.c_void_p, C.c_int, C.c_int, _i64p, C.POINTER(C.c_int)]
         lib.oracle_run.argtypes = [C.c_void_p, C.POINTER(_u16p), C.POINTER(_u16p)]
+        lib.oracle_yuv420_to_model.argtypes = [_u8p] + [C.c_int] * 5 + [C.c_float, _u16p]
+        lib.oracle_model_to_yuv420.argtypes = [_u16p] + [C.c_int] * 7 + [C.c_float, _u8p]
+        lib.oracle_frame_padding.argtypes = [C.c_int] * 4 + [C.POINTER(C.c_int)]
         _oracle = lib
     return _oracle
 
@@ -85,6 +89,8 @@ def ref_lib() -> C.CDLL:
             raise OracleError(f"{REF_LIB} is not built (needs the reference checkout)")
         lib = C.CDLL(str(REF_LIB))
         _kernel_api(lib, "ref_")
+        lib.ref_prepare_model_input.argtypes = [_u8p] + [C.c_int] * 4 + [C.c_float, _u16p, C.POINTER(C.c_int)]
+        lib.ref_prepare_model_output.argtypes = [_u16p] + [C.c_int] * 4 + [C.c_float, C.POINTER(C.c_int), _u8p]
         _ref = lib
     return _ref
 
@@ -208,7 +214,9 @@ class OraclePlan:
             raise OracleError(self._lib.oracle_last_error().decode())
 
     def run(self, inputs) -> list[np.ndarray]:
-        ins = [np.ascontiguousarray(a, dtype=np.uint16) for a in inputs]
+        # FP16 inputs as uint16 bits; INT32 control inputs pass as raw bytes.
+        ins = [np.ascontiguousarray(a).view(np.uint16) if np.asarray(a).dtype == np.int32
+               else np.ascontiguousarray(a, dtype=np.uint16) for a in inputs]
         if len(ins) != len(self.in_shapes):
             raise OracleError("graph input count mismatch")
         outs = [np.empty(s, np.uint16) for s in self.out_shapes]
@@ -228,6 +236,69 @@ class OraclePlan:
             self.close()
         except Exception:
             pass
+
+
+# ---- codec I/O (frame <-> model image), I420 frames as flat uint8 arrays
+
+def yuv_frame_bytes(w: int, h: int) -> int:
+    return w * h + 2 * (w // 2) * (h // 2)
+
+
+def _check(lib, prefix, rc):
+    if rc != 0:
+        raise OracleError(getattr(lib, prefix + "last_error")().decode())
+
+
+def frame_padding(w: int, h: int, mw: int, mh: int) -> tuple:
+    """(left, right, top, bottom, rotated) of core/src/yuv.cpp:325-337."""
+    lib = oracle_lib()
+    pad = (C.c_int * 5)()
+    _check(lib, "oracle_", lib.oracle_frame_padding(w, h, mw, mh, pad))
+    return tuple(pad)
+
+
+def yuv_to_model(yuv: np.ndarray, w: int, h: int, mw: int, mh: int, rotated: int, pixel_range: float) -> np.ndarray:
+    """I420 frame -> FP16 bits [3, mh, mw]."""
+    lib = oracle_lib()
+    yuv = np.ascontiguousarray(yuv, np.uint8)
+    out = np.zeros((3, mh, mw), np.uint16)
+    _check(lib, "oracle_", lib.oracle_yuv420_to_model(yuv.ctypes.data_as(_u8p), w, h, mw, mh, rotated,
+                                                       pixel_range, out.ctypes.data_as(_u16p)))
+    return out
+
+
+def model_to_yuv(x: np.ndarray, w: int, h: int, pad: tuple, pixel_range: float) -> np.ndarray:
+    """FP16 bits [3, mh, mw] -> I420 frame; pad = (left, right, top, bottom, rotated)."""
+    lib = oracle_lib()
+    x = np.ascontiguousarray(x, np.uint16)
+    mh, mw = x.shape[-2], x.shape[-1]
+    out = np.zeros(yuv_frame_bytes(w, h), np.uint8)
+    _check(lib, "oracle_", lib.oracle_model_to_yuv420(x.ctypes.data_as(_u16p), w, h, mw, mh, pad[0], pad[2], pad[4],
+                                                       pixel_range, out.ctypes.data_as(_u8p)))
+    return out
+
+
+def ref_prepare_model_input(yuv: np.ndarray, w: int, h: int, mw: int, mh: int, pixel_range: float):
+    """The reference's prepare_model_input (core/src/yuv.cpp): (image, pad)."""
+    lib = ref_lib()
+    yuv = np.ascontiguousarray(yuv, np.uint8)
+    out = np.zeros((3, mh, mw), np.uint16)
+    pad = (C.c_int * 5)()
+    _check(lib, "ref_", lib.ref_prepare_model_input(yuv.ctypes.data_as(_u8p), w, h, mw, mh, pixel_range,
+                                                     out.ctypes.data_as(_u16p), pad))
+    return out, tuple(pad)
+
+
+def ref_prepare_model_output(x: np.ndarray, w: int, h: int, pad: tuple, pixel_range: float) -> np.ndarray:
+    """The reference's prepare_model_output_into (core/src/yuv.cpp)."""
+    lib = ref_lib()
+    x = np.ascontiguousarray(x, np.uint16)
+    mh, mw = x.shape[-2], x.shape[-1]
+    out = np.zeros(yuv_frame_bytes(w, h), np.uint8)
+    cpad = (C.c_int * 5)(*pad)
+    _check(lib, "ref_", lib.ref_prepare_model_output(x.ctypes.data_as(_u16p), w, h, mw, mh, pixel_range, cpad,
+                                                      out.ctypes.data_as(_u8p)))
+    return out
 
 
 def parity_stats(got: np.ndarray, want: np.ndarray) -> dict:

@@ -65,6 +65,13 @@ int oracle_depth_to_space_nhwc(const uint16_t* in, uint16_t* out, int n, int c, 
 int oracle_space_to_depth_nhwc(const uint16_t* in, uint16_t* out, int n, int c, int h, int w, int block);
 int oracle_nchw_to_nhwc(const uint16_t* in, uint16_t* out, size_t n, size_t c, size_t hw);
 int oracle_nhwc_to_nchw(const uint16_t* in, uint16_t* out, size_t n, size_t hw, size_t c);
+/* Codec I/O: I420 frame (w x h) <-> model image [3, mh, mw] FP16.
+ * pad5 = {left, right, top, bottom, rotated}. */
+int oracle_yuv420_to_model(const uint8_t* yuv, int w, int h, int mw, int mh, int rotated, float pixel_range,
+                           uint16_t* out);
+int oracle_model_to_yuv420(const uint16_t* x, int w, int h, int mw, int mh, int pad_left, int pad_top, int rotated,
+                           float pixel_range, uint8_t* yuv);
+int oracle_frame_padding(int w, int h, int mw, int mh, int* pad5);
 uint16_t oracle_float_to_half(float f);
 float oracle_half_to_float(uint16_t h);
 

@@ -2,7 +2,8 @@
 //
 // Built by oracle/build_ref.sh together with the reference's own sources
 // backends/cpu/src/{kernels_scalar,kernels_x86_avx2,thread_pool,cpu_features}.cpp
-// (compiled where they lie under the reference checkout) into
+// and core/src/yuv.cpp (compiled where they lie under the reference checkout)
+// into
 // oracle/_ref/libmlvc_ref_kernels.so. It exposes the kernel-level entry
 // points of oracle.h under a ref_ prefix so tests can compare the oracle's
 // restatement with the reference kernels on identical inputs. The graph-level
@@ -12,6 +13,7 @@
 
 #include "kernels_common.hpp"
 #include "mlvc/core/half.hpp"
+#include "mlvc/core/yuv.hpp"
 
 #include <cstdint>
 #include <cstring>
@@ -160,6 +162,43 @@ int ref_nchw_to_nhwc(const std::uint16_t* in, std::uint16_t* out, std::size_t n,
 int ref_nhwc_to_nchw(const std::uint16_t* in, std::uint16_t* out, std::size_t n, std::size_t hw, std::size_t c)
 {
     return guard([&] { get_x86_avx2_kernels().nhwc_to_nchw(in, out, n, hw, c, pool(1)); });
+}
+
+// core/src/yuv.cpp: prepare_model_input (frame -> [1, 3, mh, mw], padding
+// chosen by frame_padding) and prepare_model_output_into (model image ->
+// frame). pad5 = {left, right, top, bottom, rotated}.
+int ref_prepare_model_input(const std::uint8_t* yuv, int w, int h, int mw, int mh, float pixel_range,
+                            std::uint16_t* out, int* pad5)
+{
+    return guard([&] {
+        const std::size_t ysz = static_cast<std::size_t>(w) * h, uvsz = ysz / 4;
+        const Yuv420FrameView view(w, h, std::span<const std::uint8_t>(yuv, ysz),
+                                   std::span<const std::uint8_t>(yuv + ysz, uvsz),
+                                   std::span<const std::uint8_t>(yuv + ysz + uvsz, uvsz));
+        FramePadding pad;
+        const Tensor t = prepare_model_input(view, mw, mh, pixel_range, pad);
+        const auto& v = std::get<std::vector<Float16Storage>>(t.data);
+        std::memcpy(out, v.data(), v.size() * sizeof(Float16Storage));
+        pad5[0] = pad.left;
+        pad5[1] = pad.right;
+        pad5[2] = pad.top;
+        pad5[3] = pad.bottom;
+        pad5[4] = pad.rotated ? 1 : 0;
+    });
+}
+
+int ref_prepare_model_output(const std::uint16_t* x, int w, int h, int mw, int mh, float pixel_range, const int* pad5,
+                             std::uint8_t* yuv)
+{
+    return guard([&] {
+        Tensor t{"x_hat", {1, 3, mh, mw}, std::vector<Float16Storage>(x, x + static_cast<std::size_t>(3) * mw * mh)};
+        const std::size_t ysz = static_cast<std::size_t>(w) * h, uvsz = ysz / 4;
+        const MutableYuv420FrameView view(w, h, std::span<std::uint8_t>(yuv, ysz),
+                                          std::span<std::uint8_t>(yuv + ysz, uvsz),
+                                          std::span<std::uint8_t>(yuv + ysz + uvsz, uvsz));
+        FramePadding pad{pad5[0], pad5[1], pad5[2], pad5[3], pad5[4] != 0};
+        prepare_model_output_into(t, view, pixel_range, pad);
+    });
 }
 
 std::uint16_t ref_float_to_half(float f) { return float_to_half(f); }
