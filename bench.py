@@ -11,8 +11,10 @@ input already resident in HBM and the recurrent state carried on device.
 Prints one JSON line with frames/s (value), aggregate conv TFLOP/s and its
 fraction of the 2.5 PFLOP/s dense FP16 MFMA peak, the roofline position of
 the dominant kernel (timed live with HIP events on the backend stream) and
-the CPU oracle's frames/s on a bounded sample of the same workload. A
-per-kernel table goes to stderr.
+the CPU oracle's frames/s on a bounded sample of the same workload, and the
+codec I/O measurements around the encoder / decoder graphs (conversion
+kernels at 1080p, buffered end-to-end frames/s). A per-kernel table goes to
+stderr.
 """
 
 from __future__ import annotations
@@ -50,6 +52,142 @@ def kernel_table(gpu, reps: int):
         frac = tflops / PEAK_MFMA_TFLOPS if bound == "mfma" else gbs / PEAK_HBM_GBS
         rows.append(dict(l, ms=ms, ai=ai, bound=bound, tflops=tflops, gbs=gbs, frac=frac))
     return rows
+
+
+CODEC_SHAPE = (1920, 1080, 1920, 1088)  # 1080p I420 frame into the 1920x1088 model image
+
+
+def codec_io_kernels(reps: int) -> dict:
+    """Device-resident timing of the two codec I/O conversion kernels at the
+    1080p frame / 1920x1088 model shape (HIP events on one stream around
+    `reps` back-to-back launches). Algorithmic bytes: each tensor once (frame
+    bytes, FP16 model image; the frame side reads only the active area)."""
+    import ctypes as C
+
+    import numpy as np
+
+    import mlvc_hip
+
+    L = mlvc_hip.device_lib()
+    L.mlvc_hip_malloc.argtypes = [C.POINTER(C.c_void_p), C.c_size_t]
+    L.mlvc_hip_free.argtypes = [C.c_void_p]
+    L.mlvc_hip_memcpy_h2d.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t, C.c_void_p]
+    L.mlvc_hip_stream_create.argtypes = [C.POINTER(C.c_void_p)]
+    L.mlvc_hip_stream_destroy.argtypes = [C.c_void_p]
+    L.mlvc_hip_stream_synchronize.argtypes = [C.c_void_p]
+    L.mlvc_hip_event_create.argtypes = [C.POINTER(C.c_void_p)]
+    L.mlvc_hip_event_destroy.argtypes = [C.c_void_p]
+    L.mlvc_hip_event_record.argtypes = [C.c_void_p, C.c_void_p]
+    L.mlvc_hip_event_synchronize.argtypes = [C.c_void_p]
+    L.mlvc_hip_event_elapsed_ms.argtypes = [C.c_void_p, C.c_void_p, C.POINTER(C.c_float)]
+    L.mlvc_hip_yuv420_to_model.argtypes = [C.c_void_p, C.c_void_p, C.c_void_p] + [C.c_int] * 5 + [C.c_void_p]
+    L.mlvc_hip_model_to_yuv420.argtypes = [C.c_void_p, C.c_void_p] + [C.c_int] * 7 + [C.c_float, C.c_void_p]
+
+    def ok(rc):
+        if rc != 0:
+            raise mlvc_hip.MlvcError(L.mlvc_hip_last_error().decode())
+
+    w, h, mw, mh = CODEC_SHAPE
+    frame_bytes = w * h * 3 // 2
+    image_bytes = 3 * mw * mh * 2
+    rng = np.random.default_rng(0)
+    frame = rng.integers(0, 256, frame_bytes, dtype=np.uint8)
+    lut = (np.arange(256, dtype=np.float32) / np.float32(255.0)).astype(np.float16).view(np.uint16)
+    bufs = []
+
+    def put(a):
+        p = C.c_void_p()
+        ok(L.mlvc_hip_malloc(C.byref(p), a.nbytes))
+        ok(L.mlvc_hip_memcpy_h2d(p, a.ctypes.data, a.nbytes, None))
+        bufs.append(p)
+        return p
+
+    src, table = put(frame), put(lut)
+    image = C.c_void_p()
+    out = C.c_void_p()
+    ok(L.mlvc_hip_malloc(C.byref(image), image_bytes))
+    ok(L.mlvc_hip_malloc(C.byref(out), frame_bytes))
+    bufs += [image, out]
+    s, e0, e1 = C.c_void_p(), C.c_void_p(), C.c_void_p()
+    ok(L.mlvc_hip_stream_create(C.byref(s)))
+    ok(L.mlvc_hip_event_create(C.byref(e0)))
+    ok(L.mlvc_hip_event_create(C.byref(e1)))
+    ok(L.mlvc_hip_stream_synchronize(None))
+
+    def timed(launch):
+        for _ in range(3):
+            launch()
+        ok(L.mlvc_hip_event_record(e0, s))
+        for _ in range(reps):
+            launch()
+        ok(L.mlvc_hip_event_record(e1, s))
+        ok(L.mlvc_hip_event_synchronize(e1))
+        ms = C.c_float()
+        ok(L.mlvc_hip_event_elapsed_ms(e0, e1, C.byref(ms)))
+        return ms.value / reps * 1e3
+
+    to_model_us = timed(lambda: ok(L.mlvc_hip_yuv420_to_model(src, table, image, w, h, mw, mh, 0, s)))
+    to_frame_us = timed(lambda: ok(L.mlvc_hip_model_to_yuv420(image, out, w, h, mw, mh, 0, 0, 0, 1.0, s)))
+    for p in bufs:
+        L.mlvc_hip_free(p)
+    L.mlvc_hip_event_destroy(e0)
+    L.mlvc_hip_event_destroy(e1)
+    L.mlvc_hip_stream_destroy(s)
+    to_model_b = frame_bytes + image_bytes
+    to_frame_b = 3 * w * h * 2 + frame_bytes
+    return {"shape": f"{w}x{h} I420 frame <-> 1x3x{mh}x{mw} FP16 model image",
+            "frame_to_model_us": to_model_us, "frame_to_model_gbs": to_model_b / to_model_us / 1e3,
+            "frame_to_model_hbm_frac": to_model_b / to_model_us / 1e3 / PEAK_HBM_GBS,
+            "model_to_frame_us": to_frame_us, "model_to_frame_gbs": to_frame_b / to_frame_us / 1e3,
+            "model_to_frame_hbm_frac": to_frame_b / to_frame_us / 1e3 / PEAK_HBM_GBS,
+            "algorithmic_bytes": {"frame_to_model": to_model_b, "model_to_frame": to_frame_b}}
+
+
+def codec_buffered(frames: int) -> dict:
+    """End to end through BufferedCodecBackend at the 1080p frame shape: two
+    slots in flight, each submit uploading a pinned frame (encoder) or latent
+    (decoder), converting, replaying the frame graph and downloading the
+    latent (encoder) or frame (decoder). PCIe-inclusive; host time per frame."""
+    import numpy as np
+
+    import mlvc_hip
+
+    w, h, mw, mh = CODEC_SHAPE
+    res = {}
+    with tempfile.TemporaryDirectory() as d:
+        mlvc_hip.synth_write("codec_enc_1920x1088", d, 0)
+        mlvc_hip.synth_write("codec_dec_1920x1088", d, 0)
+        bindings, _ = mlvc_hip.synth_bindings("codec_enc_1920x1088")
+        rng = np.random.default_rng(1)
+        frame = rng.integers(0, 256, w * h * 3 // 2, dtype=np.uint8)
+        for model in ("MLVCEncoder", "MLVCDecoder"):
+            b = mlvc_hip.Backend(d, "hip")
+            b.load(model, bindings)
+            b.configure_codec_io(w, h, mw, mh, 1.0, slots=2)
+            b.reset_state()
+            enc = model == "MLVCEncoder"
+
+            def submit(slot):
+                if enc:
+                    b.encoder_input_yuv(slot)[:] = frame
+                    b.submit_encoder(slot, 5)
+                else:
+                    b.submit_decoder(slot, 5)
+
+            for i in range(4):  # warm-up
+                submit(i % 2)
+                b.wait_codec_slot(i % 2)
+            t0 = time.perf_counter()
+            for i in range(frames):
+                slot = i % 2
+                b.wait_codec_slot(slot)
+                submit(slot)
+            b.wait_codec_slot(0)
+            b.wait_codec_slot(1)
+            res[("encoder" if enc else "decoder") + "_frames_per_s"] = frames / (time.perf_counter() - t0)
+            b.close()
+    res["workload"] = "codec_enc/dec_1920x1088 (MLVCEncoder / MLVCDecoder pair), 1920x1080 I420 frames, 2 slots"
+    return res
 
 
 def cpu_baseline(model_dir, bindings, shape, budget_s: float):
@@ -142,6 +280,8 @@ def main() -> int:
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-codec", action="store_true", help="skip the codec I/O measurements")
+    ap.add_argument("--codec-frames", type=int, default=60)
     ap.add_argument("--api-frames", type=int, default=30,
                     help="frames timed through run() (host frame in, host reconstruction out)")
     ap.add_argument("--pmc-pass", default=None, metavar="I,J,...",
@@ -213,6 +353,13 @@ def main() -> int:
         if not args.no_cpu_baseline and rank == 0:
             base = cpu_baseline(d, bindings, shape, args.cpu_seconds)
         gpu.close()
+    codec = None
+    if not args.no_codec:
+        codec = codec_io_kernels(args.kernel_reps)
+        codec.update(codec_buffered(args.codec_frames))
+        log(f"codec I/O: frame->model {codec['frame_to_model_us']:.1f} us ({codec['frame_to_model_gbs']:.0f} GB/s), "
+            f"model->frame {codec['model_to_frame_us']:.1f} us ({codec['model_to_frame_gbs']:.0f} GB/s); buffered "
+            f"encoder {codec['encoder_frames_per_s']:.0f} frames/s, decoder {codec['decoder_frames_per_s']:.0f} frames/s")
 
     conv_tflops = conv_flops * fps / 1e12
     line = {
@@ -239,6 +386,7 @@ def main() -> int:
         "run_api_frames_per_s": api_fps,
         "roofline": roof,
         "cpu_baseline": base,
+        "codec_io": codec,
     }
     if rank == 0:
         print(json.dumps(line), flush=True)

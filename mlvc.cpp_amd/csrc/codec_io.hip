@@ -20,9 +20,9 @@
 //   for every pixel range.
 //
 // Both directions are HBM-bound byte/half streams: one thread converts 8
-// model columns (frame -> model) or a 2x8 luma block with its 4 U and 4 V
-// samples (model -> frame), with 4/8/16-byte accesses where the shapes keep
-// them aligned and a per-element path otherwise.
+// model columns (frame -> model) or a 2x4 luma block with its 2 U and 2 V
+// samples (model -> frame), with 2- to 16-byte accesses where the shapes
+// keep them aligned and a per-element path otherwise.
 
 #include "common.hpp"
 #include "mlvc_hip_device.h"
@@ -121,53 +121,76 @@ __global__ __launch_bounds__(kYuvThreads) void yuv_to_model_rotated_kernel(const
 }
 
 constexpr int kToYuvThreads = 128;
+constexpr int kChromaPerThread = 2;  // 2x4 luma pixels, 2 U and 2 V samples per thread
 
-// One thread: chroma samples [4t, 4t + 4) of chroma row uy, i.e. luma rows
-// 2uy, 2uy + 1 and columns [8t, 8t + 8) (grid x: column groups, y: chroma
+// value / pixel_range as the CPU backend computes it; x / 1 is exact, so the
+// unit-range instantiation has no IEEE division.
+template <bool UNIT>
+__device__ __forceinline__ float scaled(std::uint16_t h, float range)
+{
+    if constexpr (UNIT)
+        return h2f(h);
+    else
+        return h2f(h) / range;
+}
+
+// One thread: chroma samples [2t, 2t + 2) of chroma row uy, i.e. luma rows
+// 2uy, 2uy + 1 and columns [4t, 4t + 4) (grid x: column groups, y: chroma
 // rows).
+template <bool UNIT>
 __global__ __launch_bounds__(kToYuvThreads) void model_to_yuv_kernel(const std::uint16_t* __restrict__ x,
                                                                      std::uint8_t* __restrict__ yuv, int w, int h,
                                                                      int mw, int mh, int pad_left, int pad_top,
                                                                      float range)
 {
+    constexpr int CPT = kChromaPerThread, LPT = 2 * CPT;  // chroma / luma columns per thread
     const int t = blockIdx.x * kToYuvThreads + threadIdx.x;
     const int uy = blockIdx.y;
     const int uw = w / 2;
-    const int ux0 = t * 4;
+    const int ux0 = t * CPT;
     if (ux0 >= uw) return;
     const size_t plane = static_cast<size_t>(mw) * mh;
     const size_t ysz = static_cast<size_t>(w) * h, uvsz = ysz / 4;
-    const int n = min(4, uw - ux0);  // chroma samples of this thread
+    const int n = min(CPT, uw - ux0);  // chroma samples of this thread
     const int col0 = pad_left + 2 * ux0;
     const size_t r0 = static_cast<size_t>(pad_top + 2 * uy) * mw + col0;
     const size_t r1 = r0 + mw;
-    // Sixteen luma and sixteen of each chroma plane: two rows of 8 columns.
-    float s[3][2][8];
-    const bool vec = n == 4 && (col0 & 7) == 0 && (mw & 7) == 0;
+    float s[3][2][LPT];
+    // One branch around all six row loads, so they are all in flight before
+    // the first wait (a branch per load would wait after each).
+    if (n == CPT && (col0 % LPT) == 0 && (mw % LPT) == 0) {
+        uint2 q[3][2];
 #pragma unroll
-    for (int c = 0; c < 3; ++c)
+        for (int c = 0; c < 3; ++c)
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            const std::uint16_t* src = x + static_cast<size_t>(c) * plane + (r ? r1 : r0);
-            if (vec) {
-                const u32x4 q = *reinterpret_cast<const u32x4*>(src);
+            for (int r = 0; r < 2; ++r)
+                q[c][r] = *reinterpret_cast<const uint2*>(x + static_cast<size_t>(c) * plane + (r ? r1 : r0));
 #pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    s[c][r][2 * k] = h2f(static_cast<std::uint16_t>(q[k] & 0xFFFFu)) / range;
-                    s[c][r][2 * k + 1] = h2f(static_cast<std::uint16_t>(q[k] >> 16)) / range;
-                }
-            } else {
+        for (int c = 0; c < 3; ++c)
 #pragma unroll
-                for (int k = 0; k < 8; ++k) s[c][r][k] = k < 2 * n ? h2f(src[k]) / range : 0.0F;
+            for (int r = 0; r < 2; ++r) {
+                s[c][r][0] = scaled<UNIT>(static_cast<std::uint16_t>(q[c][r].x & 0xFFFFu), range);
+                s[c][r][1] = scaled<UNIT>(static_cast<std::uint16_t>(q[c][r].x >> 16), range);
+                s[c][r][2] = scaled<UNIT>(static_cast<std::uint16_t>(q[c][r].y & 0xFFFFu), range);
+                s[c][r][3] = scaled<UNIT>(static_cast<std::uint16_t>(q[c][r].y >> 16), range);
             }
-        }
-    std::uint8_t yb[2][8], ub[4], vb[4];
+    } else {
+#pragma unroll
+        for (int c = 0; c < 3; ++c)
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                const std::uint16_t* src = x + static_cast<size_t>(c) * plane + (r ? r1 : r0);
+#pragma unroll
+                for (int k = 0; k < LPT; ++k) s[c][r][k] = k < 2 * n ? scaled<UNIT>(src[k], range) : 0.0F;
+            }
+    }
+    std::uint8_t yb[2][LPT], ub[CPT], vb[CPT];
 #pragma unroll
     for (int r = 0; r < 2; ++r)
 #pragma unroll
-        for (int k = 0; k < 8; ++k) yb[r][k] = quantize_byte(s[0][r][k]);
+        for (int k = 0; k < LPT; ++k) yb[r][k] = quantize_byte(s[0][r][k]);
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
+    for (int k = 0; k < CPT; ++k) {
         const float su = s[1][0][2 * k] + s[1][0][2 * k + 1] + s[1][1][2 * k] + s[1][1][2 * k + 1];
         const float sv = s[2][0][2 * k] + s[2][0][2 * k + 1] + s[2][1][2 * k] + s[2][1][2 * k + 1];
         ub[k] = quantize_byte(su * 0.25F);
@@ -176,18 +199,13 @@ __global__ __launch_bounds__(kToYuvThreads) void model_to_yuv_kernel(const std::
     std::uint8_t* yo = yuv + static_cast<size_t>(2 * uy) * w + 2 * ux0;
     std::uint8_t* uo = yuv + ysz + static_cast<size_t>(uy) * uw + ux0;
     std::uint8_t* vo = uo + uvsz;
-    if (n == 4 && (w & 7) == 0) {
+    if (n == CPT && (w % LPT) == 0) {
 #pragma unroll
-        for (int r = 0; r < 2; ++r) {
-            uint2 q;
-            q.x = yb[r][0] | (yb[r][1] << 8) | (yb[r][2] << 16) | (static_cast<std::uint32_t>(yb[r][3]) << 24);
-            q.y = yb[r][4] | (yb[r][5] << 8) | (yb[r][6] << 16) | (static_cast<std::uint32_t>(yb[r][7]) << 24);
-            *reinterpret_cast<uint2*>(yo + static_cast<size_t>(r) * w) = q;
-        }
-        *reinterpret_cast<std::uint32_t*>(uo) =
-            ub[0] | (ub[1] << 8) | (ub[2] << 16) | (static_cast<std::uint32_t>(ub[3]) << 24);
-        *reinterpret_cast<std::uint32_t*>(vo) =
-            vb[0] | (vb[1] << 8) | (vb[2] << 16) | (static_cast<std::uint32_t>(vb[3]) << 24);
+        for (int r = 0; r < 2; ++r)
+            *reinterpret_cast<std::uint32_t*>(yo + static_cast<size_t>(r) * w) =
+                yb[r][0] | (yb[r][1] << 8) | (yb[r][2] << 16) | (static_cast<std::uint32_t>(yb[r][3]) << 24);
+        *reinterpret_cast<std::uint16_t*>(uo) = static_cast<std::uint16_t>(ub[0] | (ub[1] << 8));
+        *reinterpret_cast<std::uint16_t*>(vo) = static_cast<std::uint16_t>(vb[0] | (vb[1] << 8));
     } else {
         for (int k = 0; k < n; ++k) {
             yo[2 * k] = yb[0][2 * k];
@@ -212,7 +230,8 @@ __global__ __launch_bounds__(kYuvThreads) void model_to_yuv_rotated_kernel(const
     const size_t ysz = static_cast<size_t>(w) * h, uvsz = ysz / 4;
     const int uw = w / 2;
     auto sample = [&](int c, int fy, int fx) {
-        return h2f(x[static_cast<size_t>(c) * plane + static_cast<size_t>(fx + pad_top) * mw + fy + pad_left]) / range;
+        return scaled<false>(x[static_cast<size_t>(c) * plane + static_cast<size_t>(fx + pad_top) * mw + fy + pad_left],
+                             range);
     };
     for (size_t i = static_cast<size_t>(blockIdx.x) * kYuvThreads + threadIdx.x; i < ysz;
          i += static_cast<size_t>(gridDim.x) * kYuvThreads) {
@@ -290,10 +309,14 @@ int mlvc_hip_model_to_yuv420(const void* x, uint8_t* yuv, int w, int h, int mw, 
                                dim3(kYuvThreads), 0, to_stream(s), xi, yuv, w, h, mw, mh, pad_left, pad_top,
                                pixel_range);
         } else {
-            const int groups = (w / 2 + 3) / 4;
+            const int groups = (w / 2 + kChromaPerThread - 1) / kChromaPerThread;
             const dim3 grid((groups + kToYuvThreads - 1) / kToYuvThreads, h / 2);
-            hipLaunchKernelGGL(model_to_yuv_kernel, grid, dim3(kToYuvThreads), 0, to_stream(s), xi, yuv, w, h, mw, mh,
-                               pad_left, pad_top, pixel_range);
+            if (pixel_range == 1.0F)
+                hipLaunchKernelGGL(model_to_yuv_kernel<true>, grid, dim3(kToYuvThreads), 0, to_stream(s), xi, yuv, w, h,
+                                   mw, mh, pad_left, pad_top, pixel_range);
+            else
+                hipLaunchKernelGGL(model_to_yuv_kernel<false>, grid, dim3(kToYuvThreads), 0, to_stream(s), xi, yuv, w, h,
+                                   mw, mh, pad_left, pad_top, pixel_range);
         }
         check(hipGetLastError(), "codec I/O kernel launch");
     });
