@@ -218,6 +218,76 @@ int mlvc_hip_concat_channels(const void* a, int ca, const void* b, int cb, void*
 /* Zero fill by kernel (safe inside captured graphs). */
 int mlvc_hip_zero(void* y, size_t bytes, mlvc_hip_stream s);
 
+/* ---- operators of the real MLVC graphs (NCHW FP16) ----
+ * Same values as the reference CPU kernels (backends/cpu/src/
+ * kernels_scalar.cpp:80-110, 244-537; kernels_x86_avx2.cpp:30-62, 304-712)
+ * computed per element in FP32 with one RNE rounding per materialised value;
+ * the driver backend's counterparts are kernels/elementwise.cu,
+ * tensor_ops.cu, activation.cu, recurrent_feature.cu and
+ * quantization_tail.cu. Buffers of the vector paths are 16-byte aligned. */
+enum { MLVC_UNARY_CLIP = 0, MLVC_UNARY_SIGMOID = 1, MLVC_UNARY_RECIPROCAL = 2, MLVC_UNARY_ROUND = 3 };
+/* CLIP to [lo, hi] (NaN -> hi, as the reference's vector lanes), SIGMOID
+ * with the reference's vector exponential, 1/x, round half to even. */
+int mlvc_hip_unary(const void* x, void* y, size_t count, int op, float lo, float hi, mlvc_hip_stream s);
+enum { MLVC_BINARY_ADD = 0, MLVC_BINARY_SUB = 1, MLVC_BINARY_MUL = 2 };
+/* y = a op b on right-aligned 4-D dims; an operand dim of 1 broadcasts. */
+int mlvc_hip_binary(const void* a, const int64_t* a_dims, const void* b, const int64_t* b_dims, void* y,
+                    const int64_t* y_dims, int op, mlvc_hip_stream s);
+/* y[i] = x[starts + i * steps] per dim (4-D); every read must lie in x. */
+int mlvc_hip_slice(const void* x, const int64_t* x_dims, void* y, const int64_t* y_dims, const int64_t* starts,
+                   const int64_t* steps, mlvc_hip_stream s);
+/* rows x row_elems block copy between row strides (a CONCAT input placed
+ * into its output). */
+int mlvc_hip_copy_rows(const void* x, void* y, size_t rows, size_t row_elems, size_t x_stride, size_t y_stride,
+                       mlvc_hip_stream s);
+/* y[o][i][r] = data[o][indices[i]][r] for data viewed as [outer, axis_dim,
+ * inner]; indices int32 or int64 in device memory, negative ones count from
+ * the end; the caller checks the range (the kernel clamps). */
+int mlvc_hip_gather(const void* data, const void* indices, int indices_int64, size_t count, size_t outer,
+                    size_t axis_dim, size_t inner, void* y, mlvc_hip_stream s);
+/* x [n, 2G, hw] -> y [n, G, hw] = fp16(fp16(clamp(gate, lo, hi)) * linear)
+ * (reglu_nhwc, kernels_scalar.cpp:304-322). */
+int mlvc_hip_reglu(const void* x, void* y, int n, int gate_channels, size_t hw, float lo, float hi, mlvc_hip_stream s);
+/* Recurrent feature update (feature_update[_outputs]_nhwc,
+ * kernels_scalar.cpp:324-405): x [n, 3C, hw], history [n, C, hw], scale [C]
+ * -> feature [n, 2C, hw] = scaled | blended; scaled / blended [n, C, hw]
+ * also written when both are non-null. */
+int mlvc_hip_feature_update(const void* x, const void* history, const void* scale, void* feature, void* scaled,
+                            void* blended, int n, int channels, size_t hw, mlvc_hip_stream s);
+/* y0 / y1 quantisation tails (kernels_scalar.cpp:407-537); planes of
+ * [n, 2q, hw] unless noted: prior [n, 4q, hw] (y0) or [n, 2q, hw] (y1),
+ * update scales and y_raw [n, q, hw], concat3 [n, 6q, hw]. */
+typedef struct mlvc_hip_y0_tail_desc {
+    const void* latent;
+    const void* prior;
+    const void* quant_scale;
+    const void* update_scale0;
+    const void* update_scale1;
+    void* normalized;
+    void* clipped;
+    void* y_raw;
+    void* concat2;
+    void* concat3;
+    int n, q;
+    size_t hw;
+    float clip_min;
+} mlvc_hip_y0_tail_desc;
+int mlvc_hip_y0_tail(const mlvc_hip_y0_tail_desc* desc, mlvc_hip_stream s);
+typedef struct mlvc_hip_y1_tail_desc {
+    const void* normalized;
+    const void* prior;
+    const void* quant_scale;
+    const void* update_scale0;
+    const void* update_scale1;
+    const void* concat2;
+    const void* clipped;
+    void* y_raw;
+    void* out;
+    int n, q;
+    size_t hw;
+} mlvc_hip_y1_tail_desc;
+int mlvc_hip_y1_tail(const mlvc_hip_y1_tail_desc* desc, mlvc_hip_stream s);
+
 #ifdef __cplusplus
 }
 #endif

@@ -108,9 +108,22 @@ struct HostMem {
 };
 
 struct Launch {
-    enum Kind { kConv, kDepthwise, kDwBlock, kPair, kLeaky, kAdd, kD2S, kS2D, kConcat } kind = kConv;
+    enum Kind {
+        kConv, kDepthwise, kDwBlock, kPair, kLeaky, kAdd, kD2S, kS2D, kConcat,
+        kUnary, kBinary, kSlice, kConcatAny, kGather, kReglu, kFeature, kY0, kY1
+    } kind = kConv;
     std::string name, kind_name;
     TensorId x = 0, x2 = 0, res = 0, y = 0;  // tensors read (x, x2, res) and written (y)
+    std::vector<TensorId> ins, outs;         // further tensors read / written
+    int op = 0;
+    float lo = 0.0F, hi = 0.0F;
+    std::int64_t da[4] = {}, db[4] = {}, dy[4] = {}, starts[4] = {}, steps[4] = {};
+    struct Piece {
+        std::size_t rows, row_elems, y_offset, y_stride;
+    };
+    std::vector<Piece> pieces;  // CONCAT: one block copy per input (ins)
+    std::size_t outer = 0, dim = 0, inner = 0;
+    bool idx64 = false;
     mlvc_hip_conv_desc conv{};
     mlvc_hip_dwblock_desc blk{};
     mlvc_hip_convpair_desc pair{};
@@ -274,6 +287,8 @@ public:
     {
         CodecSlot& sl = idle_slot(index, true, "encoder");
         if (!initialized_) fail("reset_state() must be called before submit_encoder()");
+        const std::int32_t q32 = static_cast<std::int32_t>(shifted_q);
+        check_gather_indices(static_cast<std::size_t>(codec_q_), &q32);
         select();
         hip_check(mlvc_hip_memcpy_h2d(codec_frame_.ptr, sl.frame.ptr, codec_frame_bytes_, stream_), "frame upload");
         const FramePadding& pad = codec_.padding;
@@ -318,6 +333,8 @@ public:
     {
         CodecSlot& sl = idle_slot(index, false, "decoder");
         if (!initialized_) fail("reset_state() must be called before submit_decoder()");
+        const std::int32_t q32 = static_cast<std::int32_t>(shifted_q);
+        check_gather_indices(static_cast<std::size_t>(codec_q_), &q32);
         select();
         for (std::size_t i = 0; i < ext_in_.size(); ++i) {
             if (static_cast<int>(i) == codec_q_) continue;
@@ -374,6 +391,7 @@ public:
             const auto& d = desc(ext_in_[i]);
             if (t.shape != d.shape || t.data_type() != public_dtype(d.dtype) || t.byte_size() != aot::tensor_bytes(d))
                 fail("graph input shape, dtype, or byte size mismatch");
+            check_gather_indices(i, t.raw_data());
             std::memcpy(in_stage_[i].ptr, t.raw_data(), t.byte_size());
             hip_check(mlvc_hip_memcpy_h2d(input_buf_.at(ext_in_[i]).ptr, in_stage_[i].ptr, t.byte_size(), stream_), "input upload");
         }
@@ -398,6 +416,7 @@ public:
     void upload_inputs(const std::vector<const void*>& inputs)
     {
         if (inputs.size() != ext_in_.size()) fail("graph input count mismatch");
+        for (std::size_t i = 0; i < inputs.size(); ++i) check_gather_indices(i, inputs[i]);
         select();
         for (std::size_t i = 0; i < inputs.size(); ++i)
             hip_check(mlvc_hip_memcpy_h2d(input_buf_.at(ext_in_[i]).ptr, inputs[i], aot::tensor_bytes(desc(ext_in_[i])), stream_),
@@ -494,7 +513,7 @@ private:
             state_out_[out] = bindings_.size() - 1;
         }
         // FP16 activations, plus INT32 control inputs such as q_index_shifted
-        // (consumed by no kernel on this path; an operator reading one is
+        // (read only as GATHER indices; any other operator reading one is
         // rejected when the graph is lowered).
         for (TensorId id : g.inputs) {
             const auto dt = desc(id).dtype;
@@ -508,12 +527,605 @@ private:
         }
     }
 
+    // ------------------------------------- real-model pattern matching
+    // The reference CPU matcher's patterns (fusion_matcher.cpp:78-850): a
+    // matched chain becomes one kernel that writes every tensor of the chain
+    // that is read outside it. The matcher's consumer-count and shape rules
+    // are kept, so exactly the chains it fuses are fused here.
+    bool graph_output(TensorId id) const
+    {
+        const auto& o = graph_.descriptor.outputs;
+        return std::find(o.begin(), o.end(), id) != o.end();
+    }
+    bool internal_only(TensorId id, int n) const
+    {
+        const auto it = consumers_.find(id);
+        return id && !graph_output(id) && (it == consumers_.end() ? 0 : it->second) == n;
+    }
+    bool named(TensorId id) const
+    {
+        return id && id < graph_.descriptor.tensors.size() && !desc(id).name.empty();
+    }
+    std::vector<std::uint8_t> weight_bytes(TensorId id) const
+    {
+        const auto& w = std::get<aot::WeightLocation>(desc(id).storage);
+        const auto* p = reinterpret_cast<const std::uint8_t*>(graph_.weights.data()) + w.offset;
+        return std::vector<std::uint8_t>(p, p + w.bytes);
+    }
+    bool int64_init(TensorId id, std::vector<std::int64_t>& v) const
+    {
+        if (!named(id) || !is_weight(id) || desc(id).dtype != aot::DataType::INT64) return false;
+        const auto raw = weight_bytes(id);
+        if (raw.size() % 8) return false;
+        v.resize(raw.size() / 8);
+        if (!raw.empty()) std::memcpy(v.data(), raw.data(), raw.size());
+        return true;
+    }
+    bool fp16_scalar_init(TensorId id, float& v) const
+    {
+        if (!named(id) || !is_weight(id) || desc(id).dtype != aot::DataType::FP16) return false;
+        const auto raw = weight_bytes(id);
+        if (raw.size() != 2) return false;
+        std::uint16_t h;
+        std::memcpy(&h, raw.data(), 2);
+        v = half_to_float(h);
+        return true;
+    }
+    static int axis_of(const aot::Node& n)
+    {
+        const auto* a = std::get_if<aot::AxisAttributes>(&n.attributes);
+        return a ? a->axis : 0;
+    }
+    bool clip_constants(const aot::Node& n, float& lo, float& hi) const
+    {
+        if (n.op != Op::CLIP || n.inputs.size() < 2 || n.outputs.size() != 1) return false;
+        lo = -HUGE_VALF;
+        hi = HUGE_VALF;
+        if (n.inputs[1] && !fp16_scalar_init(n.inputs[1], lo)) return false;
+        if (n.inputs.size() >= 3 && n.inputs[2] && !fp16_scalar_init(n.inputs[2], hi)) return false;
+        return true;
+    }
+    bool channel_slice(const aot::Node& n, TensorId x, std::int64_t b, std::int64_t e) const
+    {
+        if (n.op != Op::SLICE || n.inputs.size() < 3 || n.outputs.size() != 1 || n.inputs[0] != x) return false;
+        std::vector<std::int64_t> st, en, ax, sp;
+        if (!int64_init(n.inputs[1], st) || !int64_init(n.inputs[2], en) || st.size() != 1 || en.size() != 1 || st[0] != b ||
+            en[0] != e)
+            return false;
+        if (n.inputs.size() < 4 || !n.inputs[3] || !int64_init(n.inputs[3], ax) || ax.size() != 1 || ax[0] != 1) return false;
+        if (n.inputs.size() >= 5 && n.inputs[4] && (!int64_init(n.inputs[4], sp) || sp.size() != 1 || sp[0] != 1)) return false;
+        const auto& o = desc(n.outputs[0]);
+        return o.dtype == aot::DataType::FP16 && o.shape.size() == 4 && o.shape[1] == e - b;
+    }
+    static bool pair(const aot::Node& n, Op op, TensorId x, TensorId y)
+    {
+        return n.op == op && n.inputs.size() == 2 && n.outputs.size() == 1 &&
+               ((n.inputs[0] == x && n.inputs[1] == y) || (n.inputs[0] == y && n.inputs[1] == x));
+    }
+    static bool other_in_pair(const aot::Node& n, Op op, TensorId x, TensorId& other)
+    {
+        if (n.op != op || n.inputs.size() != 2 || n.outputs.size() != 1) return false;
+        if (n.inputs[0] == x) { other = n.inputs[1]; return true; }
+        if (n.inputs[1] == x) { other = n.inputs[0]; return true; }
+        return false;
+    }
+    bool fp16_of(TensorId id, const std::vector<std::int64_t>& shape) const
+    {
+        return named(id) && desc(id).dtype == aot::DataType::FP16 && desc(id).shape == shape;
+    }
+    bool fp16_4d(TensorId id) const { return named(id) && desc(id).dtype == aot::DataType::FP16 && desc(id).shape.size() == 4; }
+
+    // try_reglu (fusion_matcher.cpp:304-346): SLICE [0,G) / [G,2G) of x ->
+    // CLIP(gate) -> MUL(clipped, linear). A 1x1 conv producing x is lowered on
+    // its own, so this also covers try_pointwise_reglu (:258-302).
+    bool match_reglu(std::size_t i, Launch& L, std::vector<bool>& done)
+    {
+        const auto& ns = nodes();
+        if (i + 4 > ns.size() || ns[i].op != Op::SLICE || ns[i].inputs.empty()) return false;
+        const TensorId x = ns[i].inputs[0];
+        if (!fp16_4d(x) || desc(x).shape[1] <= 0 || desc(x).shape[1] % 2) return false;
+        const std::int64_t g = desc(x).shape[1] / 2;
+        if (!channel_slice(ns[i], x, 0, g) || !channel_slice(ns[i + 1], x, g, 2 * g)) return false;
+        const TensorId gate = ns[i].outputs[0], lin = ns[i + 1].outputs[0];
+        if (!internal_only(gate, 1) || !internal_only(lin, 1)) return false;
+        float lo, hi;
+        if (!clip_constants(ns[i + 2], lo, hi) || ns[i + 2].inputs[0] != gate) return false;
+        const TensorId clipped = ns[i + 2].outputs[0];
+        if (!internal_only(clipped, 1) || !pair(ns[i + 3], Op::MUL, clipped, lin)) return false;
+        const auto& s = desc(x).shape;
+        if (desc(ns[i + 3].outputs[0]).shape != std::vector<std::int64_t>{s[0], g, s[2], s[3]}) return false;
+        L.kind = Launch::kReglu;
+        L.kind_name = "reglu";
+        L.x = x;
+        L.y = ns[i + 3].outputs[0];
+        L.n = static_cast<int>(s[0]);
+        L.c = static_cast<int>(g);
+        L.hw = static_cast<std::size_t>(s[2] * s[3]);
+        L.lo = lo;
+        L.hi = hi;
+        L.bytes = 2.0 * static_cast<double>(elem_count(s)) * 1.5;
+        for (std::size_t k = i; k < i + 4; ++k) done[k] = true;
+        return true;
+    }
+
+    // try_feature_update (fusion_matcher.cpp:413-541).
+    bool match_feature(std::size_t i, Launch& L, std::vector<bool>& done)
+    {
+        const auto& ns = nodes();
+        if (i + 11 > ns.size() || ns[i].op != Op::SLICE || ns[i].inputs.empty()) return false;
+        const TensorId x = ns[i].inputs[0];
+        if (!fp16_4d(x) || desc(x).shape[1] <= 0 || desc(x).shape[1] % 3) return false;
+        const std::int64_t ch = desc(x).shape[1] / 3;
+        if (!channel_slice(ns[i], x, 0, ch) || !channel_slice(ns[i + 1], x, ch, 2 * ch) || !channel_slice(ns[i + 2], x, 2 * ch, 3 * ch))
+            return false;
+        const TensorId a = ns[i].outputs[0], b = ns[i + 1].outputs[0], cg = ns[i + 2].outputs[0];
+        if (!internal_only(a, 1) || !internal_only(b, 1) || !internal_only(cg, 1)) return false;
+        const aot::Node& s0 = ns[i + 3];
+        const aot::Node& s1 = ns[i + 4];
+        if (s0.op != Op::SIGMOID || s0.inputs.size() != 1 || s0.inputs[0] != b || s0.outputs.size() != 1 || s1.op != Op::SIGMOID ||
+            s1.inputs.size() != 1 || s1.inputs[0] != cg || s1.outputs.size() != 1)
+            return false;
+        const TensorId sb = s0.outputs[0], sc = s1.outputs[0];
+        if (!internal_only(sb, 2) || !internal_only(sc, 1)) return false;
+        TensorId hist = 0;
+        if (!other_in_pair(ns[i + 5], Op::MUL, sb, hist) || !named(hist) || is_weight(hist) || !fp16_of(hist, desc(a).shape)) return false;
+        const TensorId wb = ns[i + 5].outputs[0];
+        if (!internal_only(wb, 1)) return false;
+        const aot::Node& sub = ns[i + 6];
+        if (sub.op != Op::SUB || sub.inputs.size() != 2 || sub.outputs.size() != 1 || sub.inputs[1] != sb) return false;
+        float one = 0.0F;
+        if (!fp16_scalar_init(sub.inputs[0], one) || std::fabs(one - 1.0F) > 1e-4F) return false;
+        const TensorId inv = sub.outputs[0];
+        if (!internal_only(inv, 1) || !pair(ns[i + 7], Op::MUL, inv, a)) return false;
+        const TensorId wa = ns[i + 7].outputs[0];
+        if (!internal_only(wa, 1) || !pair(ns[i + 8], Op::ADD, wb, wa)) return false;
+        const TensorId blended = ns[i + 8].outputs[0];
+        if (!pair(ns[i + 9], Op::MUL, sc, blended)) return false;
+        const TensorId gated = ns[i + 9].outputs[0];
+        if (!internal_only(gated, 1)) return false;
+        TensorId scale = 0;
+        if (!other_in_pair(ns[i + 10], Op::MUL, gated, scale) || !fp16_of(scale, {1, ch, 1, 1})) return false;
+        const TensorId scaled = ns[i + 10].outputs[0];
+        auto concat_of = [&](const aot::Node& c) {
+            return c.op == Op::CONCAT && axis_of(c) == 1 && c.inputs.size() == 2 && c.inputs[0] == scaled && c.inputs[1] == blended &&
+                   c.outputs.size() == 1;
+        };
+        std::size_t cat = 0, end = 0;
+        if (i + 12 <= ns.size() && internal_only(scaled, 1) && internal_only(blended, 2) && concat_of(ns[i + 11])) {
+            cat = i + 11;
+            end = i + 12;
+        } else if (!graph_output(scaled) && internal_only(blended, 2)) {
+            for (std::size_t j = i + 11; j < ns.size() && !cat; ++j)
+                if (concat_of(ns[j])) cat = j;
+            end = i + 11;
+            if (cat) {
+                L.outs = {scaled, blended};
+            }
+        }
+        if (!cat) return false;
+        const auto& s = desc(x).shape;
+        const std::vector<std::int64_t> cs{s[0], ch, s[2], s[3]}, fs{s[0], 2 * ch, s[2], s[3]};
+        if (desc(ns[cat].outputs[0]).shape != fs || desc(scaled).shape != cs || desc(blended).shape != cs) return false;
+        L.kind = Launch::kFeature;
+        L.kind_name = L.outs.empty() ? "feature_update" : "feature_update_outputs";
+        L.x = x;
+        L.ins = {hist, scale};
+        L.y = ns[cat].outputs[0];
+        L.n = static_cast<int>(s[0]);
+        L.c = static_cast<int>(ch);
+        L.hw = static_cast<std::size_t>(s[2] * s[3]);
+        const double plane = 2.0 * static_cast<double>(s[0] * s[2] * s[3]);
+        L.bytes = plane * static_cast<double>(ch) * (3 + 1 + 2 + (L.outs.empty() ? 0 : 2));
+        for (std::size_t k = i; k < end; ++k) done[k] = true;
+        done[cat] = true;
+        return true;
+    }
+
+    // The update shared by both quantisation tails (fusion_matcher.cpp:
+    // 620-697, 760-836), from node k with `scaled` matched.
+    std::size_t match_update(std::size_t k, TensorId scaled, TensorId tail, std::int64_t q, const std::vector<std::int64_t>& qshape,
+                             TensorId& y_raw, TensorId& u0, TensorId& u1, TensorId& us0, TensorId& us1) const
+    {
+        const auto& ns = nodes();
+        if (!channel_slice(ns[k], scaled, 0, q) || !channel_slice(ns[k + 1], scaled, q, 2 * q)) return 0;
+        const TensorId h0 = ns[k].outputs[0], h1 = ns[k + 1].outputs[0];
+        if (!internal_only(h0, 1) || !internal_only(h1, 1) || !pair(ns[k + 2], Op::ADD, h0, h1)) return 0;
+        const TensorId sum = ns[k + 2].outputs[0];
+        if (!internal_only(sum, 1)) return 0;
+        const aot::Node& rnd = ns[k + 3];
+        if (rnd.op != Op::ROUND || rnd.inputs.size() != 1 || rnd.inputs[0] != sum || rnd.outputs.size() != 1) return 0;
+        y_raw = rnd.outputs[0];
+        if (!channel_slice(ns[k + 4], tail, 0, q) || !channel_slice(ns[k + 5], tail, q, 2 * q)) return 0;
+        const TensorId t0 = ns[k + 4].outputs[0], t1 = ns[k + 5].outputs[0];
+        if (!internal_only(t0, 1) || !internal_only(t1, 1) || !pair(ns[k + 6], Op::ADD, y_raw, t0)) return 0;
+        const TensorId a0 = ns[k + 6].outputs[0];
+        if (!internal_only(a0, 1) || !other_in_pair(ns[k + 7], Op::MUL, a0, us0) || !fp16_of(us0, qshape)) return 0;
+        u0 = ns[k + 7].outputs[0];
+        if (!internal_only(u0, 1) || !pair(ns[k + 8], Op::ADD, y_raw, t1)) return 0;
+        const TensorId a1 = ns[k + 8].outputs[0];
+        if (!internal_only(a1, 1) || !other_in_pair(ns[k + 9], Op::MUL, a1, us1) || !fp16_of(us1, qshape)) return 0;
+        u1 = ns[k + 9].outputs[0];
+        if (!internal_only(u1, 1)) return 0;
+        return k + 10;
+    }
+
+    // try_y0_tail (fusion_matcher.cpp:543-696).
+    bool match_y0(std::size_t i, Launch& L, std::vector<bool>& done)
+    {
+        const auto& ns = nodes();
+        if (i + 19 > ns.size() || ns[i].op != Op::SLICE || ns[i].inputs.empty()) return false;
+        const TensorId prior = ns[i].inputs[0];
+        if (!fp16_4d(prior) || desc(prior).shape[1] <= 0 || desc(prior).shape[1] % 4) return false;
+        const auto& ps = desc(prior).shape;
+        const std::int64_t q = ps[1] / 4;
+        if (!channel_slice(ns[i], prior, 0, 2 * q) || !channel_slice(ns[i + 1], prior, 2 * q, 4 * q)) return false;
+        const TensorId head = ns[i].outputs[0], tail = ns[i + 1].outputs[0];
+        if (!internal_only(head, 1) || !internal_only(tail, 3)) return false;
+        float lo, hi;
+        if (!clip_constants(ns[i + 2], lo, hi) || ns[i + 2].inputs[0] != head || hi < 65504.0F) return false;
+        const TensorId clipped = ns[i + 2].outputs[0];
+        if (graph_output(clipped)) return false;
+        const aot::Node& rec = ns[i + 3];
+        if (rec.op != Op::RECIPROCAL || rec.inputs.size() != 1 || rec.inputs[0] != clipped || rec.outputs.size() != 1) return false;
+        TensorId inv = rec.outputs[0];
+        if (!internal_only(inv, 1)) return false;
+        std::size_t k = i + 4;
+        if (k + 15 <= ns.size() && ns[k].op == Op::MUL && ns[k].inputs.size() == 2 && ns[k].outputs.size() == 1) {
+            TensorId other = 0;
+            float one = 0.0F;
+            if (other_in_pair(ns[k], Op::MUL, inv, other) && fp16_scalar_init(other, one) && std::fabs(one - 1.0F) <= 1e-4F) {
+                inv = ns[k].outputs[0];
+                if (!internal_only(inv, 1)) return false;
+                ++k;
+            }
+        }
+        if (k + 15 > ns.size()) return false;
+        const std::vector<std::int64_t> nshape{ps[0], 2 * q, ps[2], ps[3]}, qshape{ps[0], q, ps[2], ps[3]};
+        TensorId latent = 0;
+        if (!other_in_pair(ns[k], Op::MUL, inv, latent) || !named(latent) || is_weight(latent) || !fp16_of(latent, nshape)) return false;
+        const TensorId normalized = ns[k].outputs[0];
+        const aot::Node& sub = ns[k + 1];
+        if (sub.op != Op::SUB || sub.inputs.size() != 2 || sub.outputs.size() != 1 || sub.inputs[0] != normalized || sub.inputs[1] != tail)
+            return false;
+        const TensorId diff = sub.outputs[0];
+        TensorId qs = 0;
+        if (!internal_only(diff, 1) || !other_in_pair(ns[k + 2], Op::MUL, diff, qs) || !fp16_of(qs, nshape)) return false;
+        const TensorId scaled = ns[k + 2].outputs[0];
+        if (!internal_only(scaled, 2)) return false;
+        TensorId y_raw, u0, u1, us0, us1;
+        const std::size_t e = match_update(k + 3, scaled, tail, q, qshape, y_raw, u0, u1, us0, us1);
+        if (!e) return false;
+        const aot::Node& c2 = ns[e];
+        const aot::Node& c3 = ns[e + 1];
+        if (c2.op != Op::CONCAT || axis_of(c2) != 1 || c2.inputs.size() != 2 || c2.inputs[0] != u0 || c2.inputs[1] != u1 ||
+            c2.outputs.size() != 1)
+            return false;
+        const TensorId concat2 = c2.outputs[0];
+        if (c3.op != Op::CONCAT || axis_of(c3) != 1 || c3.inputs.size() != 2 || c3.inputs[0] != concat2 || c3.inputs[1] != prior ||
+            c3.outputs.size() != 1)
+            return false;
+        const std::vector<std::int64_t> c6{ps[0], 6 * q, ps[2], ps[3]};
+        if (desc(normalized).shape != nshape || desc(clipped).shape != nshape || desc(y_raw).shape != qshape ||
+            desc(concat2).shape != nshape || desc(c3.outputs[0]).shape != c6)
+            return false;
+        L.kind = Launch::kY0;
+        L.kind_name = "y0_tail";
+        L.ins = {latent, prior, qs, us0, us1};
+        L.outs = {normalized, clipped, y_raw, concat2};
+        L.y = c3.outputs[0];
+        L.n = static_cast<int>(ps[0]);
+        L.c = static_cast<int>(q);
+        L.hw = static_cast<std::size_t>(ps[2] * ps[3]);
+        L.lo = lo;
+        L.bytes = 2.0 * static_cast<double>(ps[0] * ps[2] * ps[3]) * static_cast<double>(q) * (10 + 13);
+        for (std::size_t n = i; n < e + 2; ++n) done[n] = true;
+        return true;
+    }
+
+    // try_y1_tail (fusion_matcher.cpp:698-850).
+    bool match_y1(std::size_t i, Launch& L, std::vector<bool>& done)
+    {
+        const auto& ns = nodes();
+        if (i + 15 > ns.size()) return false;
+        const aot::Node& sub = ns[i];
+        if (sub.op != Op::SUB || sub.inputs.size() != 2 || sub.outputs.size() != 1) return false;
+        const TensorId normalized = sub.inputs[0], prior = sub.inputs[1];
+        if (!fp16_4d(normalized) || !fp16_4d(prior) || desc(normalized).shape != desc(prior).shape) return false;
+        const auto& ns_shape = desc(normalized).shape;
+        if (ns_shape[1] <= 0 || ns_shape[1] % 2) return false;
+        const std::int64_t q = ns_shape[1] / 2;
+        const std::vector<std::int64_t> qshape{ns_shape[0], q, ns_shape[2], ns_shape[3]};
+        const TensorId diff = sub.outputs[0];
+        TensorId qs = 0;
+        if (!internal_only(diff, 1) || !other_in_pair(ns[i + 1], Op::MUL, diff, qs) || !fp16_of(qs, ns_shape)) return false;
+        const TensorId scaled = ns[i + 1].outputs[0];
+        if (!internal_only(scaled, 2)) return false;
+        TensorId y_raw, u0, u1, us0, us1;
+        const std::size_t e = match_update(i + 2, scaled, prior, q, qshape, y_raw, u0, u1, us0, us1);
+        if (!e) return false;
+        const aot::Node& c2 = ns[e];
+        if (c2.op != Op::CONCAT || axis_of(c2) != 1 || c2.inputs.size() != 2 || c2.inputs[0] != u0 || c2.inputs[1] != u1 ||
+            c2.outputs.size() != 1)
+            return false;
+        const TensorId cat = c2.outputs[0];
+        TensorId concat2 = 0, clipped = 0;
+        if (!internal_only(cat, 1) || !other_in_pair(ns[e + 1], Op::ADD, cat, concat2) || !named(concat2) || is_weight(concat2) ||
+            !fp16_of(concat2, ns_shape))
+            return false;
+        const TensorId added = ns[e + 1].outputs[0];
+        if (!internal_only(added, 1) || !other_in_pair(ns[e + 2], Op::MUL, added, clipped) || !named(clipped) || is_weight(clipped) ||
+            !fp16_of(clipped, ns_shape))
+            return false;
+        if (desc(y_raw).shape != qshape || desc(ns[e + 2].outputs[0]).shape != ns_shape) return false;
+        L.kind = Launch::kY1;
+        L.kind_name = "y1_tail";
+        L.ins = {normalized, prior, qs, us0, us1, concat2, clipped};
+        L.outs = {y_raw};
+        L.y = ns[e + 2].outputs[0];
+        L.n = static_cast<int>(ns_shape[0]);
+        L.c = static_cast<int>(q);
+        L.hw = static_cast<std::size_t>(ns_shape[2] * ns_shape[3]);
+        L.bytes = 2.0 * static_cast<double>(ns_shape[0] * ns_shape[2] * ns_shape[3]) * static_cast<double>(q) * (12 + 3);
+        for (std::size_t n = i; n < e + 3; ++n) done[n] = true;
+        return true;
+    }
+
+    // ------------------------------------------------- single operators
+    // FP16 operand of an elementwise / layout operator: an activation or an
+    // FP16 initializer (uploaded once as a constant buffer).
+    void fp16_operand(TensorId id)
+    {
+        if (!named(id) || desc(id).dtype != aot::DataType::FP16) fail("operand must be an FP16 tensor");
+        if (is_weight(id) && !const_buf_.count(id)) {
+            auto raw = weight_bytes(id);
+            DeviceMem m(std::max<std::size_t>(raw.size(), 16));
+            pending_uploads_.push_back({m.ptr, std::move(raw)});
+            const_buf_.emplace(id, std::move(m));
+        }
+    }
+
+    static void dims4(const std::vector<std::int64_t>& s, std::int64_t (&d)[4])
+    {
+        if (s.size() > 4) fail("tensors of rank above 4 are not supported");
+        for (int k = 0; k < 4; ++k) d[k] = 1;
+        for (std::size_t k = 0; k < s.size(); ++k) d[4 - s.size() + k] = s[k];
+    }
+
+    void lower_unary(Launch& L, const aot::Node& n)
+    {
+        fp16_operand(n.inputs.at(0));
+        if (desc(n.inputs[0]).shape != desc(n.outputs[0]).shape) fail("unary operator output shape differs from its input");
+        L.kind = Launch::kUnary;
+        L.x = n.inputs[0];
+        L.y = n.outputs[0];
+        L.count = elem_count(desc(L.y).shape);
+        L.lo = 0.0F;
+        L.hi = 0.0F;
+        switch (n.op) {
+        case Op::CLIP:
+            // execution_plan.cpp:512-520: absent bounds are -inf / +inf.
+            L.op = MLVC_UNARY_CLIP;
+            L.kind_name = "clip";
+            L.lo = -HUGE_VALF;
+            L.hi = HUGE_VALF;
+            if (n.inputs.size() > 1 && n.inputs[1] && !fp16_scalar_init(n.inputs[1], L.lo)) fail("expected scalar FP16 initializer");
+            if (n.inputs.size() > 2 && n.inputs[2] && !fp16_scalar_init(n.inputs[2], L.hi)) fail("expected scalar FP16 initializer");
+            break;
+        case Op::SIGMOID: L.op = MLVC_UNARY_SIGMOID; L.kind_name = "sigmoid"; break;
+        case Op::RECIPROCAL: L.op = MLVC_UNARY_RECIPROCAL; L.kind_name = "reciprocal"; break;
+        default: L.op = MLVC_UNARY_ROUND; L.kind_name = "round"; break;
+        }
+        L.bytes = 4.0 * static_cast<double>(L.count);
+    }
+
+    // ADD / SUB / MUL with numpy broadcasting (execution_plan.cpp:527-563,
+    // 958-985). Outputs of rank other than 4 are indexed flat modulo the
+    // operand size there, which is numpy broadcasting only when each operand
+    // shape is a suffix of the output's; other such graphs are rejected.
+    void lower_binary(Launch& L, const aot::Node& n)
+    {
+        const TensorId a = n.inputs.at(0), b = n.inputs.at(1), y = n.outputs[0];
+        fp16_operand(a);
+        fp16_operand(b);
+        const auto& as = desc(a).shape;
+        const auto& bs = desc(b).shape;
+        const auto& ys = desc(y).shape;
+        const std::size_t r = std::max(as.size(), bs.size());
+        std::vector<std::int64_t> want(r, 1);
+        for (std::size_t i = 0; i < r; ++i) {
+            const std::int64_t u = i + as.size() >= r ? as[i + as.size() - r] : 1;
+            const std::int64_t v = i + bs.size() >= r ? bs[i + bs.size() - r] : 1;
+            if (u != v && u != 1 && v != 1) fail("binary operand shapes do not broadcast");
+            want[i] = std::max(u, v);
+        }
+        if (want != ys) fail("binary output shape is not the broadcast of its operands");
+        auto suffix_or_scalar = [&](const std::vector<std::int64_t>& s) {
+            if (elem_count(s) == 1) return true;
+            std::vector<std::int64_t> t = s;
+            while (!t.empty() && t.front() == 1) t.erase(t.begin());
+            return t.size() <= ys.size() && std::equal(t.rbegin(), t.rend(), ys.rbegin());
+        };
+        if (ys.size() != 4 && !(suffix_or_scalar(as) && suffix_or_scalar(bs)))
+            fail("broadcast of a non-4-D output with a non-trailing operand is not supported");
+        // A rank < 4 operand of a 4-D output is indexed as NHWC there; that
+        // equals NCHW broadcasting only when its padded shape has a single
+        // channel or a single pixel.
+        for (const auto* s : {&as, &bs})
+            if (ys.size() == 4 && s->size() < 4 && elem_count(*s) > 1) {
+                std::int64_t d[4];
+                dims4(*s, d);
+                if (d[1] > 1 && d[2] * d[3] > 1) fail("broadcast operand of rank < 4 with channels and pixels is not supported");
+            }
+        L.kind = n.op == Op::ADD && as == ys && bs == ys ? Launch::kAdd : Launch::kBinary;
+        L.op = n.op == Op::SUB ? MLVC_BINARY_SUB : n.op == Op::MUL ? MLVC_BINARY_MUL : MLVC_BINARY_ADD;
+        L.kind_name = n.op == Op::SUB ? "sub" : n.op == Op::MUL ? "mul" : "add";
+        L.x = a;
+        L.x2 = b;
+        L.y = y;
+        L.count = elem_count(ys);
+        dims4(as, L.da);
+        dims4(bs, L.db);
+        dims4(ys, L.dy);
+        L.bytes = 2.0 * static_cast<double>(elem_count(as) + elem_count(bs) + elem_count(ys));
+    }
+
+    // SLICE (execution_plan.cpp:565-604): INT64 starts / ends / axes / steps
+    // initializers; negative starts count from the end and are clamped to
+    // [0, dim]; the output shape gives the extent.
+    void lower_slice(Launch& L, const aot::Node& n)
+    {
+        const TensorId x = n.inputs.at(0), y = n.outputs[0];
+        fp16_operand(x);
+        const auto& xs = desc(x).shape;
+        const auto& ys = desc(y).shape;
+        if (xs.size() != 4 || ys.size() != 4) fail("expected 4D NCHW tensor");
+        std::vector<std::int64_t> st, en, ax, sp;
+        if (n.inputs.size() < 3 || !int64_init(n.inputs[1], st) || !int64_init(n.inputs[2], en))
+            fail("SLICE starts and ends must be INT64 initializers");
+        if (n.inputs.size() > 3 && n.inputs[3]) {
+            if (!int64_init(n.inputs[3], ax)) fail("SLICE axes must be an INT64 initializer");
+        } else {
+            for (std::size_t a = 0; a < st.size(); ++a) ax.push_back(static_cast<std::int64_t>(a));
+        }
+        sp.assign(st.size(), 1);
+        if (n.inputs.size() > 4 && n.inputs[4] && !int64_init(n.inputs[4], sp)) fail("SLICE steps must be an INT64 initializer");
+        if (ax.size() < st.size() || sp.size() < st.size()) fail("SLICE parameter lengths differ");
+        for (int k = 0; k < 4; ++k) {
+            L.starts[k] = 0;
+            L.steps[k] = 1;
+            L.da[k] = xs[static_cast<std::size_t>(k)];
+            L.dy[k] = ys[static_cast<std::size_t>(k)];
+        }
+        for (std::size_t a = 0; a < st.size(); ++a) {
+            std::int64_t k = ax[a];
+            if (k < 0) k += 4;
+            if (k < 0 || k >= 4) fail("SLICE axis out of range");
+            const std::int64_t dim = xs[static_cast<std::size_t>(k)];
+            std::int64_t v = st[a];
+            if (v < 0) v += dim;
+            L.starts[k] = std::clamp<std::int64_t>(v, 0, dim);
+            L.steps[k] = sp[a];
+        }
+        for (int k = 0; k < 4; ++k) {
+            const std::int64_t last = L.starts[k] + (L.dy[k] - 1) * L.steps[k];
+            if (L.steps[k] == 0 || L.starts[k] >= L.da[k] || last < 0 || last >= L.da[k]) fail("SLICE reads outside its input");
+        }
+        L.kind = Launch::kSlice;
+        L.kind_name = "slice";
+        L.x = x;
+        L.y = y;
+        L.bytes = 4.0 * static_cast<double>(elem_count(ys));
+    }
+
+    // CONCAT of 4-D tensors along any axis (execution_plan.cpp:606-620):
+    // every input is one block copy into its place in the output.
+    void lower_concat(Launch& L, const aot::Node& n)
+    {
+        const TensorId y = n.outputs[0];
+        const auto& ys = desc(y).shape;
+        if (ys.size() != 4) fail("expected 4D NCHW tensor");
+        int axis = axis_of(n);
+        if (axis < 0) axis += 4;
+        if (axis < 0 || axis >= 4) fail("CONCAT axis out of range");
+        std::size_t after = 1;
+        for (int k = axis + 1; k < 4; ++k) after *= static_cast<std::size_t>(ys[static_cast<std::size_t>(k)]);
+        std::size_t rows = 1;
+        for (int k = 0; k < axis; ++k) rows *= static_cast<std::size_t>(ys[static_cast<std::size_t>(k)]);
+        std::int64_t off = 0;
+        for (TensorId id : n.inputs) {
+            fp16_operand(id);
+            const auto& s = desc(id).shape;
+            if (s.size() != 4) fail("expected 4D NCHW tensor");
+            for (int k = 0; k < 4; ++k)
+                if (k != axis && s[static_cast<std::size_t>(k)] != ys[static_cast<std::size_t>(k)]) fail("CONCAT input shape mismatch");
+            const std::size_t along = static_cast<std::size_t>(s[static_cast<std::size_t>(axis)]);
+            L.ins.push_back(id);
+            L.pieces.push_back({rows, along * after, static_cast<std::size_t>(off) * after,
+                                static_cast<std::size_t>(ys[static_cast<std::size_t>(axis)]) * after});
+            off += s[static_cast<std::size_t>(axis)];
+        }
+        if (off != ys[static_cast<std::size_t>(axis)]) fail("CONCAT output shape mismatch");
+        L.kind = Launch::kConcatAny;
+        L.kind_name = "concat";
+        L.y = y;
+        L.bytes = 4.0 * static_cast<double>(elem_count(ys));
+    }
+
+    // GATHER (execution_plan.cpp:1004-1012, 101-168): FP16 data, INT64
+    // initializer indices or INT32 graph-input indices (q_index_shifted);
+    // out = take(data, indices, axis). Initializer indices are range-checked
+    // here, graph-input indices on every upload.
+    void lower_gather(Launch& L, const aot::Node& n)
+    {
+        const TensorId d = n.inputs.at(0), ix = n.inputs.at(1), y = n.outputs[0];
+        fp16_operand(d);
+        const auto& ds = desc(d).shape;
+        const int rank = static_cast<int>(ds.size());
+        int axis = axis_of(n);
+        if (axis < 0) axis += rank;
+        if (axis < 0 || axis >= rank) fail("GATHER axis out of range");
+        // The reference indexes 4-D data in its NHWC order; the result is
+        // take() on the logical array when the output keeps rank 4 or the data
+        // is one pixel per row (its [72, C, 1, 1] table case).
+        const auto& is = desc(ix).shape;
+        const bool pixel_rows = axis == 0 && (rank != 4 || (ds[2] == 1 && ds[3] == 1));
+        if (rank == 4 && !pixel_rows && is.size() != 1) fail("GATHER of 4-D data with indices of rank other than 1 is not supported");
+        L.outer = 1;
+        L.inner = 1;
+        for (int k = 0; k < axis; ++k) L.outer *= static_cast<std::size_t>(ds[static_cast<std::size_t>(k)]);
+        for (int k = axis + 1; k < rank; ++k) L.inner *= static_cast<std::size_t>(ds[static_cast<std::size_t>(k)]);
+        L.dim = static_cast<std::size_t>(ds[static_cast<std::size_t>(axis)]);
+        L.count = elem_count(is);
+        if (L.count == 0 || elem_count(desc(y).shape) != L.outer * L.count * L.inner) fail("GATHER output size mismatch");
+        if (is_weight(ix)) {
+            std::vector<std::int64_t> v;
+            if (!int64_init(ix, v)) fail("GATHER indices must be INT64 initializers or INT32 graph inputs");
+            for (std::int64_t i : v)
+                if ((i < 0 ? i + static_cast<std::int64_t>(L.dim) : i) < 0 || (i < 0 ? i + static_cast<std::int64_t>(L.dim) : i) >=
+                                                                                   static_cast<std::int64_t>(L.dim))
+                    fail("GATHER index out of range");
+            auto raw = weight_bytes(ix);
+            DeviceMem m(raw.size());
+            pending_uploads_.push_back({m.ptr, std::move(raw)});
+            const_buf_.emplace(ix, std::move(m));
+            L.idx64 = true;
+        } else {
+            const auto& g = graph_.descriptor.inputs;
+            const auto it = std::find(ext_in_.begin(), ext_in_.end(), ix);
+            if (desc(ix).dtype != aot::DataType::INT32 || it == ext_in_.end() || std::find(g.begin(), g.end(), ix) == g.end())
+                fail("GATHER indices must be INT64 initializers or INT32 graph inputs");
+            gather_checks_.push_back({static_cast<std::size_t>(it - ext_in_.begin()), L.dim});
+            L.idx64 = false;
+        }
+        L.kind = Launch::kGather;
+        L.kind_name = "gather";
+        L.x = d;
+        L.x2 = ix;
+        L.y = y;
+        L.bytes = 4.0 * static_cast<double>(elem_count(desc(y).shape));
+    }
+
+    // Host check of graph-input GATHER indices (the reference throws
+    // "GATHER index out of range" while executing).
+    void check_gather_indices(std::size_t ext_pos, const void* data) const
+    {
+        for (const auto& [pos, dim] : gather_checks_) {
+            if (pos != ext_pos) continue;
+            const std::size_t n = elem_count(desc(ext_in_[pos]).shape);
+            const auto* v = static_cast<const std::int32_t*>(data);
+            for (std::size_t i = 0; i < n; ++i) {
+                const std::int64_t k = v[i] < 0 ? static_cast<std::int64_t>(v[i]) + static_cast<std::int64_t>(dim) : v[i];
+                if (k < 0 || k >= static_cast<std::int64_t>(dim)) fail("GATHER index out of range");
+            }
+        }
+    }
+
     // ---------------------------------------------------------- lowering
     void lower()
     {
         const auto& g = graph_.descriptor;
         const auto& ns = nodes();
-        std::map<TensorId, int> consumers;
+        std::map<TensorId, int>& consumers = consumers_;
         std::map<TensorId, std::size_t> producer, first_consumer;
         for (const aot::Node& n : ns) {
             for (TensorId id : n.inputs)
@@ -551,8 +1163,29 @@ private:
         std::vector<bool> done(ns.size(), false);
         for (const aot::Node& n : ns) {
             if (done[n.index] || folded[n.index]) continue;
-            done[n.index] = true;
             auto L = std::make_unique<Launch>();
+            // Real-model chains, in the reference matcher's order
+            // (fusion_matcher.cpp:50-72); a chain is taken only when none of
+            // its nodes was already lowered into another launch.
+            if (fuse && (n.op == Op::SLICE || n.op == Op::SUB)) {
+                std::vector<bool> take(ns.size(), false);
+                const bool hit = match_y0(n.index, *L, take) || match_y1(n.index, *L, take) || match_feature(n.index, *L, take) ||
+                                 match_reglu(n.index, *L, take);
+                bool free = hit;
+                for (std::size_t k = 0; hit && k < ns.size(); ++k)
+                    if (take[k] && (done[k] || folded[k])) free = false;
+                if (free) {
+                    for (std::size_t k = 0; k < ns.size(); ++k)
+                        if (take[k]) done[k] = true;
+                    if (L->x) fp16_operand(L->x);
+                    for (TensorId id : L->ins) fp16_operand(id);
+                    L->name = desc(L->y).name;
+                    launches_.push_back(std::move(L));
+                    continue;
+                }
+                L = std::make_unique<Launch>();
+            }
+            done[n.index] = true;
             switch (n.op) {
             case Op::CONV:
                 if (n.conv().groups == 1) {
@@ -573,17 +1206,21 @@ private:
                 L->bytes = 4.0 * static_cast<double>(L->count);
                 break;
             case Op::ADD:
-                require_fp16_activation(n.inputs[0]);
-                require_fp16_activation(n.inputs[1]);
-                if (desc(n.inputs[0]).shape != desc(n.outputs[0]).shape || desc(n.inputs[1]).shape != desc(n.outputs[0]).shape)
-                    fail("broadcast ADD is outside the conv-graph path");
-                L->kind = Launch::kAdd;
-                L->kind_name = "add";
-                L->x = n.inputs[0];
-                L->x2 = n.inputs[1];
-                L->y = n.outputs[0];
-                L->count = elem_count(desc(L->y).shape);
-                L->bytes = 6.0 * static_cast<double>(L->count);
+            case Op::SUB:
+            case Op::MUL:
+                lower_binary(*L, n);
+                break;
+            case Op::CLIP:
+            case Op::SIGMOID:
+            case Op::RECIPROCAL:
+            case Op::ROUND:
+                lower_unary(*L, n);
+                break;
+            case Op::SLICE:
+                lower_slice(*L, n);
+                break;
+            case Op::GATHER:
+                lower_gather(*L, n);
                 break;
             case Op::DEPTH_TO_SPACE:
             case Op::SPACE_TO_DEPTH: {
@@ -604,11 +1241,17 @@ private:
             }
             case Op::CONCAT: {
                 const int axis = n.axis() < 0 ? n.axis() + 4 : n.axis();
-                if (axis != 1 || n.inputs.size() != 2) fail("only two-input channel CONCAT is on this path");
-                require_fp16_activation(n.inputs[0]);
-                require_fp16_activation(n.inputs[1]);
+                const bool two_channel = axis == 1 && n.inputs.size() == 2 && fp16_4d(n.inputs[0]) && fp16_4d(n.inputs[1]) &&
+                                         !is_weight(n.inputs[0]) && !is_weight(n.inputs[1]) &&
+                                         desc(n.outputs[0]).shape.size() == 4;
+                if (!two_channel) {
+                    lower_concat(*L, n);
+                    break;
+                }
                 const auto& a = desc(n.inputs[0]).shape;
                 const auto& b = desc(n.inputs[1]).shape;
+                if (a[0] != b[0] || a[2] != b[2] || a[3] != b[3] || desc(n.outputs[0]).shape != std::vector<std::int64_t>{a[0], a[1] + b[1], a[2], a[3]})
+                    fail("CONCAT input shape mismatch");
                 L->kind = Launch::kConcat;
                 L->kind_name = "concat";
                 L->x = n.inputs[0];
@@ -1019,12 +1662,16 @@ private:
         };
         for (std::size_t i = 0; i < n; ++i) {
             const Launch& l = *launches_[i];
-            if (arena_resident(l.y)) {
-                auto it = live.find(l.y);
-                if (it == live.end()) live[l.y] = {i, i};
+            std::vector<TensorId> writes{l.y}, reads{l.x, l.x2, l.res};
+            writes.insert(writes.end(), l.outs.begin(), l.outs.end());
+            reads.insert(reads.end(), l.ins.begin(), l.ins.end());
+            for (TensorId w : writes) {
+                if (!arena_resident(w)) continue;
+                auto it = live.find(w);
+                if (it == live.end()) live[w] = {i, i};
                 else it->second.second = std::max(it->second.second, i);
             }
-            for (TensorId r : {l.x, l.x2, l.res}) {
+            for (TensorId r : reads) {
                 if (!arena_resident(r)) continue;
                 auto it = live.find(r);
                 if (it == live.end()) fail("tensor read before it is written: " + desc(r).name);
@@ -1084,6 +1731,7 @@ private:
         if (auto it = state_in_.find(id); it != state_in_.end()) return bindings_[it->second].buf[parity].ptr;
         if (auto it = state_out_.find(id); it != state_out_.end()) return bindings_[it->second].buf[parity ^ 1].ptr;
         if (auto it = input_buf_.find(id); it != input_buf_.end()) return it->second.ptr;
+        if (auto it = const_buf_.find(id); it != const_buf_.end()) return it->second.ptr;
         if (auto it = offset_.find(id); it != offset_.end()) return static_cast<char*>(arena_.ptr) + it->second;
         fail("tensor without device storage: " + desc(id).name);
     }
@@ -1152,6 +1800,76 @@ private:
                                                stream_),
                       "concat launch");
             break;
+        case Launch::kUnary:
+            hip_check(mlvc_hip_unary(ptr(l.x, parity), ptr(l.y, parity), l.count, l.op, l.lo, l.hi, stream_), "unary launch");
+            break;
+        case Launch::kBinary:
+            hip_check(mlvc_hip_binary(ptr(l.x, parity), l.da, ptr(l.x2, parity), l.db, ptr(l.y, parity), l.dy, l.op, stream_),
+                      "binary launch");
+            break;
+        case Launch::kSlice:
+            hip_check(mlvc_hip_slice(ptr(l.x, parity), l.da, ptr(l.y, parity), l.dy, l.starts, l.steps, stream_), "slice launch");
+            break;
+        case Launch::kConcatAny: {
+            auto* out = static_cast<std::uint16_t*>(ptr(l.y, parity));
+            for (std::size_t k = 0; k < l.ins.size(); ++k) {
+                const Launch::Piece& p = l.pieces[k];
+                hip_check(mlvc_hip_copy_rows(ptr(l.ins[k], parity), out + p.y_offset, p.rows, p.row_elems, p.row_elems, p.y_stride,
+                                             stream_),
+                          "concat launch");
+            }
+            break;
+        }
+        case Launch::kGather:
+            hip_check(mlvc_hip_gather(ptr(l.x, parity), ptr(l.x2, parity), l.idx64 ? 1 : 0, l.count, l.outer, l.dim, l.inner,
+                                      ptr(l.y, parity), stream_),
+                      "gather launch");
+            break;
+        case Launch::kReglu:
+            hip_check(mlvc_hip_reglu(ptr(l.x, parity), ptr(l.y, parity), l.n, l.c, l.hw, l.lo, l.hi, stream_), "reglu launch");
+            break;
+        case Launch::kFeature:
+            hip_check(mlvc_hip_feature_update(ptr(l.x, parity), ptr(l.ins[0], parity), ptr(l.ins[1], parity), ptr(l.y, parity),
+                                              l.outs.empty() ? nullptr : ptr(l.outs[0], parity),
+                                              l.outs.empty() ? nullptr : ptr(l.outs[1], parity), l.n, l.c, l.hw, stream_),
+                      "feature update launch");
+            break;
+        case Launch::kY0: {
+            mlvc_hip_y0_tail_desc d{};
+            d.latent = ptr(l.ins[0], parity);
+            d.prior = ptr(l.ins[1], parity);
+            d.quant_scale = ptr(l.ins[2], parity);
+            d.update_scale0 = ptr(l.ins[3], parity);
+            d.update_scale1 = ptr(l.ins[4], parity);
+            d.normalized = ptr(l.outs[0], parity);
+            d.clipped = ptr(l.outs[1], parity);
+            d.y_raw = ptr(l.outs[2], parity);
+            d.concat2 = ptr(l.outs[3], parity);
+            d.concat3 = ptr(l.y, parity);
+            d.n = l.n;
+            d.q = l.c;
+            d.hw = l.hw;
+            d.clip_min = l.lo;
+            hip_check(mlvc_hip_y0_tail(&d, stream_), "y0 tail launch");
+            break;
+        }
+        case Launch::kY1: {
+            mlvc_hip_y1_tail_desc d{};
+            d.normalized = ptr(l.ins[0], parity);
+            d.prior = ptr(l.ins[1], parity);
+            d.quant_scale = ptr(l.ins[2], parity);
+            d.update_scale0 = ptr(l.ins[3], parity);
+            d.update_scale1 = ptr(l.ins[4], parity);
+            d.concat2 = ptr(l.ins[5], parity);
+            d.clipped = ptr(l.ins[6], parity);
+            d.y_raw = ptr(l.outs[0], parity);
+            d.out = ptr(l.y, parity);
+            d.n = l.n;
+            d.q = l.c;
+            d.hw = l.hw;
+            hip_check(mlvc_hip_y1_tail(&d, stream_), "y1 tail launch");
+            break;
+        }
         }
     }
 
@@ -1310,6 +2028,9 @@ private:
     std::size_t arena_bytes_ = 0;
     DeviceMem arena_;
     std::map<TensorId, DeviceMem> input_buf_;
+    std::map<TensorId, DeviceMem> const_buf_;  // initializers read by elementwise / layout operators
+    std::map<TensorId, int> consumers_;
+    std::vector<std::pair<std::size_t, std::size_t>> gather_checks_;  // (external input, axis length)
     std::vector<HostMem> in_stage_, out_stage_;
     std::vector<mlvc_hip_graph> graphs_;
     int parity_ = 0;

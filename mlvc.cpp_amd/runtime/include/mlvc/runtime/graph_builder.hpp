@@ -41,6 +41,12 @@ public:
     Id pixel(aot::Op op, const std::string& name, Id x, int block);
     Id concat(const std::string& name, const std::vector<Id>& xs, int axis);
     Id unary(aot::Op op, const std::string& name, Id x);
+    // CLIP with FP16 scalar initializers `lo` / `hi` (0 = unbounded side).
+    Id clip(const std::string& name, Id x, Id lo, Id hi);
+    // SLICE with INT64 initializers; `axes` / `steps` may be empty (absent).
+    Id slice(const std::string& name, Id x, const std::vector<std::int64_t>& starts, const std::vector<std::int64_t>& ends,
+             const std::vector<std::int64_t>& axes = {}, const std::vector<std::int64_t>& steps = {});
+    Id gather(const std::string& name, Id data, Id indices, int axis);
 
     void output(Id id) { outputs_.push_back(id); }
     const Shape& shape(Id id) const { return tensors_.at(id - 1).shape; }

@@ -204,8 +204,71 @@ GraphBuilder::Id GraphBuilder::leaky_relu(const std::string& name, Id x, float a
 
 GraphBuilder::Id GraphBuilder::binary(aot::Op op, const std::string& name, Id a, Id b)
 {
-    const Shape out = element_count(shape(a)) >= element_count(shape(b)) ? shape(a) : shape(b);
+    // Output shape: numpy broadcasting of the two operand shapes.
+    const Shape& sa = shape(a);
+    const Shape& sb = shape(b);
+    const std::size_t r = std::max(sa.size(), sb.size());
+    Shape out(r, 1);
+    for (std::size_t i = 0; i < r; ++i) {
+        const std::int64_t x = i + sa.size() >= r ? sa[i + sa.size() - r] : 1;
+        const std::int64_t y = i + sb.size() >= r ? sb[i + sb.size() - r] : 1;
+        if (x != y && x != 1 && y != 1) throw std::runtime_error("graph builder: operand shapes do not broadcast");
+        out[i] = std::max(x, y);
+    }
     return add_node(make_node(op, {a, b}), out, name);
+}
+
+GraphBuilder::Id GraphBuilder::clip(const std::string& name, Id x, Id lo, Id hi)
+{
+    std::vector<Id> ins{x, lo};
+    if (hi) ins.push_back(hi);
+    return add_node(make_node(aot::Op::CLIP, ins), shape(x), name);
+}
+
+GraphBuilder::Id GraphBuilder::slice(const std::string& name, Id x, const std::vector<std::int64_t>& starts,
+                                     const std::vector<std::int64_t>& ends, const std::vector<std::int64_t>& axes,
+                                     const std::vector<std::int64_t>& steps)
+{
+    // Output extent per sliced axis: ceil((clamp(end) - clamp(start)) / step)
+    // for positive steps, the reverse range for negative ones.
+    Shape out = shape(x);
+    const auto n = static_cast<std::int64_t>(out.size());
+    for (std::size_t a = 0; a < starts.size(); ++a) {
+        std::int64_t ax = axes.empty() ? static_cast<std::int64_t>(a) : axes[a];
+        if (ax < 0) ax += n;
+        const std::int64_t dim = shape(x)[static_cast<std::size_t>(ax)];
+        const std::int64_t step = steps.empty() ? 1 : steps[a];
+        auto norm = [&](std::int64_t v, std::int64_t lo, std::int64_t hi) { return std::clamp(v < 0 ? v + dim : v, lo, hi); };
+        std::int64_t len;
+        if (step > 0) {
+            len = (norm(ends[a], 0, dim) - norm(starts[a], 0, dim) + step - 1) / step;
+        } else {
+            len = (norm(starts[a], -1, dim - 1) - norm(ends[a], -1, dim - 1) + (-step) - 1) / (-step);
+        }
+        out[static_cast<std::size_t>(ax)] = std::max<std::int64_t>(len, 0);
+    }
+    const std::string p = name + "/";
+    std::vector<Id> ins{x, weight_int64(p + "starts", {static_cast<std::int64_t>(starts.size())}, starts),
+                        weight_int64(p + "ends", {static_cast<std::int64_t>(ends.size())}, ends)};
+    if (!axes.empty()) ins.push_back(weight_int64(p + "axes", {static_cast<std::int64_t>(axes.size())}, axes));
+    if (!steps.empty()) {
+        if (axes.empty()) ins.push_back(0);
+        ins.push_back(weight_int64(p + "steps", {static_cast<std::int64_t>(steps.size())}, steps));
+    }
+    return add_node(make_node(aot::Op::SLICE, ins), out, name);
+}
+
+GraphBuilder::Id GraphBuilder::gather(const std::string& name, Id data, Id indices, int axis)
+{
+    const Shape& ds = shape(data);
+    const int ax = axis < 0 ? axis + static_cast<int>(ds.size()) : axis;
+    Shape out(ds.begin(), ds.begin() + ax);
+    for (auto d : shape(indices)) out.push_back(d);
+    out.insert(out.end(), ds.begin() + ax + 1, ds.end());
+    N n = make_node(aot::Op::GATHER, {data, indices});
+    n.attr = wire::AttrCase::kAxis;
+    n.axis = axis;
+    return add_node(std::move(n), out, name);
 }
 
 GraphBuilder::Id GraphBuilder::unary(aot::Op op, const std::string& name, Id x)

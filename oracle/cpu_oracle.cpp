@@ -36,17 +36,27 @@
 //     (fusion_matcher.cpp:352-411) and the thread-count rule
 //     (thread_pool.cpp:35-69).
 //
-// The reference's real-model fusions (ReGLU, recurrent feature update,
-// quantisation tails) and the SLICE/GATHER/CLIP/SIGMOID/... operators are not
-// on the conv-graph path and are not restated; graphs that need them are
-// rejected. Parity pins: see the test files under tests/ (bit-exact against
-// the reference kernels built from source, known-answer graphs, brute force).
+//   * Operators of the real-model graphs: CLIP / SIGMOID / RECIPROCAL /
+//     ROUND (scalar_unary kernels_scalar.cpp:80-97, 244-255; avx2_unary
+//     kernels_x86_avx2.cpp:30-62, 304-352 with its polynomial exp), ADD /
+//     SUB / MUL with every broadcast form (execution_plan.cpp:170-236,
+//     527-563, 958-985), SLICE (:565-604; kernels_scalar.cpp:830-890),
+//     CONCAT on any axis (:606-620; kernels_scalar.cpp:892-952), GATHER
+//     (:101-168, 1004-1012).
+//   * The real-model fusions and their matcher (fusion_matcher.cpp:258-850):
+//     ReGLU (standalone and as a 1x1 conv epilogue), the recurrent feature
+//     update (one- and three-output forms), the y0 / y1 quantisation tails
+//     (kernels_scalar.cpp:304-537, kernels_x86_avx2.cpp:443-712).
+// Parity pins: see the test files under tests/ (bit-exact against the
+// reference kernels built from source, known-answer graphs, brute force,
+// numpy semantics where the reference code sits in its plan).
 
 #include "oracle.h"
 
 #include <immintrin.h>
 
 #include <algorithm>
+#include <array>
 #include <cmath>
 #include <atomic>
 #include <bit>
@@ -528,6 +538,357 @@ void nhwc_to_nchw(const u16* in, u16* out, std::size_t n, std::size_t hw, std::s
             for (std::size_t ch = 0; ch < c; ++ch) out[(b * c + ch) * hw + p] = in[(b * hw + p) * c + ch];
 }
 
+// ------------------------------------- elementwise and layout operators
+// UnaryKind / BinaryKind of kernels_common.hpp:34-46.
+enum Unary { kUClip = 0, kUSigmoid = 1, kUReciprocal = 2, kURound = 3 };
+enum Binary { kBAdd = 0, kBSub = 1, kBMul = 2 };
+
+// MAXPS / MINPS lane semantics (the second operand wins when either is NaN).
+inline float maxps(float a, float b) { return a > b ? a : b; }
+inline float minps(float a, float b) { return a < b ? a : b; }
+
+// exp of one AVX2 lane, kernels_x86_avx2.cpp:30-55: clamp to
+// [-87.33654475, 88.72283905], n = rne(x * log2(e)), r = x - n*ln2 with ln2
+// split in two parts (fused steps), a degree-6 Taylor polynomial by Horner
+// with fused steps, then times 2^n assembled from exponent bits.
+float exp_lane(float x)
+{
+    x = minps(maxps(x, -87.33654475F), 88.72283905F);
+    const float fx = std::nearbyint(x * 1.4426950408889634F);
+    const float r = std::fma(-fx, 1.428606765330187E-6F, std::fma(-fx, 0.693145751953125F, x));
+    float p = 0.0013888889F;
+    p = std::fma(p, r, 0.0083333338F);
+    p = std::fma(p, r, 0.0416666679F);
+    p = std::fma(p, r, 0.1666666716F);
+    p = std::fma(p, r, 0.5F);
+    p = std::fma(p, r, 1.0F);
+    p = std::fma(p, r, 1.0F);
+    const auto bits = static_cast<std::uint32_t>(static_cast<std::int32_t>(fx) + 127) << 23;
+    return p * std::bit_cast<float>(bits);
+}
+
+// fast_sigmoid_ps_avx2 (kernels_x86_avx2.cpp:57-62) lane-wise, and the
+// scalar form used by the scalar kernels and the AVX2 tails.
+float sigmoid_lane(float x) { return 1.0F / (1.0F + exp_lane(0.0F - x)); }
+float sigmoid_exact(float x) { return 1.0F / (1.0F + std::exp(-x)); }
+
+// scalar_unary (kernels_scalar.cpp:80-97, 244-255) and avx2_unary
+// (kernels_x86_avx2.cpp:304-352). The AVX2 path works in lanes of 8 inside
+// chunks of 4096 that start at multiples of 4096 (thread_pool.cpp:185-192),
+// so only the last count % 8 values take its scalar tail.
+void unary(const u16* in, u16* out, std::size_t count, int op, float lo, float hi, int isa)
+{
+    const std::size_t vec = isa == 0 ? count - count % 8 : 0;
+    for (std::size_t i = 0; i < count; ++i) {
+        const float x = h2f(in[i]);
+        const bool lane = i < vec;
+        float r;
+        switch (op) {
+        case kUClip: r = lane ? maxps(minps(x, hi), lo) : std::min(std::max(x, lo), hi); break;
+        case kUSigmoid: r = lane ? sigmoid_lane(x) : sigmoid_exact(x); break;
+        case kUReciprocal: r = 1.0F / x; break;
+        default: r = std::nearbyint(x); break;
+        }
+        out[i] = f2h(r);
+    }
+}
+
+inline float binary_op(float a, float b, int op) { return op == kBSub ? a - b : op == kBMul ? a * b : a + b; }
+
+// binary_contiguous (kernels_scalar.cpp:257-268; the AVX2 lanes compute the
+// same single rounding).
+void binary_same(const u16* a, const u16* b, u16* out, std::size_t count, int op)
+{
+    for (std::size_t i = 0; i < count; ++i) out[i] = f2h(binary_op(h2f(a[i]), h2f(b[i]), op));
+}
+
+// binary_scalar_bcast (kernels_scalar.cpp:289-302).
+void binary_scalar(const u16* vec, u16 scalar, u16* out, std::size_t count, int op, bool scalar_lhs)
+{
+    const float s = h2f(scalar);
+    for (std::size_t i = 0; i < count; ++i) {
+        const float v = h2f(vec[i]);
+        out[i] = f2h(scalar_lhs ? binary_op(s, v, op) : binary_op(v, s, op));
+    }
+}
+
+// binary_channel_bcast over an NHWC [spatial, C] operand (kernels_scalar.cpp:270-287).
+void binary_channel(const u16* vec, const u16* chan, u16* out, std::size_t spatial, std::size_t c, int op, bool chan_lhs)
+{
+    for (std::size_t p = 0; p < spatial; ++p)
+        for (std::size_t ch = 0; ch < c; ++ch) {
+            const float v = h2f(vec[p * c + ch]), k = h2f(chan[ch]);
+            out[p * c + ch] = f2h(chan_lhs ? binary_op(k, v, op) : binary_op(v, k, op));
+        }
+}
+
+// execute_binary_broadcast_fallback_nhwc (execution_plan.cpp:170-236): flat
+// modulo indexing when the output is not 4-D; otherwise shapes right-aligned
+// to 4-D and every operand indexed as NHWC, size-1 dimensions broadcast.
+void binary_broadcast(const u16* a, const std::vector<std::int64_t>& as, const u16* b, const std::vector<std::int64_t>& bs,
+                      u16* out, const std::vector<std::int64_t>& os, int op)
+{
+    auto count = [](const std::vector<std::int64_t>& s) {
+        std::size_t n = 1;
+        for (auto d : s) n *= static_cast<std::size_t>(d);
+        return n;
+    };
+    if (os.size() != 4) {
+        const std::size_t total = count(os), na = count(as), nb = count(bs);
+        for (std::size_t i = 0; i < total; ++i)
+            out[i] = f2h(binary_op(h2f(a[na == 1 ? 0 : i % na]), h2f(b[nb == 1 ? 0 : i % nb]), op));
+        return;
+    }
+    auto dim4 = [](const std::vector<std::int64_t>& s) {
+        std::array<std::size_t, 4> r{1, 1, 1, 1};
+        const std::size_t off = 4 - s.size();
+        for (std::size_t i = 0; i < s.size(); ++i) r[off + i] = static_cast<std::size_t>(s[i]);
+        return r;
+    };
+    const auto ad = dim4(as), bd = dim4(bs), od = dim4(os);
+    for (std::size_t bi = 0; bi < od[0]; ++bi)
+        for (std::size_t y = 0; y < od[2]; ++y)
+            for (std::size_t x = 0; x < od[3]; ++x) {
+                const u16* ap = a + (((ad[0] == 1 ? 0 : bi) * ad[2] + (ad[2] == 1 ? 0 : y)) * ad[3] + (ad[3] == 1 ? 0 : x)) * ad[1];
+                const u16* bp = b + (((bd[0] == 1 ? 0 : bi) * bd[2] + (bd[2] == 1 ? 0 : y)) * bd[3] + (bd[3] == 1 ? 0 : x)) * bd[1];
+                u16* dst = out + ((bi * od[2] + y) * od[3] + x) * od[1];
+                for (std::size_t c = 0; c < od[1]; ++c)
+                    dst[c] = f2h(binary_op(h2f(ap[ad[1] == 1 ? 0 : c]), h2f(bp[bd[1] == 1 ? 0 : c]), op));
+            }
+}
+
+// ADD / SUB / MUL dispatch of the reference plan, execution_plan.cpp:527-563
+// (classification) and 958-985 (execution), over NHWC buffers.
+void binary_dispatch(const u16* a, const std::vector<std::int64_t>& as, const u16* b, const std::vector<std::int64_t>& bs, u16* o,
+                     const std::vector<std::int64_t>& os, int op)
+{
+    auto count_of = [](const std::vector<std::int64_t>& s) {
+        std::size_t n = 1;
+        for (auto d : s) n *= static_cast<std::size_t>(d);
+        return n;
+    };
+    // The output must be the broadcast of the operand shapes (the
+    // reference reads out of bounds otherwise).
+    const std::size_t r = std::max(as.size(), bs.size());
+    std::vector<std::int64_t> want(r, 1);
+    for (std::size_t i = 0; i < r; ++i) {
+        const std::int64_t x = i + as.size() >= r ? as[i + as.size() - r] : 1;
+        const std::int64_t y = i + bs.size() >= r ? bs[i + bs.size() - r] : 1;
+        if (x != y && x != 1 && y != 1) throw std::runtime_error("oracle: binary operand shapes do not broadcast");
+        want[i] = std::max(x, y);
+    }
+    if (want != os) throw std::runtime_error("oracle: binary output shape is not the broadcast shape");
+    const std::size_t count = count_of(os);
+    if (as == os && bs == os) {
+        binary_same(a, b, o, count, op);
+    } else if (count_of(bs) == 1) {
+        binary_scalar(a, b[0], o, count, op, false);
+    } else if (count_of(as) == 1) {
+        binary_scalar(b, a[0], o, count, op, true);
+    } else if (os.size() == 4 && as == os && bs == std::vector<std::int64_t>{1, os[1], 1, 1}) {
+        binary_channel(a, b, o, static_cast<std::size_t>(os[0] * os[2] * os[3]), static_cast<std::size_t>(os[1]), op, false);
+    } else if (os.size() == 4 && bs == os && as == std::vector<std::int64_t>{1, os[1], 1, 1}) {
+        binary_channel(b, a, o, static_cast<std::size_t>(os[0] * os[2] * os[3]), static_cast<std::size_t>(os[1]), op, true);
+    } else {
+        binary_broadcast(a, as, b, bs, o, os, op);
+    }
+}
+
+// execute_slice_nhwc (kernels_scalar.cpp:830-890): dims, starts and steps
+// are logical NCHW, buffers NHWC; its block-copy fast paths give the same
+// values as this element loop.
+void slice_nhwc(const u16* in, u16* out, const int* id, const int* od, const int* starts, const int* steps)
+{
+    std::size_t o = 0;
+    for (int b = 0; b < od[0]; ++b)
+        for (int y = 0; y < od[2]; ++y)
+            for (int x = 0; x < od[3]; ++x)
+                for (int c = 0; c < od[1]; ++c, ++o) {
+                    const std::size_t ib = static_cast<std::size_t>(starts[0] + b * steps[0]);
+                    const std::size_t iy = static_cast<std::size_t>(starts[2] + y * steps[2]);
+                    const std::size_t ix = static_cast<std::size_t>(starts[3] + x * steps[3]);
+                    const std::size_t ic = static_cast<std::size_t>(starts[1] + c * steps[1]);
+                    out[o] = in[((ib * id[2] + iy) * id[3] + ix) * id[1] + ic];
+                }
+}
+
+// execute_concat_nhwc (kernels_scalar.cpp:892-952): inputs placed one after
+// another along the logical axis.
+void concat_nhwc(const std::vector<const u16*>& ins, const std::vector<std::array<int, 4>>& dims, u16* out,
+                 const std::array<int, 4>& od, int axis)
+{
+    std::array<int, 4> off{0, 0, 0, 0};
+    for (std::size_t k = 0; k < ins.size(); ++k) {
+        const auto& d = dims[k];
+        const u16* in = ins[k];
+        for (int b = 0; b < d[0]; ++b)
+            for (int y = 0; y < d[2]; ++y)
+                for (int x = 0; x < d[3]; ++x) {
+                    const u16* src = in + ((static_cast<std::size_t>(b) * d[2] + y) * d[3] + x) * d[1];
+                    u16* dst = out + ((static_cast<std::size_t>(b + off[0]) * od[2] + y + off[2]) * od[3] + x + off[3]) * od[1] + off[1];
+                    std::memcpy(dst, src, static_cast<std::size_t>(d[1]) * 2);
+                }
+        off[static_cast<std::size_t>(axis)] += d[static_cast<std::size_t>(axis)];
+    }
+}
+
+// execute_gather_general (execution_plan.cpp:101-168): 4-D data is indexed
+// in its NHWC order (logical axis a -> physical {0, 3, 1, 2}[a]); negative
+// indices count from the end; an index outside the axis is an error.
+void gather(const u16* data, const std::vector<std::int64_t>& shape, const std::int32_t* idx32, const std::int64_t* idx64,
+            std::size_t count, int axis, u16* out)
+{
+    const int rank = static_cast<int>(shape.size());
+    const int ax = axis < 0 ? axis + rank : axis;
+    if (ax < 0 || ax >= rank) throw std::runtime_error("oracle: GATHER axis out of range");
+    std::vector<std::int64_t> phys = shape;
+    int pax = ax;
+    if (rank == 4) {
+        phys = {shape[0], shape[2], shape[3], shape[1]};
+        static constexpr int kMap[4] = {0, 3, 1, 2};
+        pax = kMap[ax];
+    }
+    std::size_t outer = 1, inner = 1;
+    for (int d = 0; d < pax; ++d) outer *= static_cast<std::size_t>(phys[static_cast<std::size_t>(d)]);
+    for (int d = pax + 1; d < rank; ++d) inner *= static_cast<std::size_t>(phys[static_cast<std::size_t>(d)]);
+    const auto dim = static_cast<std::size_t>(phys[static_cast<std::size_t>(pax)]);
+    for (std::size_t o = 0; o < outer; ++o)
+        for (std::size_t i = 0; i < count; ++i) {
+            std::int64_t raw = idx32 ? idx32[i] : idx64[i];
+            if (raw < 0) raw += static_cast<std::int64_t>(dim);
+            if (raw < 0 || static_cast<std::size_t>(raw) >= dim) throw std::runtime_error("oracle: GATHER index out of range");
+            std::memcpy(out + (o * count + i) * inner, data + (o * dim + static_cast<std::size_t>(raw)) * inner, inner * 2);
+        }
+}
+
+// ------------------------------------------- real-model fused operators
+// reglu_nhwc (kernels_scalar.cpp:304-322, kernels_x86_avx2.cpp:443-470):
+// out = fp16(fp16(clamp(gate)) * linear), gate = channels [0, G), linear
+// [G, 2G) of each pixel. AVX2 lanes clamp as max(min(g, hi), lo).
+void reglu(const u16* in, u16* out, std::size_t spatial, std::size_t g, float lo, float hi, int isa)
+{
+    const std::size_t vec = isa == 0 ? g - g % 8 : 0;
+    for (std::size_t p = 0; p < spatial; ++p) {
+        const u16* ip = in + p * 2 * g;
+        for (std::size_t c = 0; c < g; ++c) {
+            const float x = h2f(ip[c]);
+            const float cg = h2f(f2h(c < vec ? maxps(minps(x, hi), lo) : std::min(std::max(x, lo), hi)));
+            out[p * g + c] = f2h(cg * h2f(ip[c + g]));
+        }
+    }
+}
+
+// feature_update_nhwc / feature_update_outputs_nhwc (kernels_scalar.cpp:
+// 324-405, kernels_x86_avx2.cpp:472-583). Per pixel, with input channels
+// a | b | c (C each) and the previous feature h:
+//   sb = fp16(sigmoid(b)), sc = fp16(sigmoid(c)),
+//   blended = fp16(fp16(sb*h) + fp16(fp16(1 - sb)*a)),
+//   scaled = fp16(fp16(sc*blended) * scale[ch]).
+// `feature` (stride 2C) gets scaled | blended; `scaled_out` / `blended_out`
+// (stride C) are optional. AVX2 lanes use the polynomial sigmoid for
+// channels below C - C % 8.
+void feature_update(const u16* in, const u16* hist, const u16* scale, u16* scaled_out, u16* blended_out, u16* feature,
+                    std::size_t spatial, std::size_t ch, int isa)
+{
+    const std::size_t vec = isa == 0 ? ch - ch % 8 : 0;
+    for (std::size_t p = 0; p < spatial; ++p) {
+        const u16* ip = in + p * 3 * ch;
+        for (std::size_t c = 0; c < ch; ++c) {
+            const bool lane = c < vec;
+            const float a = h2f(ip[c]), b = h2f(ip[c + ch]), cg = h2f(ip[c + 2 * ch]), prev = h2f(hist[p * ch + c]);
+            const float sb = h2f(f2h(lane ? sigmoid_lane(b) : sigmoid_exact(b)));
+            const float sc = h2f(f2h(lane ? sigmoid_lane(cg) : sigmoid_exact(cg)));
+            const float wb = h2f(f2h(sb * prev));
+            const float inv = h2f(f2h(1.0F - sb));
+            const float wa = h2f(f2h(inv * a));
+            const u16 blended = f2h(wb + wa);
+            const float gated = h2f(f2h(sc * h2f(blended)));
+            const u16 scaled = f2h(gated * h2f(scale[c]));
+            feature[p * 2 * ch + c] = scaled;
+            feature[p * 2 * ch + ch + c] = blended;
+            if (scaled_out) scaled_out[p * ch + c] = scaled;
+            if (blended_out) blended_out[p * ch + c] = blended;
+        }
+    }
+}
+
+// y0_tail_nhwc (kernels_scalar.cpp:407-481, kernels_x86_avx2.cpp:585-656;
+// the AVX2 form needs Q % 8 == 0). Channels of one pixel, q = 0..Q-1 and
+// its pair q + Q: prior = head (2Q) | tail (2Q).
+//   clipped = fp16(max(head, clip_min)), normalized = fp16(latent * fp16(1/clipped)),
+//   s = fp16(fp16(normalized - tail) * quant_scale),
+//   y_raw[q] = fp16(rne(fp16(s[q] + s[q+Q]))),
+//   upd = fp16(fp16(y_raw + tail) * update_scale{0,1}),
+//   concat2 = upd (2Q), concat3 = upd | prior (6Q).
+void y0_tail(const u16* latent, const u16* prior, const u16* qs, const u16* us0, const u16* us1, u16* normalized,
+             u16* clipped, u16* y_raw, u16* concat2, u16* concat3, float clip_min, std::size_t spatial, std::size_t q,
+             int isa)
+{
+    const bool lanes = isa == 0 && q % 8 == 0;
+    const std::size_t nc = 2 * q;
+    for (std::size_t p = 0; p < spatial; ++p) {
+        const u16* pri = prior + p * 4 * q;
+        for (std::size_t c = 0; c < q; ++c) {
+            float upd[2];
+            float s[2];
+            float tail[2];
+            for (int h = 0; h < 2; ++h) {
+                const std::size_t cc = c + static_cast<std::size_t>(h) * q;
+                const float head = h2f(pri[cc]);
+                const u16 clip = f2h(lanes ? maxps(head, clip_min) : std::max(head, clip_min));
+                const float inv = h2f(f2h(1.0F / h2f(clip)));
+                const u16 nrm = f2h(h2f(latent[p * nc + cc]) * inv);
+                normalized[p * nc + cc] = nrm;
+                clipped[p * nc + cc] = clip;
+                tail[h] = h2f(pri[cc + nc]);
+                const float d = h2f(f2h(h2f(nrm) - tail[h]));
+                s[h] = h2f(f2h(d * h2f(qs[p * nc + cc])));
+            }
+            const float sum = h2f(f2h(s[0] + s[1]));
+            const u16 rounded = f2h(std::nearbyint(sum));
+            y_raw[p * q + c] = rounded;
+            for (int h = 0; h < 2; ++h) {
+                const u16* us = h ? us1 : us0;
+                const float uin = h2f(f2h(h2f(rounded) + tail[h]));
+                upd[h] = h2f(f2h(uin * h2f(us[p * q + c])));
+                const std::size_t cc = c + static_cast<std::size_t>(h) * q;
+                concat2[p * nc + cc] = f2h(upd[h]);
+                concat3[p * 6 * q + cc] = f2h(upd[h]);
+            }
+        }
+        std::memcpy(concat3 + p * 6 * q + nc, pri, 4 * q * 2);
+    }
+}
+
+// y1_tail_nhwc (kernels_scalar.cpp:483-537, kernels_x86_avx2.cpp:658-712):
+//   s = fp16(fp16(normalized - prior) * quant_scale), y_raw as in y0_tail,
+//   upd = fp16(fp16(y_raw + prior) * update_scale{0,1}),
+//   out = fp16(fp16(concat2 + upd) * clipped).
+void y1_tail(const u16* normalized, const u16* prior, const u16* qs, const u16* us0, const u16* us1, const u16* concat2,
+             const u16* clipped, u16* y_raw, u16* out, std::size_t spatial, std::size_t q)
+{
+    const std::size_t nc = 2 * q;
+    for (std::size_t p = 0; p < spatial; ++p)
+        for (std::size_t c = 0; c < q; ++c) {
+            float s[2];
+            for (int h = 0; h < 2; ++h) {
+                const std::size_t cc = p * nc + c + static_cast<std::size_t>(h) * q;
+                const float d = h2f(f2h(h2f(normalized[cc]) - h2f(prior[cc])));
+                s[h] = h2f(f2h(d * h2f(qs[cc])));
+            }
+            const u16 rounded = f2h(std::nearbyint(h2f(f2h(s[0] + s[1]))));
+            y_raw[p * q + c] = rounded;
+            for (int h = 0; h < 2; ++h) {
+                const std::size_t cc = p * nc + c + static_cast<std::size_t>(h) * q;
+                const u16* us = h ? us1 : us0;
+                const float uin = h2f(f2h(h2f(rounded) + h2f(prior[cc])));
+                const float upd = h2f(f2h(uin * h2f(us[p * q + c])));
+                const float add = h2f(f2h(h2f(concat2[cc]) + upd));
+                out[cc] = f2h(add * h2f(clipped[cc]));
+            }
+        }
+}
+
 // ------------------------------------------------------ graph file parse
 // Minimal protobuf reader for mlvc.wire.Graph (proto/mlvc_model.proto:30-83).
 struct PbReader {
@@ -573,7 +934,11 @@ struct PbReader {
     }
 };
 
-enum Op { ADD = 1, CLIP = 4, CONCAT = 5, CONV = 6, D2S = 7, LEAKY = 9, S2D = 14 };
+// OpKind, proto/mlvc_model.proto:12-28.
+enum Op {
+    ADD = 1, SUB = 2, MUL = 3, CLIP = 4, CONCAT = 5, CONV = 6, D2S = 7, GATHER = 8, LEAKY = 9, RECIPROCAL = 10,
+    ROUND = 11, SIGMOID = 12, SLICE = 13, S2D = 14
+};
 
 struct GTensor {
     std::string name;
@@ -693,12 +1058,19 @@ struct ConvInfo {
     int n = 0, ic = 0, ih = 0, iw = 0, oc = 0, oh = 0, ow = 0, kh = 0, kw = 0, sh = 1, sw = 1, ph = 0, pw = 0;
     std::vector<u16> packed;
 };
+// FusedStepKind of fusion_matcher.hpp:12-20.
+enum StepKind { kSingle = 0, kConvEpi = 1, kRegluStep = 2, kFeature = 3, kFeatureOutputs = 4, kY0 = 5, kY1 = 6 };
 struct Step {
-    int kind = 0;  // 0 single node, 1 conv with epilogue
-    std::size_t node = 0;
+    int kind = kSingle;
+    std::size_t node = 0, end = 0;  // nodes [node, end) of the schedule
     Epilogue epi;
+    bool reglu_epi = false;  // kConvEpi with the ReGLU epilogue
     std::uint32_t conv_in = 0, residual = 0, out = 0;
     ConvInfo conv;
+    float lo = 0.0F, hi = 0.0F;
+    std::size_t ch = 0;                // gate / feature / quantised channels
+    std::vector<std::uint32_t> ids;    // operands and results of fused kinds
+    std::array<int, 4> id4{}, od4{}, starts{}, steps{};  // SLICE
 };
 
 class Plan {
@@ -729,8 +1101,8 @@ public:
         for (std::size_t id = 1; id < g_.t.size(); ++id) {
             const GTensor& t = g_.t[id];
             if (t.name.empty()) continue;
-            // FP16 activations; INT32 graph inputs (q_index_shifted, which no
-            // operator of this path reads) are carried as raw bytes.
+            // FP16 activations; INT32 graph inputs (q_index_shifted, read by
+            // GATHER as indices) are carried as raw bytes.
             const bool int32_input = t.dtype == 2 && in_pos_.count(static_cast<std::uint32_t>(id));
             if (t.dtype != 1 && !t.weight && !int32_input)
                 throw std::runtime_error("oracle: only FP16 activations are on this path");
@@ -744,6 +1116,12 @@ public:
             std::memcpy(raw.data(), weights_.data() + t.woff, raw.size() * 2);
             if (needs_nhwc(t)) nchw_to_nhwc(raw.data(), bufs_[id].data(), static_cast<std::size_t>(t.shape[0]), static_cast<std::size_t>(t.shape[1]), static_cast<std::size_t>(t.shape[2] * t.shape[3]));
             else bufs_[id] = raw;
+        }
+        for (const GNode& n : g_.nodes) {
+            if (n.out.size() != 1) throw std::runtime_error("oracle: every node has one output");
+            for (auto id : n.in)
+                if (id >= g_.t.size() || (id && g_.t[id].name.empty())) throw std::runtime_error("oracle: node input is not a tensor");
+            if (!n.out[0] || n.out[0] >= g_.t.size() || g_.t[n.out[0]].name.empty()) throw std::runtime_error("oracle: node output is not a tensor");
         }
         compile(fuse);
         initialized_ = bindings_.empty();
@@ -884,27 +1262,445 @@ private:
         return false;
     }
 
+    // ---- helpers of the fusion matcher (fusion_matcher.cpp:78-256)
+    bool is_output(std::uint32_t id) const { return std::find(g_.outputs.begin(), g_.outputs.end(), id) != g_.outputs.end(); }
+    bool internal_only(std::uint32_t id, int n) const
+    {
+        const auto it = consumers_.find(id);
+        return id && !is_output(id) && (it == consumers_.end() ? 0 : it->second) == n;
+    }
+    bool int64_init(std::uint32_t id, std::vector<std::int64_t>& v) const
+    {
+        if (!is_init(id) || g_.t[id].dtype != 3 || g_.t[id].wbytes % 8) return false;
+        v.resize(g_.t[id].wbytes / 8);
+        if (!v.empty()) std::memcpy(v.data(), weights_.data() + g_.t[id].woff, g_.t[id].wbytes);
+        return true;
+    }
+    bool fp16_scalar_init(std::uint32_t id, float& v) const
+    {
+        if (!is_init(id) || g_.t[id].dtype != 1 || g_.t[id].wbytes != 2) return false;
+        u16 h;
+        std::memcpy(&h, weights_.data() + g_.t[id].woff, 2);
+        v = h2f(h);
+        return true;
+    }
+    bool clip_constants(const GNode& n, float& lo, float& hi) const
+    {
+        if (n.op != CLIP || n.in.size() < 2 || n.out.size() != 1) return false;
+        lo = -HUGE_VALF;
+        hi = HUGE_VALF;
+        if (n.in[1] && !fp16_scalar_init(n.in[1], lo)) return false;
+        if (n.in.size() >= 3 && n.in[2] && !fp16_scalar_init(n.in[2], hi)) return false;
+        return true;
+    }
+    bool channel_slice(const GNode& n, std::uint32_t x, std::int64_t b, std::int64_t e) const
+    {
+        if (n.op != SLICE || n.in.size() < 3 || n.out.size() != 1 || n.in[0] != x) return false;
+        std::vector<std::int64_t> st, en, ax, sp;
+        if (!int64_init(n.in[1], st) || !int64_init(n.in[2], en) || st.size() != 1 || en.size() != 1 || st[0] != b || en[0] != e)
+            return false;
+        if (n.in.size() < 4 || !n.in[3] || !int64_init(n.in[3], ax) || ax.size() != 1 || ax[0] != 1) return false;
+        if (n.in.size() >= 5 && n.in[4] && (!int64_init(n.in[4], sp) || sp.size() != 1 || sp[0] != 1)) return false;
+        const GTensor& o = g_.t[n.out[0]];
+        return o.dtype == 1 && o.shape.size() == 4 && o.shape[1] == e - b;
+    }
+    static bool pair(const GNode& n, int op, std::uint32_t x, std::uint32_t y)
+    {
+        return n.op == op && n.in.size() == 2 && n.out.size() == 1 &&
+               ((n.in[0] == x && n.in[1] == y) || (n.in[0] == y && n.in[1] == x));
+    }
+    static bool other_in_pair(const GNode& n, int op, std::uint32_t x, std::uint32_t& other)
+    {
+        if (n.op != op || n.in.size() != 2 || n.out.size() != 1) return false;
+        if (n.in[0] == x) { other = n.in[1]; return true; }
+        if (n.in[1] == x) { other = n.in[0]; return true; }
+        return false;
+    }
+    bool fp16_of(std::uint32_t id, const std::vector<std::int64_t>& shape) const
+    {
+        return id && id < g_.t.size() && !g_.t[id].name.empty() && g_.t[id].dtype == 1 && g_.t[id].shape == shape;
+    }
+    // is_standard_conv (fusion_matcher.cpp:230-256) with require_1x1.
+    bool std_1x1_conv(const GNode& c) const
+    {
+        if (c.op != CONV || c.in.size() < 2 || c.out.size() != 1 || c.groups != 1 || c.strides.size() != 2 ||
+            c.pads.size() != 4 || c.dil.size() != 2 || c.dil[0] != 1 || c.dil[1] != 1)
+            return false;
+        const GTensor& w = g_.t[c.in[1]];
+        if (!w.weight || w.dtype != 1 || w.shape.size() != 4) return false;
+        if (g_.t[c.in[0]].dtype != 1 || g_.t[c.in[0]].shape.size() != 4 || g_.t[c.out[0]].dtype != 1 || g_.t[c.out[0]].shape.size() != 4)
+            return false;
+        return w.shape[2] == 1 && w.shape[3] == 1 && c.strides[0] == 1 && c.strides[1] == 1 && c.pads[0] == 0 && c.pads[1] == 0 &&
+               c.pads[2] == 0 && c.pads[3] == 0;
+    }
+
+    // try_pointwise_reglu (fusion_matcher.cpp:258-302): 1x1 conv (2G
+    // outputs) -> SLICE [0,G) / [G,2G) -> CLIP(gate) -> MUL(clipped, linear).
+    bool try_conv_reglu(std::size_t i, Step& s) const
+    {
+        const auto& ns = g_.nodes;
+        if (i + 5 > ns.size() || !std_1x1_conv(ns[i])) return false;
+        const std::uint32_t co = ns[i].out[0];
+        if (!internal_only(co, 2)) return false;
+        const auto& cs = g_.t[co].shape;
+        if (cs[1] <= 0 || cs[1] % 2) return false;
+        const std::int64_t g = cs[1] / 2;
+        if (!channel_slice(ns[i + 1], co, 0, g) || !channel_slice(ns[i + 2], co, g, 2 * g)) return false;
+        const std::uint32_t gate = ns[i + 1].out[0], lin = ns[i + 2].out[0];
+        if (!internal_only(gate, 1) || !internal_only(lin, 1)) return false;
+        float lo, hi;
+        if (!clip_constants(ns[i + 3], lo, hi) || ns[i + 3].in[0] != gate) return false;
+        const std::uint32_t clipped = ns[i + 3].out[0];
+        if (!internal_only(clipped, 1) || !pair(ns[i + 4], MUL, clipped, lin)) return false;
+        s = Step{};
+        s.kind = kConvEpi;
+        s.reglu_epi = true;
+        s.node = i;
+        s.end = i + 5;
+        s.lo = lo;
+        s.hi = hi;
+        s.conv_in = ns[i].in[0];
+        s.out = ns[i + 4].out[0];
+        s.ch = static_cast<std::size_t>(g);
+        return true;
+    }
+
+    // try_reglu (fusion_matcher.cpp:304-346).
+    bool try_reglu(std::size_t i, Step& s) const
+    {
+        const auto& ns = g_.nodes;
+        if (i + 4 > ns.size() || ns[i].op != SLICE || ns[i].in.empty()) return false;
+        const std::uint32_t x = ns[i].in[0];
+        const GTensor& t = g_.t[x];
+        if (t.name.empty() || t.dtype != 1 || t.shape.size() != 4 || t.shape[1] <= 0 || t.shape[1] % 2) return false;
+        const std::int64_t g = t.shape[1] / 2;
+        if (!channel_slice(ns[i], x, 0, g) || !channel_slice(ns[i + 1], x, g, 2 * g)) return false;
+        const std::uint32_t gate = ns[i].out[0], lin = ns[i + 1].out[0];
+        if (!internal_only(gate, 1) || !internal_only(lin, 1)) return false;
+        float lo, hi;
+        if (!clip_constants(ns[i + 2], lo, hi) || ns[i + 2].in[0] != gate) return false;
+        const std::uint32_t clipped = ns[i + 2].out[0];
+        if (!internal_only(clipped, 1) || !pair(ns[i + 3], MUL, clipped, lin)) return false;
+        s = Step{};
+        s.kind = kRegluStep;
+        s.node = i;
+        s.end = i + 4;
+        s.lo = lo;
+        s.hi = hi;
+        s.ids = {x};
+        s.out = ns[i + 3].out[0];
+        s.ch = static_cast<std::size_t>(g);
+        return true;
+    }
+
+    // try_feature_update (fusion_matcher.cpp:413-541): three channel slices
+    // a | b | c, two SIGMOIDs, w_b = sb*h, inv = 1 - sb, w_a = inv*a,
+    // blended = w_b + w_a, gated = sc*blended, scaled = gated*scale[1,C,1,1],
+    // then CONCAT(scaled, blended) right after (one output) or further down
+    // (three outputs; the CONCAT node is then skipped).
+    bool try_feature(std::size_t i, std::vector<bool>& elided, Step& s) const
+    {
+        const auto& ns = g_.nodes;
+        if (i + 11 > ns.size() || ns[i].op != SLICE || ns[i].in.empty()) return false;
+        const std::uint32_t x = ns[i].in[0];
+        const GTensor& t = g_.t[x];
+        if (t.name.empty() || t.dtype != 1 || t.shape.size() != 4 || t.shape[1] <= 0 || t.shape[1] % 3) return false;
+        const std::int64_t ch = t.shape[1] / 3;
+        if (!channel_slice(ns[i], x, 0, ch) || !channel_slice(ns[i + 1], x, ch, 2 * ch) || !channel_slice(ns[i + 2], x, 2 * ch, 3 * ch))
+            return false;
+        const std::uint32_t a = ns[i].out[0], b = ns[i + 1].out[0], cg = ns[i + 2].out[0];
+        if (!internal_only(a, 1) || !internal_only(b, 1) || !internal_only(cg, 1)) return false;
+        const GNode& s0 = ns[i + 3];
+        const GNode& s1 = ns[i + 4];
+        if (s0.op != SIGMOID || s0.in.size() != 1 || s0.in[0] != b || s0.out.size() != 1 || s1.op != SIGMOID ||
+            s1.in.size() != 1 || s1.in[0] != cg || s1.out.size() != 1)
+            return false;
+        const std::uint32_t sb = s0.out[0], sc = s1.out[0];
+        if (!internal_only(sb, 2) || !internal_only(sc, 1)) return false;
+        std::uint32_t hist = 0;
+        if (!other_in_pair(ns[i + 5], MUL, sb, hist)) return false;
+        if (is_init(hist) || !fp16_of(hist, g_.t[a].shape)) return false;
+        const std::uint32_t wb = ns[i + 5].out[0];
+        if (!internal_only(wb, 1)) return false;
+        const GNode& sub = ns[i + 6];
+        if (sub.op != SUB || sub.in.size() != 2 || sub.out.size() != 1 || sub.in[1] != sb) return false;
+        float one = 0.0F;
+        if (!fp16_scalar_init(sub.in[0], one) || std::fabs(one - 1.0F) > 1e-4F) return false;
+        const std::uint32_t inv = sub.out[0];
+        if (!internal_only(inv, 1) || !pair(ns[i + 7], MUL, inv, a)) return false;
+        const std::uint32_t wa = ns[i + 7].out[0];
+        if (!internal_only(wa, 1) || !pair(ns[i + 8], ADD, wb, wa)) return false;
+        const std::uint32_t blended = ns[i + 8].out[0];
+        if (!pair(ns[i + 9], MUL, sc, blended)) return false;
+        const std::uint32_t gated = ns[i + 9].out[0];
+        if (!internal_only(gated, 1)) return false;
+        std::uint32_t scale = 0;
+        if (!other_in_pair(ns[i + 10], MUL, gated, scale)) return false;
+        if (!fp16_of(scale, {1, ch, 1, 1})) return false;
+        const std::uint32_t scaled = ns[i + 10].out[0];
+        auto concat_of = [&](const GNode& c) {
+            const int ax = c.attr == 5 ? c.axis : 0;
+            return c.op == CONCAT && ax == 1 && c.in.size() == 2 && c.in[0] == scaled && c.in[1] == blended && c.out.size() == 1;
+        };
+        if (i + 12 <= ns.size() && internal_only(scaled, 1) && internal_only(blended, 2) && concat_of(ns[i + 11])) {
+            s = Step{};
+            s.kind = kFeature;
+            s.node = i;
+            s.end = i + 12;
+            s.ids = {x, hist, scale};
+            s.out = ns[i + 11].out[0];
+            s.ch = static_cast<std::size_t>(ch);
+            return true;
+        }
+        if (!is_output(scaled) && internal_only(blended, 2)) {
+            for (std::size_t j = i + 11; j < ns.size(); ++j) {
+                if (!concat_of(ns[j])) continue;
+                elided[j] = true;
+                s = Step{};
+                s.kind = kFeatureOutputs;
+                s.node = i;
+                s.end = i + 11;
+                s.ids = {x, hist, scale, scaled, blended};
+                s.out = ns[j].out[0];
+                s.ch = static_cast<std::size_t>(ch);
+                return true;
+            }
+        }
+        return false;
+    }
+
+    // The update part shared by both quantisation tails
+    // (fusion_matcher.cpp:620-697 and 760-836), starting at node k with
+    // `scaled` = fp16((normalized - tail) * quant_scale) already matched:
+    // two half slices, ADD, ROUND, two tail slices, (y_raw + tail_h) *
+    // update_scale_h. Returns the first node after it, or 0.
+    std::size_t match_update(std::size_t k, std::uint32_t scaled, std::uint32_t tail, std::int64_t q,
+                             const std::vector<std::int64_t>& qshape, std::uint32_t& y_raw, std::uint32_t& u0,
+                             std::uint32_t& u1, std::uint32_t& us0, std::uint32_t& us1) const
+    {
+        const auto& ns = g_.nodes;
+        if (!channel_slice(ns[k], scaled, 0, q) || !channel_slice(ns[k + 1], scaled, q, 2 * q)) return 0;
+        const std::uint32_t h0 = ns[k].out[0], h1 = ns[k + 1].out[0];
+        if (!internal_only(h0, 1) || !internal_only(h1, 1) || !pair(ns[k + 2], ADD, h0, h1)) return 0;
+        const std::uint32_t sum = ns[k + 2].out[0];
+        if (!internal_only(sum, 1)) return 0;
+        const GNode& rnd = ns[k + 3];
+        if (rnd.op != ROUND || rnd.in.size() != 1 || rnd.in[0] != sum || rnd.out.size() != 1) return 0;
+        y_raw = rnd.out[0];
+        if (!channel_slice(ns[k + 4], tail, 0, q) || !channel_slice(ns[k + 5], tail, q, 2 * q)) return 0;
+        const std::uint32_t t0 = ns[k + 4].out[0], t1 = ns[k + 5].out[0];
+        if (!internal_only(t0, 1) || !internal_only(t1, 1)) return 0;
+        if (!pair(ns[k + 6], ADD, y_raw, t0)) return 0;
+        const std::uint32_t a0 = ns[k + 6].out[0];
+        if (!internal_only(a0, 1) || !other_in_pair(ns[k + 7], MUL, a0, us0) || !fp16_of(us0, qshape)) return 0;
+        u0 = ns[k + 7].out[0];
+        if (!internal_only(u0, 1) || !pair(ns[k + 8], ADD, y_raw, t1)) return 0;
+        const std::uint32_t a1 = ns[k + 8].out[0];
+        if (!internal_only(a1, 1) || !other_in_pair(ns[k + 9], MUL, a1, us1) || !fp16_of(us1, qshape)) return 0;
+        u1 = ns[k + 9].out[0];
+        if (!internal_only(u1, 1)) return 0;
+        return k + 10;
+    }
+
+    // try_y0_tail (fusion_matcher.cpp:543-696).
+    bool try_y0(std::size_t i, Step& s) const
+    {
+        const auto& ns = g_.nodes;
+        if (i + 19 > ns.size() || ns[i].op != SLICE || ns[i].in.empty()) return false;
+        const std::uint32_t prior = ns[i].in[0];
+        const GTensor& pt = g_.t[prior];
+        if (pt.name.empty() || pt.dtype != 1 || pt.shape.size() != 4 || pt.shape[1] <= 0 || pt.shape[1] % 4) return false;
+        const std::int64_t q = pt.shape[1] / 4;
+        if (!channel_slice(ns[i], prior, 0, 2 * q) || !channel_slice(ns[i + 1], prior, 2 * q, 4 * q)) return false;
+        const std::uint32_t head = ns[i].out[0], tail = ns[i + 1].out[0];
+        if (!internal_only(head, 1) || !internal_only(tail, 3)) return false;
+        float lo, hi;
+        if (!clip_constants(ns[i + 2], lo, hi) || ns[i + 2].in[0] != head || hi < 65504.0F) return false;
+        const std::uint32_t clipped = ns[i + 2].out[0];
+        if (is_output(clipped)) return false;
+        const GNode& rec = ns[i + 3];
+        if (rec.op != RECIPROCAL || rec.in.size() != 1 || rec.in[0] != clipped || rec.out.size() != 1) return false;
+        std::uint32_t inv = rec.out[0];
+        if (!internal_only(inv, 1)) return false;
+        std::size_t k = i + 4;
+        if (k + 15 <= ns.size() && ns[k].op == MUL && ns[k].in.size() == 2 && ns[k].out.size() == 1) {
+            std::uint32_t other = 0;
+            float one = 0.0F;
+            if (other_in_pair(ns[k], MUL, inv, other) && fp16_scalar_init(other, one) && std::fabs(one - 1.0F) <= 1e-4F) {
+                inv = ns[k].out[0];
+                if (!internal_only(inv, 1)) return false;
+                ++k;
+            }
+        }
+        if (k + 15 > ns.size()) return false;
+        const std::vector<std::int64_t> nshape{pt.shape[0], 2 * q, pt.shape[2], pt.shape[3]};
+        const std::vector<std::int64_t> qshape{pt.shape[0], q, pt.shape[2], pt.shape[3]};
+        std::uint32_t latent = 0;
+        if (!other_in_pair(ns[k], MUL, inv, latent) || is_init(latent) || !fp16_of(latent, nshape)) return false;
+        const std::uint32_t normalized = ns[k].out[0];
+        const GNode& sub = ns[k + 1];
+        if (sub.op != SUB || sub.in.size() != 2 || sub.out.size() != 1 || sub.in[0] != normalized || sub.in[1] != tail) return false;
+        const std::uint32_t diff = sub.out[0];
+        std::uint32_t qs = 0;
+        if (!internal_only(diff, 1) || !other_in_pair(ns[k + 2], MUL, diff, qs) || !fp16_of(qs, nshape)) return false;
+        const std::uint32_t scaled = ns[k + 2].out[0];
+        if (!internal_only(scaled, 2)) return false;
+        std::uint32_t y_raw, u0, u1, us0, us1;
+        const std::size_t e = match_update(k + 3, scaled, tail, q, qshape, y_raw, u0, u1, us0, us1);
+        if (!e) return false;
+        const GNode& c2 = ns[e];
+        const GNode& c3 = ns[e + 1];
+        auto axis1 = [](const GNode& c) { return (c.attr == 5 ? c.axis : 0) == 1; };
+        if (c2.op != CONCAT || !axis1(c2) || c2.in.size() != 2 || c2.in[0] != u0 || c2.in[1] != u1 || c2.out.size() != 1) return false;
+        const std::uint32_t concat2 = c2.out[0];
+        if (c3.op != CONCAT || !axis1(c3) || c3.in.size() != 2 || c3.in[0] != concat2 || c3.in[1] != prior || c3.out.size() != 1)
+            return false;
+        s = Step{};
+        s.kind = kY0;
+        s.node = i;
+        s.end = e + 2;
+        s.ids = {latent, prior, qs, us0, us1, normalized, clipped, y_raw, concat2, c3.out[0]};
+        s.out = c3.out[0];
+        s.lo = lo;
+        s.ch = static_cast<std::size_t>(q);
+        return true;
+    }
+
+    // try_y1_tail (fusion_matcher.cpp:698-850).
+    bool try_y1(std::size_t i, Step& s) const
+    {
+        const auto& ns = g_.nodes;
+        if (i + 15 > ns.size()) return false;
+        const GNode& sub = ns[i];
+        if (sub.op != SUB || sub.in.size() != 2 || sub.out.size() != 1) return false;
+        const std::uint32_t normalized = sub.in[0], prior = sub.in[1];
+        const GTensor& nt = g_.t[normalized];
+        const GTensor& pt = g_.t[prior];
+        if (!normalized || !prior || nt.name.empty() || pt.name.empty() || nt.dtype != 1 || pt.dtype != 1 || nt.shape.size() != 4 ||
+            nt.shape != pt.shape || nt.shape[1] <= 0 || nt.shape[1] % 2)
+            return false;
+        const std::int64_t q = nt.shape[1] / 2;
+        const std::vector<std::int64_t> qshape{nt.shape[0], q, nt.shape[2], nt.shape[3]};
+        const std::uint32_t diff = sub.out[0];
+        std::uint32_t qs = 0;
+        if (!internal_only(diff, 1) || !other_in_pair(ns[i + 1], MUL, diff, qs) || !fp16_of(qs, nt.shape)) return false;
+        const std::uint32_t scaled = ns[i + 1].out[0];
+        if (!internal_only(scaled, 2)) return false;
+        std::uint32_t y_raw, u0, u1, us0, us1;
+        const std::size_t e = match_update(i + 2, scaled, prior, q, qshape, y_raw, u0, u1, us0, us1);
+        if (!e) return false;
+        const GNode& c2 = ns[e];
+        if (c2.op != CONCAT || (c2.attr == 5 ? c2.axis : 0) != 1 || c2.in.size() != 2 || c2.in[0] != u0 || c2.in[1] != u1 ||
+            c2.out.size() != 1)
+            return false;
+        const std::uint32_t cat = c2.out[0];
+        std::uint32_t concat2 = 0, clipped = 0;
+        if (!internal_only(cat, 1) || !other_in_pair(ns[e + 1], ADD, cat, concat2) || is_init(concat2) || !fp16_of(concat2, nt.shape))
+            return false;
+        const std::uint32_t added = ns[e + 1].out[0];
+        if (!internal_only(added, 1) || !other_in_pair(ns[e + 2], MUL, added, clipped) || is_init(clipped) ||
+            !fp16_of(clipped, nt.shape))
+            return false;
+        s = Step{};
+        s.kind = kY1;
+        s.node = i;
+        s.end = e + 3;
+        s.ids = {normalized, prior, qs, us0, us1, concat2, clipped, y_raw, ns[e + 2].out[0]};
+        s.out = ns[e + 2].out[0];
+        s.ch = static_cast<std::size_t>(q);
+        return true;
+    }
+
+    static std::array<int, 4> dims4(const std::vector<std::int64_t>& s)
+    {
+        if (s.size() != 4) throw std::runtime_error("oracle: expected 4D NCHW tensor");
+        std::array<int, 4> d{};
+        for (std::size_t i = 0; i < 4; ++i) {
+            if (s[i] <= 0 || s[i] > 0x7FFFFFFF) throw std::runtime_error("oracle: tensor dimension out of int range");
+            d[i] = static_cast<int>(s[i]);
+        }
+        return d;
+    }
+
+    // SLICE parameters (execution_plan.cpp:565-604): starts (negative ones
+    // count from the end, clamped to [0, dim]) and steps per axis; the
+    // output shape gives the extent, `ends` is not read.
+    void compile_slice(const GNode& n, Step& s) const
+    {
+        const GTensor& in = g_.t[n.in.at(0)];
+        s.id4 = dims4(in.shape);
+        s.od4 = dims4(g_.t[n.out.at(0)].shape);
+        s.starts = {0, 0, 0, 0};
+        s.steps = {1, 1, 1, 1};
+        std::vector<std::int64_t> st, en, ax, sp;
+        if (n.in.size() < 3 || !int64_init(n.in[1], st) || !int64_init(n.in[2], en))
+            throw std::runtime_error("oracle: SLICE starts/ends must be INT64 initializers");
+        if (n.in.size() > 3 && n.in[3]) {
+            if (!int64_init(n.in[3], ax)) throw std::runtime_error("oracle: SLICE axes must be an INT64 initializer");
+        } else {
+            for (std::size_t a = 0; a < st.size(); ++a) ax.push_back(static_cast<std::int64_t>(a));
+        }
+        sp.assign(st.size(), 1);
+        if (n.in.size() > 4 && n.in[4] && !int64_init(n.in[4], sp)) throw std::runtime_error("oracle: SLICE steps must be an INT64 initializer");
+        if (ax.size() < st.size() || sp.size() < st.size()) throw std::runtime_error("oracle: SLICE parameter lengths differ");
+        for (std::size_t a = 0; a < st.size(); ++a) {
+            int x = static_cast<int>(ax[a]);
+            if (x < 0) x += 4;
+            if (x < 0 || x >= 4) throw std::runtime_error("oracle: SLICE axis out of range");
+            const std::int64_t dim = in.shape[static_cast<std::size_t>(x)];
+            std::int64_t v = st[a];
+            if (v < 0) v += dim;
+            v = std::clamp<std::int64_t>(v, 0, dim);
+            s.starts[static_cast<std::size_t>(x)] = static_cast<int>(v);
+            s.steps[static_cast<std::size_t>(x)] = static_cast<int>(sp[a]);
+        }
+        // Every element read must lie inside the input (the reference does
+        // not check; an out-of-range read is undefined there).
+        for (std::size_t d = 0; d < 4; ++d) {
+            const std::int64_t last = s.starts[d] + static_cast<std::int64_t>(s.od4[d] - 1) * s.steps[d];
+            if (s.starts[d] >= s.id4[d] || last < 0 || last >= s.id4[d]) throw std::runtime_error("oracle: SLICE reads outside its input");
+        }
+    }
+
     void compile(bool fuse)
     {
-        std::map<std::uint32_t, int> consumers;
+        consumers_.clear();
         for (const GNode& n : g_.nodes)
             for (auto id : n.in)
-                if (id) ++consumers[id];
+                if (id) ++consumers_[id];
+        std::vector<bool> elided(g_.nodes.size(), false);
         for (std::size_t i = 0; i < g_.nodes.size();) {
+            if (elided[i]) {
+                ++i;
+                continue;
+            }
             Step s;
-            if (fuse && try_epilogue(i, consumers, s)) {
-                s.conv = conv_info(g_.nodes[i]);
+            // build_fused_schedule's order (fusion_matcher.cpp:50-72).
+            if (fuse && (try_y0(i, s) || try_y1(i, s) || try_feature(i, elided, s) || try_conv_reglu(i, s) || try_reglu(i, s) ||
+                         try_epilogue(i, consumers_, s))) {
+                if (s.kind == kConvEpi) s.conv = conv_info(g_.nodes[i]);
+                if (s.end == 0) s.end = i + 2;
+                i = s.end;
                 steps_.push_back(std::move(s));
-                i += 2;
                 continue;
             }
             s = Step{};
             s.node = i;
+            s.end = i + 1;
             const GNode& n = g_.nodes[i];
             switch (n.op) {
             case CONV: s.conv = conv_info(n); break;
-            case LEAKY: case ADD: case D2S: case S2D: case CONCAT: break;
-            default: throw std::runtime_error("oracle: operator outside the conv-graph path: " + std::to_string(n.op));
+            case SLICE: compile_slice(n, s); break;
+            case CLIP:
+                s.lo = -HUGE_VALF;
+                s.hi = HUGE_VALF;
+                if (n.in.size() > 1 && n.in[1] && !fp16_scalar_init(n.in[1], s.lo)) throw std::runtime_error("oracle: expected scalar FP16 initializer");
+                if (n.in.size() > 2 && n.in[2] && !fp16_scalar_init(n.in[2], s.hi)) throw std::runtime_error("oracle: expected scalar FP16 initializer");
+                break;
+            case LEAKY: case ADD: case SUB: case MUL: case D2S: case S2D: case CONCAT: case GATHER: case SIGMOID: case RECIPROCAL:
+            case ROUND:
+                break;
+            default: throw std::runtime_error("oracle: unsupported AOT operator: " + std::to_string(n.op));
             }
             s.out = n.out.at(0);
             steps_.push_back(std::move(s));
@@ -914,8 +1710,11 @@ private:
 
     void run_conv(const ConvInfo& c, std::uint32_t in, std::uint32_t out, Epilogue e)
     {
-        const u16* ip = bufs_[in].data();
-        u16* op = bufs_[out].data();
+        run_conv_ptr(c, bufs_[in].data(), bufs_[out].data(), e);
+    }
+
+    void run_conv_ptr(const ConvInfo& c, const u16* ip, u16* op, Epilogue e)
+    {
         if (c.depthwise) {
             depthwise_nhwc(pool_, isa_, ip, c.packed.data(), op, c.n, c.ic, c.ih, c.iw, c.oh, c.ow, c.kh, c.kw, c.sh, c.sw, c.ph, c.pw);
         } else if (c.is1x1) {
@@ -925,13 +1724,81 @@ private:
         }
     }
 
+    static std::size_t spatial_of(const std::vector<std::int64_t>& shape)
+    {
+        const auto d = dims4(shape);
+        return static_cast<std::size_t>(d[0]) * d[2] * d[3];
+    }
+
+    void exec_binary(const GNode& n, u16* o)
+    {
+        const int op = n.op == SUB ? kBSub : n.op == MUL ? kBMul : kBAdd;
+        binary_dispatch(bufs_[n.in.at(0)].data(), g_.t[n.in[0]].shape, bufs_[n.in.at(1)].data(), g_.t[n.in[1]].shape, o,
+                        g_.t[n.out[0]].shape, op);
+    }
+
+    // execute_gather_general call site, execution_plan.cpp:1004-1012: INT32
+    // indices (a graph input such as q_index_shifted) or INT64 initializers.
+    void exec_gather(const GNode& n, u16* o)
+    {
+        const std::uint32_t d = n.in.at(0), ix = n.in.at(1);
+        const GTensor& it = g_.t[ix];
+        const std::size_t count = elems(it.shape);
+        std::vector<std::int64_t> i64;
+        const std::int32_t* i32 = nullptr;
+        if (it.dtype == 2 && !it.weight) {
+            i32 = reinterpret_cast<const std::int32_t*>(bufs_[ix].data());
+        } else if (!int64_init(ix, i64)) {
+            throw std::runtime_error("oracle: GATHER indices must be INT32 graph inputs or INT64 initializers");
+        }
+        const auto& ds = g_.t[d].shape;
+        const int rank = static_cast<int>(ds.size());
+        const int ax = n.axis < 0 ? n.axis + rank : n.axis;
+        if (ax < 0 || ax >= rank) throw std::runtime_error("oracle: GATHER axis out of range");
+        if (elems(ds) / static_cast<std::size_t>(ds[static_cast<std::size_t>(ax)]) * count != bufs_[n.out[0]].size())
+            throw std::runtime_error("oracle: GATHER output size mismatch");
+        gather(bufs_[d].data(), ds, i32, i32 ? nullptr : i64.data(), count, n.axis, o);
+    }
+
     void exec(const Step& s)
     {
-        if (s.kind == 1) {
-            Epilogue e = s.epi;
-            if (s.residual) e.residual = bufs_[s.residual].data();
-            run_conv(s.conv, s.conv_in, s.out, e);
+        switch (s.kind) {
+        case kConvEpi:
+            if (s.reglu_epi) {
+                // The GEMM writes the rounded 2G-channel conv output, then the
+                // ReGLU post-pass (kernels_x86_avx2.cpp:216-233, kernels_scalar.cpp:121-152).
+                const auto& cs = g_.t[g_.nodes[s.node].out[0]].shape;
+                std::vector<u16> tmp(elems(cs));
+                run_conv_ptr(s.conv, bufs_[s.conv_in].data(), tmp.data(), Epilogue{});
+                reglu(tmp.data(), bufs_[s.out].data(), spatial_of(cs), s.ch, s.lo, s.hi, isa_);
+            } else {
+                Epilogue e = s.epi;
+                if (s.residual) e.residual = bufs_[s.residual].data();
+                run_conv(s.conv, s.conv_in, s.out, e);
+            }
             return;
+        case kRegluStep:
+            reglu(bufs_[s.ids[0]].data(), bufs_[s.out].data(), spatial_of(g_.t[s.out].shape), s.ch, s.lo, s.hi, isa_);
+            return;
+        case kFeature:
+        case kFeatureOutputs: {
+            const bool three = s.kind == kFeatureOutputs;
+            feature_update(bufs_[s.ids[0]].data(), bufs_[s.ids[1]].data(), bufs_[s.ids[2]].data(),
+                           three ? bufs_[s.ids[3]].data() : nullptr, three ? bufs_[s.ids[4]].data() : nullptr, bufs_[s.out].data(),
+                           spatial_of(g_.t[s.ids[1]].shape), s.ch, isa_);
+            return;
+        }
+        case kY0: {
+            auto p = [&](int k) { return bufs_[s.ids[static_cast<std::size_t>(k)]].data(); };
+            y0_tail(p(0), p(1), p(2), p(3), p(4), p(5), p(6), p(7), p(8), p(9), s.lo, spatial_of(g_.t[s.ids[7]].shape), s.ch, isa_);
+            return;
+        }
+        case kY1: {
+            auto p = [&](int k) { return bufs_[s.ids[static_cast<std::size_t>(k)]].data(); };
+            y1_tail(p(0), p(1), p(2), p(3), p(4), p(5), p(6), p(7), p(8), spatial_of(g_.t[s.ids[7]].shape), s.ch);
+            return;
+        }
+        default: break;
         }
         const GNode& n = g_.nodes[s.node];
         const GTensor& ot = g_.t[s.out];
@@ -939,11 +1806,13 @@ private:
         switch (n.op) {
         case CONV: run_conv(s.conv, n.in[0], s.out, Epilogue{}); break;
         case LEAKY: leaky(bufs_[n.in[0]].data(), o, bufs_[s.out].size(), n.attr == 6 ? n.alpha : 0.01F, isa_); break;
-        case ADD:
-            if (g_.t[n.in[0]].shape != ot.shape || g_.t[n.in[1]].shape != ot.shape)
-                throw std::runtime_error("oracle: broadcast ADD is outside the conv-graph path");
-            add(bufs_[n.in[0]].data(), bufs_[n.in[1]].data(), o, bufs_[s.out].size(), isa_);
-            break;
+        case ADD: case SUB: case MUL: exec_binary(n, o); break;
+        case CLIP: unary(bufs_[n.in[0]].data(), o, bufs_[s.out].size(), kUClip, s.lo, s.hi, isa_); break;
+        case SIGMOID: unary(bufs_[n.in[0]].data(), o, bufs_[s.out].size(), kUSigmoid, 0.0F, 0.0F, isa_); break;
+        case RECIPROCAL: unary(bufs_[n.in[0]].data(), o, bufs_[s.out].size(), kUReciprocal, 0.0F, 0.0F, isa_); break;
+        case ROUND: unary(bufs_[n.in[0]].data(), o, bufs_[s.out].size(), kURound, 0.0F, 0.0F, isa_); break;
+        case SLICE: slice_nhwc(bufs_[n.in[0]].data(), o, s.id4.data(), s.od4.data(), s.starts.data(), s.steps.data()); break;
+        case GATHER: exec_gather(n, o); break;
         case D2S: {
             const auto& is = g_.t[n.in[0]].shape;
             d2s_nhwc(bufs_[n.in[0]].data(), o, static_cast<int>(is[0]), static_cast<int>(is[1]), static_cast<int>(is[2]), static_cast<int>(is[3]), static_cast<int>(n.block));
@@ -955,17 +1824,23 @@ private:
             break;
         }
         case CONCAT: {
-            int axis = n.axis < 0 ? n.axis + 4 : n.axis;
-            if (axis != 1 || ot.shape.size() != 4) throw std::runtime_error("oracle: only channel CONCAT is on this path");
-            const std::size_t px = static_cast<std::size_t>(ot.shape[0] * ot.shape[2] * ot.shape[3]);
-            const std::size_t oc = static_cast<std::size_t>(ot.shape[1]);
-            std::size_t off = 0;
+            // execution_plan.cpp:606-620, 993-1002: 4-D inputs along any axis.
+            const int axis = n.axis < 0 ? n.axis + 4 : n.axis;
+            if (axis < 0 || axis >= 4) throw std::runtime_error("oracle: CONCAT axis out of range");
+            const auto od = dims4(ot.shape);
+            std::vector<const u16*> ins;
+            std::vector<std::array<int, 4>> dims;
+            int along = 0;
             for (auto id : n.in) {
-                const std::size_t ic = static_cast<std::size_t>(g_.t[id].shape[1]);
-                const u16* src = bufs_[id].data();
-                for (std::size_t p = 0; p < px; ++p) std::memcpy(o + p * oc + off, src + p * ic, ic * 2);
-                off += ic;
+                dims.push_back(dims4(g_.t[id].shape));
+                for (int d = 0; d < 4; ++d)
+                    if (d != axis && dims.back()[static_cast<std::size_t>(d)] != od[static_cast<std::size_t>(d)])
+                        throw std::runtime_error("oracle: CONCAT input shape mismatch");
+                along += dims.back()[static_cast<std::size_t>(axis)];
+                ins.push_back(bufs_[id].data());
             }
+            if (along != od[static_cast<std::size_t>(axis)]) throw std::runtime_error("oracle: CONCAT output shape mismatch");
+            concat_nhwc(ins, dims, o, od, axis);
             break;
         }
         default: throw std::runtime_error("oracle: unsupported operator during execution");
@@ -979,6 +1854,7 @@ private:
     std::vector<std::vector<u16>> bufs_;
     std::vector<int> state_in_, state_out_;
     std::map<std::uint32_t, std::size_t> in_pos_;
+    std::map<std::uint32_t, int> consumers_;
     std::vector<std::pair<std::uint32_t, std::uint32_t>> bindings_;
     std::vector<std::uint32_t> external_, ext_out_;
     std::vector<Step> steps_;
@@ -1261,6 +2137,67 @@ int oracle_model_to_yuv420(const uint16_t* x, int w, int h, int mw, int mh, int 
 int oracle_frame_padding(int w, int h, int mw, int mh, int* pad5)
 {
     return guard([&] { frame_padding(w, h, mw, mh, pad5); });
+}
+
+int oracle_unary(const uint16_t* in, uint16_t* out, size_t count, int op, float lo, float hi, int isa)
+{
+    return guard([&] { unary(in, out, count, op, lo, hi, isa); });
+}
+
+int oracle_binary(const uint16_t* a, const int64_t* a_shape, int a_rank, const uint16_t* b, const int64_t* b_shape, int b_rank,
+                  uint16_t* out, const int64_t* out_shape, int out_rank, int op)
+{
+    return guard([&] {
+        binary_dispatch(a, std::vector<std::int64_t>(a_shape, a_shape + a_rank), b, std::vector<std::int64_t>(b_shape, b_shape + b_rank),
+                        out, std::vector<std::int64_t>(out_shape, out_shape + out_rank), op);
+    });
+}
+
+int oracle_slice_nhwc(const uint16_t* in, uint16_t* out, const int* id4, const int* od4, const int* starts, const int* steps)
+{
+    return guard([&] { slice_nhwc(in, out, id4, od4, starts, steps); });
+}
+
+int oracle_concat_nhwc(const uint16_t* const* ins, const int* dims4, int n, uint16_t* out, const int* od4, int axis)
+{
+    return guard([&] {
+        std::vector<const u16*> v(ins, ins + n);
+        std::vector<std::array<int, 4>> d(static_cast<std::size_t>(n));
+        for (int i = 0; i < n; ++i)
+            for (int k = 0; k < 4; ++k) d[static_cast<std::size_t>(i)][static_cast<std::size_t>(k)] = dims4[4 * i + k];
+        concat_nhwc(v, d, out, {od4[0], od4[1], od4[2], od4[3]}, axis);
+    });
+}
+
+int oracle_gather(const uint16_t* data, const int64_t* shape, int rank, const int32_t* idx32, const int64_t* idx64, size_t count,
+                  int axis, uint16_t* out)
+{
+    return guard([&] { gather(data, std::vector<std::int64_t>(shape, shape + rank), idx32, idx64, count, axis, out); });
+}
+
+int oracle_reglu_nhwc(const uint16_t* in, uint16_t* out, size_t spatial, size_t gate_channels, float lo, float hi, int isa)
+{
+    return guard([&] { reglu(in, out, spatial, gate_channels, lo, hi, isa); });
+}
+
+int oracle_feature_update_nhwc(const uint16_t* in, const uint16_t* history, const uint16_t* scale, uint16_t* scaled_out,
+                               uint16_t* blended_out, uint16_t* feature_out, size_t spatial, size_t channels, int isa)
+{
+    return guard([&] { feature_update(in, history, scale, scaled_out, blended_out, feature_out, spatial, channels, isa); });
+}
+
+int oracle_y0_tail_nhwc(const uint16_t* latent, const uint16_t* prior, const uint16_t* quant_scale, const uint16_t* us0,
+                        const uint16_t* us1, uint16_t* normalized, uint16_t* clipped, uint16_t* y_raw, uint16_t* concat2,
+                        uint16_t* concat3, float clip_min, size_t spatial, size_t q, int isa)
+{
+    return guard([&] { y0_tail(latent, prior, quant_scale, us0, us1, normalized, clipped, y_raw, concat2, concat3, clip_min, spatial, q, isa); });
+}
+
+int oracle_y1_tail_nhwc(const uint16_t* normalized, const uint16_t* prior, const uint16_t* quant_scale, const uint16_t* us0,
+                        const uint16_t* us1, const uint16_t* concat2, const uint16_t* clipped, uint16_t* y_raw, uint16_t* out,
+                        size_t spatial, size_t q)
+{
+    return guard([&] { y1_tail(normalized, prior, quant_scale, us0, us1, concat2, clipped, y_raw, out, spatial, q); });
 }
 
 uint16_t oracle_float_to_half(float f) { return f2h(f); }

@@ -301,6 +301,154 @@ def ref_prepare_model_output(x: np.ndarray, w: int, h: int, pad: tuple, pixel_ra
     return out
 
 
+# ---- operators of the real-model graphs (NHWC buffers, raw FP16 bits)
+
+_i32p = C.POINTER(C.c_int32)
+_ip = C.POINTER(C.c_int)
+UNARY = {"clip": 0, "sigmoid": 1, "reciprocal": 2, "round": 3}
+BINARY = {"add": 0, "sub": 1, "mul": 2}
+_ops_bound = set()
+
+
+def _bind_ops(lib, prefix):
+    if prefix in _ops_bound:
+        return
+    f = lambda name: getattr(lib, prefix + name)  # noqa: E731
+    f("slice_nhwc").argtypes = [_u16p, _u16p, _ip, _ip, _ip, _ip]
+    f("concat_nhwc").argtypes = [C.POINTER(_u16p), _ip, C.c_int, _u16p, _ip, C.c_int]
+    f("reglu_nhwc").argtypes = [_u16p, _u16p, C.c_size_t, C.c_size_t, C.c_float, C.c_float, C.c_int]
+    f("feature_update_nhwc").argtypes = [_u16p] * 6 + [C.c_size_t, C.c_size_t, C.c_int]
+    f("y0_tail_nhwc").argtypes = [_u16p] * 10 + [C.c_float, C.c_size_t, C.c_size_t, C.c_int]
+    if prefix == "oracle_":
+        f("unary").argtypes = [_u16p, _u16p, C.c_size_t, C.c_int, C.c_float, C.c_float, C.c_int]
+        f("binary").argtypes = [_u16p, _i64p, C.c_int, _u16p, _i64p, C.c_int, _u16p, _i64p, C.c_int, C.c_int]
+        f("gather").argtypes = [_u16p, _i64p, C.c_int, _i32p, _i64p, C.c_size_t, C.c_int, _u16p]
+        f("y1_tail_nhwc").argtypes = [_u16p] * 9 + [C.c_size_t, C.c_size_t]
+    else:
+        f("unary").argtypes = [_u16p, _u16p, C.c_size_t, C.c_int, C.c_float, C.c_float, C.c_int, C.c_int]
+        f("binary_contiguous").argtypes = [_u16p, _u16p, _u16p, C.c_size_t, C.c_int, C.c_int]
+        f("binary_scalar").argtypes = [_u16p, C.c_uint16, _u16p, C.c_size_t, C.c_int, C.c_int, C.c_int]
+        f("binary_channel").argtypes = [_u16p, _u16p, _u16p, C.c_size_t, C.c_size_t, C.c_int, C.c_int, C.c_int]
+        f("gemm_reglu_nhwc").argtypes = [C.c_size_t, C.c_size_t, C.c_size_t, _u16p, _u16p, _u16p, C.c_float, C.c_float,
+                                         C.c_int, C.c_int]
+        f("y1_tail_nhwc").argtypes = [_u16p] * 9 + [C.c_size_t, C.c_size_t, C.c_int]
+    _ops_bound.add(prefix)
+
+
+class Ops:
+    """Kernel-level operators of the oracle ("oracle") or of the reference
+    kernels built from source ("ref"), on NHWC FP16 buffers."""
+
+    def __init__(self, which: str = "oracle"):
+        self.lib = oracle_lib() if which == "oracle" else ref_lib()
+        self.prefix = "oracle_" if which == "oracle" else "ref_"
+        _bind_ops(self.lib, self.prefix)
+
+    def _call(self, name, *args):
+        _check(self.lib, self.prefix, getattr(self.lib, self.prefix + name)(*args))
+
+    @staticmethod
+    def _u16(a):
+        return np.ascontiguousarray(a, np.uint16)
+
+    def unary(self, x, op, lo=0.0, hi=0.0, isa=0, threads=1):
+        x = self._u16(x)
+        out = np.zeros_like(x)
+        extra = (isa, threads) if self.prefix == "ref_" else (isa,)
+        self._call("unary", _p(x), _p(out), x.size, UNARY[op], lo, hi, *extra)
+        return out
+
+    def binary(self, a, a_shape, b, b_shape, out_shape, op):
+        """Oracle only: the reference plan's full ADD/SUB/MUL dispatch."""
+        a, b = self._u16(a), self._u16(b)
+        out = np.zeros(int(np.prod(out_shape)), np.uint16)
+        sa, sb, so = (np.asarray(s, np.int64) for s in (a_shape, b_shape, out_shape))
+        self._call("binary", _p(a), sa.ctypes.data_as(_i64p), len(sa), _p(b), sb.ctypes.data_as(_i64p), len(sb), _p(out),
+                   so.ctypes.data_as(_i64p), len(so), BINARY[op])
+        return out
+
+    def binary_contiguous(self, a, b, op, isa=0):
+        a, b = self._u16(a), self._u16(b)
+        out = np.zeros_like(a)
+        self._call("binary_contiguous", _p(a), _p(b), _p(out), a.size, BINARY[op], isa)
+        return out
+
+    def binary_scalar(self, vec, scalar, op, scalar_lhs, isa=0):
+        vec = self._u16(vec)
+        out = np.zeros_like(vec)
+        self._call("binary_scalar", _p(vec), int(scalar), _p(out), vec.size, BINARY[op], int(scalar_lhs), isa)
+        return out
+
+    def binary_channel(self, vec, chan, spatial, channels, op, chan_lhs, isa=0):
+        vec, chan = self._u16(vec), self._u16(chan)
+        out = np.zeros_like(vec)
+        self._call("binary_channel", _p(vec), _p(chan), _p(out), spatial, channels, BINARY[op], int(chan_lhs), isa)
+        return out
+
+    def slice(self, x, id4, od4, starts, steps):
+        x = self._u16(x)
+        out = np.zeros(int(np.prod(od4)), np.uint16)
+        arr = [(C.c_int * 4)(*v) for v in (id4, od4, starts, steps)]
+        self._call("slice_nhwc", _p(x), _p(out), *arr)
+        return out
+
+    def concat(self, xs, dims, od4, axis):
+        xs = [self._u16(x) for x in xs]
+        out = np.zeros(int(np.prod(od4)), np.uint16)
+        ptrs = (_u16p * len(xs))(*[_p(x) for x in xs])
+        flat = (C.c_int * (4 * len(dims)))(*[v for d in dims for v in d])
+        self._call("concat_nhwc", ptrs, flat, len(xs), _p(out), (C.c_int * 4)(*od4), axis)
+        return out
+
+    def gather(self, data, shape, idx, axis):
+        """Oracle only (the reference's gather lives in its plan)."""
+        data = self._u16(data)
+        shape = np.asarray(shape, np.int64)
+        idx = np.asarray(idx)
+        i32 = idx.astype(np.int32) if idx.dtype == np.int32 else None
+        i64 = None if i32 is not None else np.ascontiguousarray(idx, np.int64)
+        rank = len(shape)
+        ax = axis + rank if axis < 0 else axis
+        dim = int(shape[ax]) if 0 <= ax < rank else 1
+        out = np.zeros(int(np.prod(shape)) // dim * idx.size, np.uint16)
+        self._call("gather", _p(data), shape.ctypes.data_as(_i64p), rank,
+                   None if i32 is None else i32.ctypes.data_as(_i32p), None if i64 is None else i64.ctypes.data_as(_i64p),
+                   idx.size, axis, _p(out))
+        return out
+
+    def reglu(self, x, spatial, g, lo, hi, isa=0):
+        x = self._u16(x)
+        out = np.zeros(spatial * g, np.uint16)
+        self._call("reglu_nhwc", _p(x), _p(out), spatial, g, lo, hi, isa)
+        return out
+
+    def gemm_reglu(self, m, n, k, lhs, packed, lo, hi, isa=0, threads=2):
+        out = np.zeros(m * (n // 2), np.uint16)
+        self._call("gemm_reglu_nhwc", m, n, k, _p(self._u16(lhs)), _p(packed), _p(out), lo, hi, isa, threads)
+        return out
+
+    def feature_update(self, x, hist, scale, spatial, ch, outputs=False, isa=0):
+        x, hist, scale = self._u16(x), self._u16(hist), self._u16(scale)
+        feat = np.zeros(spatial * 2 * ch, np.uint16)
+        sc = np.zeros(spatial * ch, np.uint16) if outputs else None
+        bl = np.zeros(spatial * ch, np.uint16) if outputs else None
+        self._call("feature_update_nhwc", _p(x), _p(hist), _p(scale), _p(sc), _p(bl), _p(feat), spatial, ch, isa)
+        return (feat, sc, bl) if outputs else feat
+
+    def y0_tail(self, latent, prior, qs, us0, us1, clip_min, spatial, q, isa=0):
+        ins = [self._u16(a) for a in (latent, prior, qs, us0, us1)]
+        outs = [np.zeros(spatial * c, np.uint16) for c in (2 * q, 2 * q, q, 2 * q, 6 * q)]
+        self._call("y0_tail_nhwc", *[_p(a) for a in ins], *[_p(a) for a in outs], clip_min, spatial, q, isa)
+        return outs  # normalized, clipped, y_raw, concat2, concat3
+
+    def y1_tail(self, normalized, prior, qs, us0, us1, concat2, clipped, spatial, q, isa=0):
+        ins = [self._u16(a) for a in (normalized, prior, qs, us0, us1, concat2, clipped)]
+        outs = [np.zeros(spatial * q, np.uint16), np.zeros(spatial * 2 * q, np.uint16)]
+        extra = (isa,) if self.prefix == "ref_" else ()
+        self._call("y1_tail_nhwc", *[_p(a) for a in ins], *[_p(a) for a in outs], spatial, q, *extra)
+        return outs  # y_raw, out
+
+
 def parity_stats(got: np.ndarray, want: np.ndarray) -> dict:
     """max|d|/RMS(want) and mean|d|/RMS(want) over FP16 tensors (raw bits)."""
     g = got.view(np.float16).astype(np.float64)

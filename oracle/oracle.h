@@ -72,6 +72,28 @@ int oracle_yuv420_to_model(const uint8_t* yuv, int w, int h, int mw, int mh, int
 int oracle_model_to_yuv420(const uint16_t* x, int w, int h, int mw, int mh, int pad_left, int pad_top, int rotated,
                            float pixel_range, uint8_t* yuv);
 int oracle_frame_padding(int w, int h, int mw, int mh, int* pad5);
+/* Operators of the real-model graphs (NHWC buffers as in the reference).
+ * unary op: 0 clip [lo, hi], 1 sigmoid, 2 reciprocal, 3 round.
+ * binary op: 0 add, 1 sub, 2 mul; the full dispatch of the reference plan
+ * (same shape, scalar, channel and general broadcast). */
+int oracle_unary(const uint16_t* in, uint16_t* out, size_t count, int op, float lo, float hi, int isa);
+int oracle_binary(const uint16_t* a, const int64_t* a_shape, int a_rank, const uint16_t* b, const int64_t* b_shape, int b_rank,
+                  uint16_t* out, const int64_t* out_shape, int out_rank, int op);
+int oracle_slice_nhwc(const uint16_t* in, uint16_t* out, const int* id4, const int* od4, const int* starts, const int* steps);
+/* dims4: n rows of logical NCHW dims. */
+int oracle_concat_nhwc(const uint16_t* const* ins, const int* dims4, int n, uint16_t* out, const int* od4, int axis);
+int oracle_gather(const uint16_t* data, const int64_t* shape, int rank, const int32_t* idx32, const int64_t* idx64, size_t count,
+                  int axis, uint16_t* out);
+int oracle_reglu_nhwc(const uint16_t* in, uint16_t* out, size_t spatial, size_t gate_channels, float lo, float hi, int isa);
+/* scaled_out / blended_out may be NULL (the one-output form). */
+int oracle_feature_update_nhwc(const uint16_t* in, const uint16_t* history, const uint16_t* scale, uint16_t* scaled_out,
+                               uint16_t* blended_out, uint16_t* feature_out, size_t spatial, size_t channels, int isa);
+int oracle_y0_tail_nhwc(const uint16_t* latent, const uint16_t* prior, const uint16_t* quant_scale, const uint16_t* us0,
+                        const uint16_t* us1, uint16_t* normalized, uint16_t* clipped, uint16_t* y_raw, uint16_t* concat2,
+                        uint16_t* concat3, float clip_min, size_t spatial, size_t q, int isa);
+int oracle_y1_tail_nhwc(const uint16_t* normalized, const uint16_t* prior, const uint16_t* quant_scale, const uint16_t* us0,
+                        const uint16_t* us1, const uint16_t* concat2, const uint16_t* clipped, uint16_t* y_raw, uint16_t* out,
+                        size_t spatial, size_t q);
 uint16_t oracle_float_to_half(float f);
 float oracle_half_to_float(uint16_t h);
 

@@ -22,6 +22,7 @@
 #include <mutex>
 #include <stdexcept>
 #include <string>
+#include <vector>
 
 using namespace mlvc;
 using namespace mlvc::cpu_backend;
@@ -198,6 +199,102 @@ int ref_prepare_model_output(const std::uint16_t* x, int w, int h, int mw, int m
                                           std::span<std::uint8_t>(yuv + ysz + uvsz, uvsz));
         FramePadding pad{pad5[0], pad5[1], pad5[2], pad5[3], pad5[4] != 0};
         prepare_model_output_into(t, view, pixel_range, pad);
+    });
+}
+
+// Operators of the real-model graphs: the KernelSet entries and the slice /
+// concat helpers of kernels_scalar.cpp, on NHWC buffers. unary op: 0 clip,
+// 1 sigmoid, 2 reciprocal, 3 round; binary op: 0 add, 1 sub, 2 mul.
+int ref_unary(const std::uint16_t* in, std::uint16_t* out, std::size_t count, int op, float lo, float hi, int isa, int threads)
+{
+    static constexpr UnaryKind kinds[4] = {UnaryKind::kClip, UnaryKind::kSigmoid, UnaryKind::kReciprocal, UnaryKind::kRound};
+    return guard([&] { kernels(isa).unary(in, out, count, kinds[op & 3], 0.0F, lo, hi, pool(threads)); });
+}
+
+BinaryKind binary_kind(int op) { return op == 1 ? BinaryKind::kSub : op == 2 ? BinaryKind::kMul : BinaryKind::kAdd; }
+
+int ref_binary_contiguous(const std::uint16_t* a, const std::uint16_t* b, std::uint16_t* out, std::size_t count, int op, int isa)
+{
+    return guard([&] { kernels(isa).binary_contiguous(a, b, out, count, binary_kind(op), pool(1)); });
+}
+
+int ref_binary_scalar(const std::uint16_t* vec, std::uint16_t scalar, std::uint16_t* out, std::size_t count, int op, int scalar_lhs,
+                      int isa)
+{
+    return guard([&] { kernels(isa).binary_scalar_bcast(vec, scalar, out, count, binary_kind(op), scalar_lhs != 0, pool(1)); });
+}
+
+int ref_binary_channel(const std::uint16_t* vec, const std::uint16_t* chan, std::uint16_t* out, std::size_t spatial,
+                       std::size_t channels, int op, int chan_lhs, int isa)
+{
+    return guard([&] {
+        kernels(isa).binary_channel_bcast(vec, chan, out, spatial, channels, binary_kind(op), chan_lhs != 0, pool(1));
+    });
+}
+
+int ref_slice_nhwc(const std::uint16_t* in, std::uint16_t* out, const int* id4, const int* od4, const int* starts,
+                   const int* steps)
+{
+    return guard([&] { execute_slice_nhwc(in, out, id4, od4, starts, steps, pool(1)); });
+}
+
+int ref_concat_nhwc(const std::uint16_t* const* ins, const int* dims4, int n, std::uint16_t* out, const int* od4, int axis)
+{
+    return guard([&] {
+        std::vector<const int*> dims(static_cast<std::size_t>(n));
+        for (int i = 0; i < n; ++i) dims[static_cast<std::size_t>(i)] = dims4 + 4 * i;
+        execute_concat_nhwc(ins, dims.data(), static_cast<std::size_t>(n), out, od4, axis, pool(1));
+    });
+}
+
+int ref_reglu_nhwc(const std::uint16_t* in, std::uint16_t* out, std::size_t spatial, std::size_t g, float lo, float hi, int isa)
+{
+    return guard([&] { kernels(isa).reglu_nhwc(in, out, spatial, g, lo, hi, pool(1)); });
+}
+
+// 1x1 conv with the ReGLU epilogue (GemmEpilogueKind::kReglu), as the plan
+// runs a matched CONV -> SLICE -> SLICE -> CLIP -> MUL chain.
+int ref_gemm_reglu_nhwc(std::size_t m, std::size_t n, std::size_t k, const std::uint16_t* lhs, const std::uint16_t* packed,
+                        std::uint16_t* dst, float lo, float hi, int isa, int threads)
+{
+    return guard([&] {
+        GemmEpilogue e;
+        e.kind = GemmEpilogueKind::kReglu;
+        e.clamp_min = lo;
+        e.clamp_max = hi;
+        execute_gemm_nhwc(kernels(isa), m, n, k, lhs, packed, dst, e, pool(threads));
+    });
+}
+
+int ref_feature_update_nhwc(const std::uint16_t* in, const std::uint16_t* history, const std::uint16_t* scale,
+                            std::uint16_t* scaled_out, std::uint16_t* blended_out, std::uint16_t* feature_out,
+                            std::size_t spatial, std::size_t channels, int isa)
+{
+    return guard([&] {
+        if (scaled_out)
+            kernels(isa).feature_update_outputs_nhwc(in, history, scale, scaled_out, blended_out, feature_out, spatial, channels,
+                                                     pool(1));
+        else
+            kernels(isa).feature_update_nhwc(in, history, scale, feature_out, spatial, channels, pool(1));
+    });
+}
+
+int ref_y0_tail_nhwc(const std::uint16_t* latent, const std::uint16_t* prior, const std::uint16_t* qs, const std::uint16_t* us0,
+                     const std::uint16_t* us1, std::uint16_t* normalized, std::uint16_t* clipped, std::uint16_t* y_raw,
+                     std::uint16_t* concat2, std::uint16_t* concat3, float clip_min, std::size_t spatial, std::size_t q, int isa)
+{
+    return guard([&] {
+        kernels(isa).y0_tail_nhwc(latent, prior, qs, us0, us1, normalized, clipped, y_raw, concat2, concat3, clip_min, spatial, q,
+                                  pool(1));
+    });
+}
+
+int ref_y1_tail_nhwc(const std::uint16_t* normalized, const std::uint16_t* prior, const std::uint16_t* qs, const std::uint16_t* us0,
+                     const std::uint16_t* us1, const std::uint16_t* concat2, const std::uint16_t* clipped, std::uint16_t* y_raw,
+                     std::uint16_t* out, std::size_t spatial, std::size_t q, int isa)
+{
+    return guard([&] {
+        kernels(isa).y1_tail_nhwc(normalized, prior, qs, us0, us1, concat2, clipped, y_raw, out, spatial, q, pool(1));
     });
 }
 
