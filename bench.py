@@ -13,8 +13,9 @@ fraction of the 2.5 PFLOP/s dense FP16 MFMA peak, the roofline position of
 the dominant kernel (timed live with HIP events on the backend stream) and
 the CPU oracle's frames/s on a bounded sample of the same workload, and the
 codec I/O measurements around the encoder / decoder graphs (conversion
-kernels at 1080p, buffered end-to-end frames/s). A per-kernel table goes to
-stderr.
+kernels at 1080p, buffered end-to-end frames/s) and the real-model operator
+kernels (fused ReGLU, feature update, quantisation tails, GATHER, ...)
+against the HBM roofline. A per-kernel table goes to stderr.
 """
 
 from __future__ import annotations
@@ -190,6 +191,47 @@ def codec_buffered(frames: int) -> dict:
     return res
 
 
+REALOPS = "realops_544x960"
+REALOPS_KINDS = ("y0_tail", "y1_tail", "feature_update", "feature_update_outputs", "reglu", "gather", "slice", "concat",
+                 "clip", "sigmoid", "reciprocal", "round", "add", "sub", "mul")
+
+
+def realops(reps: int, frames: int) -> dict:
+    """The real-model operators at the recurrent feature's resolution
+    (realops_544x960: ReGLU FFN, q-index GATHER scaling, feature update with
+    the 64-channel state at 544x960, standalone ReGLU, deferred-CONCAT
+    feature update, y0/y1 quantisation tails with Q=96 at 272x480): frames/s
+    of the whole graph (hipGraph replay, inputs resident) and each
+    non-conv kernel's algorithmic bytes against the HBM roofline."""
+    import numpy as np
+
+    import mlvc_hip
+
+    with tempfile.TemporaryDirectory() as d:
+        mlvc_hip.synth_write(REALOPS, d, 0)
+        bindings, _ = mlvc_hip.synth_bindings(REALOPS)
+        gpu = mlvc_hip.Backend(d, "hip", device_id=0)
+        gpu.load(REALOPS, bindings)
+        x = mlvc_hip.synth_input(REALOPS, 0, 0, gpu.in_shapes[0])
+        gpu.upload_inputs([x, np.array([5], np.int32)])
+        gpu.reset_state()
+        gpu.time_frames(10)
+        ms = gpu.time_frames(frames)
+        kernels = []
+        for r in kernel_table(gpu, reps):
+            if r["kind"] not in REALOPS_KINDS:
+                continue
+            kernels.append({"launch": r["name"], "kind": r["kind"], "us": r["ms"] * 1e3, "algorithmic_bytes": r["bytes"],
+                            "gbs": r["gbs"], "hbm_frac": r["gbs"] / PEAK_HBM_GBS})
+        n_launch = len(gpu.launches())
+        gpu.close()
+    for k in kernels:
+        log(f"realops {k['kind']:24} {k['launch'][:24]:24} {k['us']:8.1f} us {k['gbs']:7.0f} GB/s {k['hbm_frac']:.3f}")
+    return {"workload": f"{REALOPS}: ReGLU FFN, q-index GATHER, feature update (C=64 at 544x960, both forms), "
+                        f"y0/y1 quantisation tails (Q=96 at 272x480) around 1x1/3x3 convs",
+            "frames_per_s": frames / (ms * 1e-3), "kernels_per_frame": n_launch, "kernels": kernels}
+
+
 def cpu_baseline(model_dir, bindings, shape, budget_s: float):
     import mlvc_hip
     import mlvc_oracle
@@ -282,6 +324,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-codec", action="store_true", help="skip the codec I/O measurements")
     ap.add_argument("--codec-frames", type=int, default=60)
+    ap.add_argument("--no-realops", action="store_true", help="skip the real-model operator measurements")
+    ap.add_argument("--realops-frames", type=int, default=50)
     ap.add_argument("--api-frames", type=int, default=30,
                     help="frames timed through run() (host frame in, host reconstruction out)")
     ap.add_argument("--pmc-pass", default=None, metavar="I,J,...",
@@ -296,6 +340,12 @@ def main() -> int:
               f"--gpus {args.gpus} is not supported", file=sys.stderr)
         return 2
     rank = int(os.environ.get("RANK", "0"))
+    # Conv tile choices recorded on an MI355X (written by the backend's tuner
+    # under MLVC_HIP_TUNE_FILE): the benchmark, its kernel trace and its
+    # counter passes then run the same kernels.
+    tuning = REPO / "mlvc.cpp_amd" / "tuning" / "mi355x.txt"
+    if tuning.exists():
+        os.environ.setdefault("MLVC_HIP_TUNE_FILE", str(tuning))
 
     import mlvc_hip
 
@@ -361,6 +411,11 @@ def main() -> int:
             f"model->frame {codec['model_to_frame_us']:.1f} us ({codec['model_to_frame_gbs']:.0f} GB/s); buffered "
             f"encoder {codec['encoder_frames_per_s']:.0f} frames/s, decoder {codec['decoder_frames_per_s']:.0f} frames/s")
 
+    ops = None
+    if not args.no_realops:
+        ops = realops(args.kernel_reps, args.realops_frames)
+        log(f"realops: {ops['frames_per_s']:.0f} frames/s, {ops['kernels_per_frame']} kernels/frame")
+
     conv_tflops = conv_flops * fps / 1e12
     line = {
         "metric": "conv-graph frames/s @1920x1088 + FP16 conv TFLOP/s (% MFMA peak), 1 GPU",
@@ -387,6 +442,7 @@ def main() -> int:
         "roofline": roof,
         "cpu_baseline": base,
         "codec_io": codec,
+        "realops": ops,
     }
     if rank == 0:
         print(json.dumps(line), flush=True)

@@ -29,6 +29,7 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <fstream>
 #include <map>
 #include <set>
 #include <stdexcept>
@@ -1884,6 +1885,17 @@ private:
         for (auto& b : bindings_)
             for (auto& buf : b.buf) hip_check(mlvc_hip_zero(buf.ptr, b.bytes, stream_), "state clear");
         constexpr int kWarm = 2, kReps = 5;
+        // MLVC_HIP_TUNE_FILE=<path>: choices listed there ("<model>:<launch>
+        // <variant>" per line) are taken without timing, and every choice is
+        // written back, so separate processes (one counter pass each, or a
+        // benchmark and its profile) run the same kernels.
+        const char* tune_file = std::getenv("MLVC_HIP_TUNE_FILE");
+        std::map<std::string, std::string> chosen;
+        if (tune_file) {
+            std::ifstream in(tune_file);
+            std::string launch, variant;
+            while (in >> launch >> variant) chosen[launch] = variant;
+        }
         for (auto& lp : launches_) {
             Launch& L = *lp;
             if (L.kind != Launch::kConv || L.forced) continue;
@@ -1895,6 +1907,15 @@ private:
             const mlvc_hip_conv_desc planned = L.conv;
             int best = planned.variant;
             float best_ms = -1.0F;
+            const std::string key = model_ + ":" + L.name;
+            if (const auto it = chosen.find(key); it != chosen.end()) {
+                for (int v : cand)
+                    if (it->second == mlvc_hip_conv_variant_name(v)) {
+                        best = v;
+                        best_ms = 0.0F;
+                    }
+                if (best_ms == 0.0F) cand.clear();
+            }
             for (int v : cand) {
                 mlvc_hip_conv_desc d = planned;
                 d.variant = v;
@@ -1926,8 +1947,13 @@ private:
                 const std::string old_name = mlvc_hip_conv_variant_name(planned.variant);
                 L.kind_name = mlvc_hip_conv_variant_name(best) + L.kind_name.substr(old_name.size());
             }
+            chosen[key] = mlvc_hip_conv_variant_name(best);
         }
         hip_check(mlvc_hip_stream_synchronize(stream_), "stream sync");
+        if (tune_file) {
+            std::ofstream out(tune_file, std::ios::trunc);
+            for (const auto& [launch, variant] : chosen) out << launch << ' ' << variant << '\n';
+        }
     }
 
     static bool tuning_enabled()

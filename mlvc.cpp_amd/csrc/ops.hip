@@ -172,10 +172,60 @@ __global__ __launch_bounds__(kBlock) void binary_bcast_kernel(const u16* __restr
     }
 }
 
+// Vector form for rows whose W stride is 1 or 0 for both operands (full rows
+// or a value broadcast along W) with W a multiple of 8: 16-byte loads of the
+// full operands, one load of a broadcast value, 16-byte stores.
+template <int OP, bool AV, bool BV>
+__global__ __launch_bounds__(kBlock) void binary_rows_kernel(const u16* __restrict__ a, const u16* __restrict__ b,
+                                                             u16* __restrict__ y, Dims4 g)
+{
+    const long long w8 = g.d[3] / 8, rows = g.d[0] * g.d[1] * g.d[2];
+    for (long long i = blockIdx.x * static_cast<long long>(kBlock) + threadIdx.x; i < rows * w8;
+         i += static_cast<long long>(gridDim.x) * kBlock) {
+        const long long row = i / w8, w0 = (i % w8) * 8;
+        const long long h = row % g.d[2], c = (row / g.d[2]) % g.d[1], n = row / (g.d[2] * g.d[1]);
+        const u16* pa = a + n * g.sa[0] + c * g.sa[1] + h * g.sa[2];
+        const u16* pb = b + n * g.sb[0] + c * g.sb[1] + h * g.sb[2];
+        u16 va[8], vb[8];
+        if (AV) {
+            ld8<true>(pa + w0, 8, va);
+        } else {
+            const u16 s = *pa;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) va[j] = s;
+        }
+        if (BV) {
+            ld8<true>(pb + w0, 8, vb);
+        } else {
+            const u16 s = *pb;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) vb[j] = s;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) va[j] = binary_op<OP>(va[j], vb[j]);
+        st8<true>(y + row * g.d[3] + w0, 8, va);
+    }
+}
+
 // ------------------------------------------------------------------ slice
 struct SliceArgs {
     long long id[4], od[4], st[4], sp[4];
 };
+
+// Unit W step, W start / extents multiples of 8: whole 16-byte groups.
+__global__ __launch_bounds__(kBlock) void slice_rows_kernel(const u16* __restrict__ x, u16* __restrict__ y, SliceArgs s)
+{
+    const long long w8 = s.od[3] / 8, rows = s.od[0] * s.od[1] * s.od[2];
+    for (long long i = blockIdx.x * static_cast<long long>(kBlock) + threadIdx.x; i < rows * w8;
+         i += static_cast<long long>(gridDim.x) * kBlock) {
+        const long long row = i / w8, w0 = (i % w8) * 8;
+        const long long h = row % s.od[2], c = (row / s.od[2]) % s.od[1], n = row / (s.od[2] * s.od[1]);
+        const long long in_row = ((s.st[0] + n * s.sp[0]) * s.id[1] + s.st[1] + c * s.sp[1]) * s.id[2] + s.st[2] + h * s.sp[2];
+        u16 v[8];
+        ld8<true>(x + in_row * s.id[3] + s.st[3] + w0, 8, v);
+        st8<true>(y + row * s.od[3] + w0, 8, v);
+    }
+}
 
 __global__ __launch_bounds__(kBlock) void slice_kernel(const u16* __restrict__ x, u16* __restrict__ y, SliceArgs s)
 {
@@ -317,10 +367,13 @@ __global__ __launch_bounds__(kBlock) void y0_tail_kernel(mlvc_hip_y0_tail_desc d
         const size_t p0 = (t % p8) * 8, qc = (t / p8) % q, b = t / p8 / q;
         const int cnt = static_cast<int>(std::min<size_t>(8, hw - p0));
         float sv[2][8], tl[2][8];
+        u16 pv[4][8];  // prior planes qc, qc+Q (head) and 2Q+qc, 3Q+qc (tail)
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
             const size_t cc = qc + h * q;
-            u16 vh[8], vt[8], vl[8], vq[8], cl[8], nr[8];
+            u16 (&vh)[8] = pv[h];
+            u16 (&vt)[8] = pv[2 + h];
+            u16 vl[8], vq[8], cl[8], nr[8];
             ld8<VEC>(prior + (b * 4 * q + cc) * hw + p0, cnt, vh);
             ld8<VEC>(prior + (b * 4 * q + 2 * q + cc) * hw + p0, cnt, vt);
             ld8<VEC>(latent + (b * 2 * q + cc) * hw + p0, cnt, vl);
@@ -352,11 +405,7 @@ __global__ __launch_bounds__(kBlock) void y0_tail_kernel(mlvc_hip_y0_tail_desc d
             st8<VEC>(concat3 + (b * 6 * q + cc) * hw + p0, cnt, up);
         }
 #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            u16 v[8];
-            ld8<VEC>(prior + (b * 4 * q + qc + k * q) * hw + p0, cnt, v);
-            st8<VEC>(concat3 + (b * 6 * q + 2 * q + qc + k * q) * hw + p0, cnt, v);
-        }
+        for (int k = 0; k < 4; ++k) st8<VEC>(concat3 + (b * 6 * q + 2 * q + qc + k * q) * hw + p0, cnt, pv[k]);
     }
 }
 
@@ -481,6 +530,21 @@ int mlvc_hip_binary(const void* a, const int64_t* a_dims, const void* b, const i
             return;
         }
         const size_t work = static_cast<size_t>(g.d[0] * g.d[1] * g.d[2] * ((g.d[3] + 7) / 8));
+        if (g.d[3] % 8 == 0 && g.sa[3] <= 1 && g.sb[3] <= 1 && aligned16(a) && aligned16(b) && aligned16(y)) {
+            // Full operands have W stride 1 and row offsets that are multiples
+            // of W, so every 8-group is 16-byte aligned.
+            const int av = g.sa[3] == 1, bv = g.sb[3] == 1;
+            const int key = op * 4 + av * 2 + bv;
+#define MLVC_ROWS(O, A, B) \
+    case O * 4 + A * 2 + B: launch(binary_rows_kernel<O, A, B>, work, st, pa, pb, py, g); return;
+            switch (key) {
+                MLVC_ROWS(0, 0, 0) MLVC_ROWS(0, 0, 1) MLVC_ROWS(0, 1, 0) MLVC_ROWS(0, 1, 1)
+                MLVC_ROWS(1, 0, 0) MLVC_ROWS(1, 0, 1) MLVC_ROWS(1, 1, 0) MLVC_ROWS(1, 1, 1)
+                MLVC_ROWS(2, 0, 0) MLVC_ROWS(2, 0, 1) MLVC_ROWS(2, 1, 0) MLVC_ROWS(2, 1, 1)
+            default: break;
+            }
+#undef MLVC_ROWS
+        }
         if (op == MLVC_BINARY_ADD) launch(binary_bcast_kernel<MLVC_BINARY_ADD>, work, st, pa, pb, py, g);
         if (op == MLVC_BINARY_SUB) launch(binary_bcast_kernel<MLVC_BINARY_SUB>, work, st, pa, pb, py, g);
         if (op == MLVC_BINARY_MUL) launch(binary_bcast_kernel<MLVC_BINARY_MUL>, work, st, pa, pb, py, g);
@@ -503,7 +567,9 @@ int mlvc_hip_slice(const void* x, const int64_t* x_dims, void* y, const int64_t*
             a.sp[k] = steps[k];
         }
         const size_t work = static_cast<size_t>(a.od[0] * a.od[1] * a.od[2] * ((a.od[3] + 7) / 8));
-        launch(slice_kernel, work, to_stream(s), static_cast<const u16*>(x), static_cast<u16*>(y), a);
+        const bool rows = a.sp[3] == 1 && a.st[3] % 8 == 0 && a.id[3] % 8 == 0 && a.od[3] % 8 == 0 && aligned16(x) && aligned16(y);
+        if (rows) launch(slice_rows_kernel, work, to_stream(s), static_cast<const u16*>(x), static_cast<u16*>(y), a);
+        else launch(slice_kernel, work, to_stream(s), static_cast<const u16*>(x), static_cast<u16*>(y), a);
     });
 }
 

@@ -106,7 +106,10 @@ def test_unary_every_half(dev, case):
 NP_OP = {"add": np.add, "sub": np.subtract, "mul": np.multiply}
 BCAST = [([1, 24, 12, 20], [1, 24, 12, 20]), ([1, 24, 12, 20], [1, 1, 1, 1]), ([1, 1, 1, 1], [1, 24, 12, 20]),
          ([1, 24, 12, 20], [1, 24, 1, 1]), ([1, 24, 1, 1], [1, 24, 12, 20]), ([2, 8, 5, 6], [1, 1, 5, 6]),
-         ([1, 8, 1, 6], [3, 8, 5, 1]), ([2, 8, 5, 7], [2, 1, 1, 1]), ([1, 1, 1, 7], [4, 3, 2, 7])]
+         ([1, 8, 1, 6], [3, 8, 5, 1]), ([2, 8, 5, 7], [2, 1, 1, 1]), ([1, 1, 1, 7], [4, 3, 2, 7]),
+         # W a multiple of 8: the 16-byte row path (full / broadcast operands).
+         ([1, 24, 12, 24], [1, 24, 1, 1]), ([1, 1, 1, 1], [1, 8, 3, 16]), ([2, 8, 5, 16], [1, 1, 5, 16]),
+         ([1, 8, 1, 16], [3, 8, 5, 1]), ([2, 8, 5, 16], [2, 8, 5, 16])]
 
 
 @pytest.mark.parametrize("op", ["add", "sub", "mul"])
@@ -134,7 +137,8 @@ SLICES = [([1, 12, 6, 10], [1, 4, 6, 10], [0, 4, 0, 0], [1, 1, 1, 1]),
           ([1, 12, 6, 10], [1, 12, 3, 10], [0, 0, 2, 0], [1, 1, 1, 1]),
           ([2, 12, 6, 10], [2, 5, 3, 4], [0, 1, 1, 3], [1, 2, 2, 1]),
           ([2, 6, 8, 9], [1, 6, 4, 3], [1, 0, 7, 8], [1, 1, -2, -3]),
-          ([1, 32, 16, 24], [1, 16, 16, 24], [0, 16, 0, 0], [1, 1, 1, 1])]
+          ([1, 32, 16, 24], [1, 16, 16, 24], [0, 16, 0, 0], [1, 1, 1, 1]),
+          ([2, 4, 6, 32], [1, 4, 3, 16], [1, 0, 1, 8], [1, 1, 2, 1])]
 
 
 @pytest.mark.parametrize("case", SLICES, ids=[str(i) for i in range(len(SLICES))])
