@@ -6,7 +6,11 @@
 #include "mlvc/runtime/graph_builder.hpp"
 #include "mlvc_hip_backend.h"
 
+#include "mlvc/core/model.hpp"
+
 #include <cstring>
+#include <optional>
+#include <cstdio>
 #include <filesystem>
 #include <stdexcept>
 #include <string>
@@ -322,6 +326,55 @@ int mlvc_aot_inspect(const char* model_dir, const char* model_name, int* nodes, 
         *arena_bytes = g.descriptor.arena_bytes;
         *weights_bytes = g.descriptor.weights_bytes;
     });
+}
+
+int mlvc_model_config_json(const char* model_dir, char* buf, size_t len)
+{
+    return guard([&] {
+        const mlvc::ModelConfig c = mlvc::load_model_config(std::filesystem::path(model_dir));
+        auto list = [](const std::vector<int>& v) {
+            std::string s = "[";
+            for (std::size_t i = 0; i < v.size(); ++i) s += (i ? "," : "") + std::to_string(v[i]);
+            return s + "]";
+        };
+        auto opt = [](const std::optional<int>& v) { return v ? std::to_string(*v) : std::string("null"); };
+        char range[64];
+        std::snprintf(range, sizeof(range), "%.9g", static_cast<double>(c.pixel_range));
+        std::string j = "{";
+        j += "\"name\":\"" + c.name + "\",\"model_version\":\"" + c.model_version + "\"";
+        j += ",\"model_width\":" + std::to_string(c.model_width) + ",\"model_height\":" + std::to_string(c.model_height);
+        j += ",\"pixel_range\":" + std::string(range);
+        j += ",\"qp_num\":" + std::to_string(c.qp_num) + ",\"total_qp_num\":" + std::to_string(c.total_qp_num);
+        j += ",\"frame_index_map\":" + list(c.frame_index_map) + ",\"qp_shift\":" + list(c.qp_shift);
+        j += ",\"feature_channels\":" + std::to_string(c.feature_channels) + ",\"latent_channels\":" +
+             std::to_string(c.latent_channels) + ",\"hyperprior_channels\":" + std::to_string(c.hyperprior_channels);
+        j += ",\"downsample_feature\":" + std::to_string(c.downsample_feature) + ",\"downsample_latent\":" +
+             std::to_string(c.downsample_latent) + ",\"downsample_hyperprior\":" + std::to_string(c.downsample_hyperprior);
+        j += ",\"y_scale_repeat\":" + std::to_string(c.y_scale_repeat) + ",\"iframe_period\":" + opt(c.iframe_period) +
+             ",\"reset_period\":" + opt(c.reset_period) + ",\"disable_feature_reset\":" +
+             (c.disable_feature_reset ? "true" : "false");
+        j += ",\"feature_hw\":[" + std::to_string(c.feature_height()) + "," + std::to_string(c.feature_width()) + "]";
+        j += ",\"latent_hw\":[" + std::to_string(c.latent_height()) + "," + std::to_string(c.latent_width()) + "]";
+        j += ",\"hyperprior_hw\":[" + std::to_string(c.hyperprior_height()) + "," + std::to_string(c.hyperprior_width()) + "]";
+        j += "}";
+        if (j.size() + 1 > len) throw std::runtime_error("buffer too small for the model configuration");
+        copy_str(j, buf, len);
+    });
+}
+
+int mlvc_model_q_index_shift(const char* model_dir, int frame, int* shift)
+{
+    return guard([&] { *shift = mlvc::load_model_config(std::filesystem::path(model_dir)).q_index_shift(frame); });
+}
+
+int mlvc_model_frame_in_gop(const char* model_dir, int frame, int* gop_frame)
+{
+    return guard([&] { *gop_frame = mlvc::load_model_config(std::filesystem::path(model_dir)).frame_in_gop(frame); });
+}
+
+int mlvc_model_verify_bundle(const char* model_dir)
+{
+    return guard([&] { mlvc::verify_model_bundle(*mlvc::make_model_asset_reader(std::filesystem::path(model_dir))); });
 }
 
 int mlvc_synth_configs(char* buf, size_t len)

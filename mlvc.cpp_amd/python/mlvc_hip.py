@@ -12,6 +12,7 @@ nothing here falls back to another implementation.
 from __future__ import annotations
 
 import ctypes as C
+import json
 import pathlib
 
 import numpy as np
@@ -82,6 +83,10 @@ def backend_lib() -> C.CDLL:
         lib.mlvc_synth_bindings.argtypes = [C.c_char_p, _i64p, C.c_int, C.POINTER(C.c_int), C.POINTER(C.c_int)]
         lib.mlvc_aot_inspect.argtypes = [C.c_char_p, C.c_char_p, C.POINTER(C.c_int), C.POINTER(C.c_int),
                                          C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]
+        lib.mlvc_model_config_json.argtypes = [C.c_char_p, C.c_char_p, C.c_size_t]
+        lib.mlvc_model_q_index_shift.argtypes = [C.c_char_p, C.c_int, C.POINTER(C.c_int)]
+        lib.mlvc_model_frame_in_gop.argtypes = [C.c_char_p, C.c_int, C.POINTER(C.c_int)]
+        lib.mlvc_model_verify_bundle.argtypes = [C.c_char_p]
         _lib = lib
     return _lib
 
@@ -349,3 +354,30 @@ def aot_inspect(model_dir, model_name: str) -> dict:
                                           C.byref(tensors), C.byref(arena), C.byref(weights)))
     return {"nodes": nodes.value, "tensors": tensors.value, "arena_bytes": arena.value,
             "weights_bytes": weights.value}
+
+
+def model_config(model_dir) -> dict:
+    """ModelConfig of a model directory: metadata.pb checked against model_bundle.pb and validated
+    (reference core/src/model.cpp:150-183), plus the derived feature/latent/hyperprior sizes."""
+    buf = C.create_string_buffer(8192)
+    _check(backend_lib().mlvc_model_config_json(str(model_dir).encode(), buf, len(buf)))
+    return json.loads(buf.value.decode())
+
+
+def q_index_shift(model_dir, frame: int) -> int:
+    """ModelConfig::q_index_shift (reference core/src/model.cpp:136-147)."""
+    out = C.c_int()
+    _check(backend_lib().mlvc_model_q_index_shift(str(model_dir).encode(), frame, C.byref(out)))
+    return out.value
+
+
+def frame_in_gop(model_dir, frame: int) -> int:
+    """ModelConfig::frame_in_gop (reference core/src/model.cpp:128-135)."""
+    out = C.c_int()
+    _check(backend_lib().mlvc_model_frame_in_gop(str(model_dir).encode(), frame, C.byref(out)))
+    return out.value
+
+
+def verify_bundle(model_dir) -> None:
+    """Checks every artifact listed in model_bundle.pb for presence, size and SHA-256."""
+    _check(backend_lib().mlvc_model_verify_bundle(str(model_dir).encode()))

@@ -2,15 +2,19 @@
 // Read-only sources of model files (graph.pb, weights.bin, metadata.pb).
 //
 // Same interface as the reference's core/include/mlvc/core/assets.hpp:16-37
-// (ModelAssetReader with location_label/exists/read_binary); this build
-// provides a directory reader and an in-memory reader. Embedded bundles are
-// outside the inference path.
+// (ModelAssetReader with location_label/exists/read_binary, the directory and
+// embedded readers, "embedded:<profile>" locations and the default-location
+// rule of core/src/model_assets.cpp:36-252), plus an in-memory reader. This
+// build links no embedded model image, so it behaves like the reference built
+// without MLVC_HAS_EMBEDDED_MODELS: embedded readers hold no files and the
+// profile list is empty.
 
 #include <cstddef>
 #include <filesystem>
 #include <map>
 #include <memory>
 #include <string>
+#include <string_view>
 #include <vector>
 
 namespace mlvc {
@@ -40,9 +44,21 @@ private:
 std::shared_ptr<const ModelAssetReader> make_directory_asset_reader(
     std::filesystem::path directory);
 
-// Returns `override_reader` when set, else a directory reader on `model_dir`.
+// Reader of a profile compiled into the binary ("embedded:<profile>");
+// profiles containing '/' or '\\' are rejected.
+std::shared_ptr<const ModelAssetReader> make_embedded_asset_reader(std::string_view profile);
+
+// "embedded:<profile>" -> embedded reader, anything else -> directory reader.
+std::shared_ptr<const ModelAssetReader> make_model_asset_reader(const std::filesystem::path& location);
+
+// `override_reader` when set, else a reader for `model_dir`, else the default
+// embedded model (an error when none is linked).
 std::shared_ptr<const ModelAssetReader> resolve_model_asset_reader(
     const std::filesystem::path& model_dir,
     std::shared_ptr<const ModelAssetReader> override_reader = nullptr);
+
+std::vector<std::string> list_embedded_model_profiles();
+// "embedded:mlvc-psnr-v1" when linked, else the first embedded profile, else empty.
+std::filesystem::path default_model_location();
 
 }  // namespace mlvc

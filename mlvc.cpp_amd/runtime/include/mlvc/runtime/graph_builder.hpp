@@ -49,6 +49,9 @@ public:
     Id gather(const std::string& name, Id data, Id indices, int axis);
 
     void output(Id id) { outputs_.push_back(id); }
+    // Model description written to metadata.pb (profile and checkpoint hash
+    // are filled by build()); unset, a minimal placeholder is written.
+    void set_metadata(const wire::ModelMetadata& m) { metadata_ = m; has_metadata_ = true; }
     const Shape& shape(Id id) const { return tensors_.at(id - 1).shape; }
     std::size_t node_count() const { return nodes_.size(); }
 
@@ -57,6 +60,9 @@ public:
     };
     // Plans the arena, serialises the graph and computes SHA-256 provenance.
     Files build(const std::string& profile) const;
+    // Writes aot/<model>/{graph.pb,weights.bin}, metadata.pb and
+    // model_bundle.pb (the bundle's artifact list keeps the entries of other
+    // graphs already written to the same directory).
     void write_directory(const std::filesystem::path& dir, const std::string& model_name,
                          const std::string& profile) const;
     std::shared_ptr<const ModelAssetReader> to_memory(const std::string& model_name,
@@ -94,6 +100,8 @@ private:
     std::vector<N> nodes_;
     std::vector<Id> inputs_, outputs_;
     std::vector<std::byte> weights_;
+    wire::ModelMetadata metadata_;
+    bool has_metadata_ = false;
 };
 
 // SHA-256 (FIPS 180-4), used for the weights_sha256 provenance field.

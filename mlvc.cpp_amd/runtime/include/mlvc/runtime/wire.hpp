@@ -15,6 +15,7 @@
 #include <cstdint>
 #include <optional>
 #include <span>
+#include <stdexcept>
 #include <string>
 #include <vector>
 
@@ -84,11 +85,50 @@ struct ModelMetadata {
     bool disable_feature_reset = false;
 };
 
+// model_bundle.pb (proto/mlvc_model.proto:135-161).
+struct CodecContract {
+    std::string container, entropy;
+    std::uint32_t decoder_max_yuv_sample_error = 0;
+    double decoder_min_psnr_db = 0.0;
+};
+struct Artifact {
+    std::string path;
+    std::uint64_t size_bytes = 0;
+    std::string sha256;
+};
+struct ModelBundle {
+    std::uint32_t schema_version = 0;
+    std::string profile, model_version;
+    std::uint32_t width = 0, height = 0;
+    std::string checkpoint_sha256, entropy_model_sha256;
+    CodecContract contract;
+    std::vector<Artifact> artifacts;
+};
+
 // Throw std::runtime_error on malformed input.
 Graph parse_graph(std::span<const std::byte> bytes);
 ModelMetadata parse_metadata(std::span<const std::byte> bytes);
+ModelBundle parse_bundle(std::span<const std::byte> bytes);
+
+// A model file as the loaders read it (reference core/src/model_proto.hpp:11-23,
+// runtime/src/aot_graph.cpp:95-106): empty or above 64 MiB is
+// "invalid Protobuf model message size: <label>", a parse failure is
+// "invalid Protobuf model message: <label>".
+template <typename Parse>
+auto parse_model_file(std::span<const std::byte> bytes, const std::string& label, Parse parse)
+{
+    constexpr std::size_t kLimit = 64U * 1024U * 1024U;
+    if (bytes.empty() || bytes.size() > kLimit)
+        throw std::runtime_error("invalid Protobuf model message size: " + label);
+    try {
+        return parse(bytes);
+    } catch (const std::exception&) {
+        throw std::runtime_error("invalid Protobuf model message: " + label);
+    }
+}
 
 std::vector<std::byte> serialize(const Graph& graph);
 std::vector<std::byte> serialize(const ModelMetadata& metadata);
+std::vector<std::byte> serialize(const ModelBundle& bundle);
 
 }  // namespace mlvc::wire

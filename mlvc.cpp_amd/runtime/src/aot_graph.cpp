@@ -62,14 +62,6 @@ Op to_op(std::int32_t v)
     return static_cast<Op>(v);
 }
 
-std::span<const std::byte> checked_message(std::span<const std::byte> bytes, const std::string& label)
-{
-    constexpr std::size_t kLimit = 64U * 1024U * 1024U;
-    if (bytes.empty() || bytes.size() > kLimit)
-        throw std::runtime_error("invalid Protobuf model message size: " + label);
-    return bytes;
-}
-
 GraphDescriptor decode(const wire::Graph& g)
 {
     require(g.schema_version == 3, "unsupported schema");
@@ -242,7 +234,7 @@ std::size_t tensor_bytes(const TensorDescriptor& t)
 
 GraphDescriptor decode_graph_binary(std::span<const std::byte> bytes)
 {
-    return decode(wire::parse_graph(checked_message(bytes, "graph.pb")));
+    return decode(wire::parse_model_file(bytes, "graph.pb", wire::parse_graph));
 }
 
 LoadedGraph load_aot_graph(const ModelAssetReader& assets, const std::string& model_name)
@@ -250,9 +242,9 @@ LoadedGraph load_aot_graph(const ModelAssetReader& assets, const std::string& mo
     const std::filesystem::path dir = std::filesystem::path("aot") / model_name;
     const auto graph_bytes = assets.read_binary(dir / "graph.pb");
     const wire::Graph graph =
-        wire::parse_graph(checked_message(graph_bytes, (dir / "graph.pb").string()));
+        wire::parse_model_file(graph_bytes, (dir / "graph.pb").string(), wire::parse_graph);
     const auto meta_bytes = assets.read_binary("metadata.pb");
-    const wire::ModelMetadata meta = wire::parse_metadata(checked_message(meta_bytes, "metadata.pb"));
+    const wire::ModelMetadata meta = wire::parse_model_file(meta_bytes, "metadata.pb", wire::parse_metadata);
     if (graph.checkpoint_sha256 != meta.checkpoint_sha256)
         throw std::runtime_error("AOT graph checkpoint differs from metadata (" +
                                  assets.location_label() + ")");

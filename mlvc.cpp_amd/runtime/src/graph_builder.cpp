@@ -9,6 +9,7 @@
 #include <fstream>
 #include <map>
 #include <stdexcept>
+#include <optional>
 
 namespace mlvc::synth {
 namespace {
@@ -404,16 +405,60 @@ GraphBuilder::Files GraphBuilder::build(const std::string& profile) const
     f.graph_pb = wire::serialize(g);
 
     wire::ModelMetadata m;
+    if (has_metadata_) {
+        m = metadata_;
+    } else {
+        m.model_version = "synthetic";
+        m.pixel_range = 255.0F;
+        m.qp_num = 1;
+        m.total_qp_num = 1;
+    }
     m.schema_version = 1;
     m.profile = profile;
-    m.model_version = "synthetic";
     m.checkpoint_sha256 = g.checkpoint_sha256;
-    m.pixel_range = 255.0F;
-    m.qp_num = 1;
-    m.total_qp_num = 1;
     f.metadata_pb = wire::serialize(m);
     return f;
 }
+
+namespace {
+
+// model_bundle.pb for a directory holding `files` (path -> bytes): schema 2,
+// the metadata's identity, the codec contract, one artifact per file with
+// its size and SHA-256, sorted by path. Entries of `previous` for other paths
+// are kept. With no entropy model tables present, the entropy hash is the
+// SHA-256 of nothing.
+std::vector<std::byte> make_bundle(const wire::ModelMetadata& m, const std::map<std::string, const std::vector<std::byte>*>& files,
+                                   const wire::ModelBundle* previous)
+{
+    wire::ModelBundle b;
+    b.schema_version = 2;
+    b.profile = m.profile;
+    b.model_version = m.model_version;
+    b.width = m.width;
+    b.height = m.height;
+    b.checkpoint_sha256 = m.checkpoint_sha256;
+    const auto empty = sha256(nullptr, 0);
+    b.entropy_model_sha256.assign(reinterpret_cast<const char*>(empty.data()), 32);
+    b.contract.container = "mlvc-nalu-v0";
+    b.contract.entropy = "canonical-pmf-v1";
+    b.contract.decoder_max_yuv_sample_error = 1;
+    b.contract.decoder_min_psnr_db = 60.0;
+    std::map<std::string, wire::Artifact> arts;
+    if (previous && previous->profile == m.profile && previous->checkpoint_sha256 == m.checkpoint_sha256)
+        for (const auto& a : previous->artifacts) arts[a.path] = a;
+    for (const auto& [path, bytes] : files) {
+        wire::Artifact a;
+        a.path = path;
+        a.size_bytes = bytes->size();
+        const auto d = sha256(bytes->data(), bytes->size());
+        a.sha256.assign(reinterpret_cast<const char*>(d.data()), 32);
+        arts[path] = a;
+    }
+    for (auto& [path, a] : arts) b.artifacts.push_back(a);
+    return wire::serialize(b);
+}
+
+}  // namespace
 
 void GraphBuilder::write_directory(const std::filesystem::path& dir, const std::string& model_name,
                                    const std::string& profile) const
@@ -429,6 +474,18 @@ void GraphBuilder::write_directory(const std::filesystem::path& dir, const std::
     put(gdir / "graph.pb", f.graph_pb);
     put(gdir / "weights.bin", f.weights_bin);
     put(dir / "metadata.pb", f.metadata_pb);
+    std::optional<wire::ModelBundle> previous;
+    if (std::filesystem::is_regular_file(dir / "model_bundle.pb")) {
+        try {
+            previous = wire::parse_bundle(make_directory_asset_reader(dir)->read_binary("model_bundle.pb"));
+        } catch (const std::exception&) {
+            previous.reset();
+        }
+    }
+    const std::string g = "aot/" + model_name + "/";
+    const std::map<std::string, const std::vector<std::byte>*> files{
+        {g + "graph.pb", &f.graph_pb}, {g + "weights.bin", &f.weights_bin}, {"metadata.pb", &f.metadata_pb}};
+    put(dir / "model_bundle.pb", make_bundle(wire::parse_metadata(f.metadata_pb), files, previous ? &*previous : nullptr));
 }
 
 std::shared_ptr<const ModelAssetReader> GraphBuilder::to_memory(const std::string& model_name,
@@ -440,6 +497,10 @@ std::shared_ptr<const ModelAssetReader> GraphBuilder::to_memory(const std::strin
     r->add(gdir / "graph.pb", f.graph_pb);
     r->add(gdir / "weights.bin", f.weights_bin);
     r->add("metadata.pb", f.metadata_pb);
+    const std::string g = "aot/" + model_name + "/";
+    const std::map<std::string, const std::vector<std::byte>*> files{
+        {g + "graph.pb", &f.graph_pb}, {g + "weights.bin", &f.weights_bin}, {"metadata.pb", &f.metadata_pb}};
+    r->add("model_bundle.pb", make_bundle(wire::parse_metadata(f.metadata_pb), files, nullptr));
     return r;
 }
 

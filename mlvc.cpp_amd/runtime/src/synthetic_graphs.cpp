@@ -261,6 +261,27 @@ void build_codec(GraphBuilder& g, Rng& rng, SyntheticModel& info, int h, int w, 
     }
     info.model_name = encoder ? "MLVCEncoder" : "MLVCDecoder";
     info.profile = "synthetic/codec_" + std::to_string(w) + "x" + std::to_string(h);
+    // The bundle's model description (metadata.pb), shared by both graphs:
+    // 64-channel feature at 1/2, 256-channel latent at 1/16, hyperprior at
+    // 1/64, QP table of 64 of 72 with a 4-frame shift cycle, no feature reset.
+    wire::ModelMetadata meta;
+    meta.model_version = "synthetic-v1";
+    meta.width = static_cast<std::uint32_t>(w);
+    meta.height = static_cast<std::uint32_t>(h);
+    meta.pixel_range = 1.0F;
+    meta.qp_num = 64;
+    meta.total_qp_num = 72;
+    meta.frame_index_map = {0, 1, 2, 3};
+    meta.qp_shift = {0, 8, 4, 8};
+    meta.feature_channels = 64;
+    meta.latent_channels = 256;
+    meta.hyperprior_channels = 128;
+    meta.downsample_feature = 2;
+    meta.downsample_latent = 16;
+    meta.downsample_hyperprior = 4;
+    meta.y_scale_repeat = 2;
+    meta.disable_feature_reset = true;
+    g.set_metadata(meta);
     info.state_bindings = {StateTensorBinding{2, 1, TensorDataType::kFloat16, {1, 64, h / 2, w / 2}}};
     info.frames = frames;
 }

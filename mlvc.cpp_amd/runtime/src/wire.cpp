@@ -68,6 +68,14 @@ public:
         p_ += 4;
         return v;
     }
+    std::uint64_t fixed64()
+    {
+        if (end_ - p_ < 8) fail("truncated fixed64");
+        std::uint64_t v;
+        std::memcpy(&v, p_, 8);
+        p_ += 8;
+        return v;
+    }
     std::span<const std::uint8_t> len_delimited()
     {
         const std::uint64_t n = varint();
@@ -291,6 +299,11 @@ public:
         u64(field, z);
     }
     void boolean(std::uint32_t field, bool v) { u64(field, v ? 1 : 0); }
+    void f64(std::uint32_t field, double v)
+    {
+        const auto bits = std::bit_cast<std::uint64_t>(v);
+        if (bits) { tag(field, kFixed64); raw(&bits, 8); }
+    }
     void f32(std::uint32_t field, float v)
     {
         const auto bits = std::bit_cast<std::uint32_t>(v);
@@ -487,6 +500,86 @@ std::vector<std::byte> serialize(const ModelMetadata& m)
     if (m.iframe_period) { w.tag(19, kVarint); w.varint(*m.iframe_period); }
     if (m.reset_period) { w.tag(20, kVarint); w.varint(*m.reset_period); }
     w.boolean(21, m.disable_feature_reset);
+    return w.take();
+}
+
+ModelBundle parse_bundle(std::span<const std::byte> bytes)
+{
+    ModelBundle b;
+    Reader r(as_u8(bytes));
+    while (!r.done()) {
+        const auto [f, wt] = r.tag();
+        bool ok = true;
+        auto u32 = [&](std::uint32_t& dst) { return wt == kVarint && (dst = as_u32(r.varint()), true); };
+        switch (f) {
+        case 1: ok = u32(b.schema_version); break;
+        case 2: ok = wt == kLen && (b.profile = read_string(r, true), true); break;
+        case 3: ok = wt == kLen && (b.model_version = read_string(r, true), true); break;
+        case 4: ok = u32(b.width); break;
+        case 5: ok = u32(b.height); break;
+        case 6: ok = wt == kLen && (b.checkpoint_sha256 = read_string(r, false), true); break;
+        case 7: ok = wt == kLen && (b.entropy_model_sha256 = read_string(r, false), true); break;
+        case 8: {
+            if (wt != kLen) { ok = false; break; }
+            Reader c(r.len_delimited());
+            while (!c.done()) {
+                const auto [cf, cwt] = c.tag();
+                bool cok = true;
+                if (cf == 1 && cwt == kLen) b.contract.container = read_string(c, true);
+                else if (cf == 2 && cwt == kLen) b.contract.entropy = read_string(c, true);
+                else if (cf == 3 && cwt == kVarint) b.contract.decoder_max_yuv_sample_error = as_u32(c.varint());
+                else if (cf == 4 && cwt == kFixed64) b.contract.decoder_min_psnr_db = std::bit_cast<double>(c.fixed64());
+                else cok = false;
+                if (!cok) c.skip(cwt);
+            }
+            break;
+        }
+        case 9: {
+            if (wt != kLen) { ok = false; break; }
+            Artifact a;
+            Reader c(r.len_delimited());
+            while (!c.done()) {
+                const auto [af, awt] = c.tag();
+                bool aok = true;
+                if (af == 1 && awt == kLen) a.path = read_string(c, true);
+                else if (af == 2 && awt == kVarint) a.size_bytes = c.varint();
+                else if (af == 3 && awt == kLen) a.sha256 = read_string(c, false);
+                else aok = false;
+                if (!aok) c.skip(awt);
+            }
+            b.artifacts.push_back(std::move(a));
+            break;
+        }
+        default: ok = false;
+        }
+        if (!ok) r.skip(wt);
+    }
+    return b;
+}
+
+std::vector<std::byte> serialize(const ModelBundle& b)
+{
+    Writer w;
+    w.u64(1, b.schema_version);
+    w.bytes(2, b.profile);
+    w.bytes(3, b.model_version);
+    w.u64(4, b.width);
+    w.u64(5, b.height);
+    w.bytes(6, b.checkpoint_sha256);
+    w.bytes(7, b.entropy_model_sha256);
+    Writer c;
+    c.bytes(1, b.contract.container);
+    c.bytes(2, b.contract.entropy);
+    c.u64(3, b.contract.decoder_max_yuv_sample_error);
+    c.f64(4, b.contract.decoder_min_psnr_db);
+    w.message(8, c);
+    for (const Artifact& a : b.artifacts) {
+        Writer aw;
+        aw.bytes(1, a.path);
+        aw.u64(2, a.size_bytes);
+        aw.bytes(3, a.sha256);
+        w.message(9, aw);
+    }
     return w.take();
 }
 

@@ -6,9 +6,9 @@
   (packed and unpacked repeated fields, fields out of order, unknown fields)
   are accepted by the C++ loader.
 * Rejections mirror decode_graph (runtime/src/aot_graph.cpp:110-284) and the
-  reference's tests/unit/model_proto_tests.cpp:59-123: bad schema, missing
-  SHA, bad arena alignment, duplicate IDs, forward references, misaligned
-  weight offsets, asymmetric pads, dilation, wrong attributes, birth.
+  reference's tests/unit/model_proto_tests.cpp:59-123: every require() of
+  decode_graph is reached by at least one case (REJECTIONS), with the
+  reference's message, plus the parse and checkpoint/weights-size checks.
 * Arena non-overlap of live tensors (reference tests/unit/aot_tests.py:99-106)
   for every synthetic workload, and weights_sha256 == hashlib.sha256.
 """
@@ -316,3 +316,294 @@ def test_synthetic_generator_is_deterministic(tmp_path):
     x1 = mlvc_hip.synth_input("mlvc_s_tiny", 0, 1, (1, 3, 32, 64))
     f = graphs.to_float(x0)
     assert not (x0 == x1).all() and f.min() >= 0.0 and f.max() <= 1.0
+
+
+# ---- every decode_graph rejection (runtime/src/aot_graph.cpp:110-284) ---------------------------
+
+def _one_input(shape=(1, 4, 4, 4), dtype=graphs.FP16):
+    g = graphs.Graph()
+    x = g.input("x", list(shape), dtype)
+    return g, x
+
+
+def _unary_graph(op="SIGMOID", extra_inputs=(), attr=None):
+    g, x = _one_input()
+    y = g.node(op, [x, *extra_inputs], "y", g.shape(x), attr)
+    g.output(y)
+    return g
+
+
+def _case_weights_sha():
+    g = _conv_graph()
+    g.weights_sha = b"x" * 5
+    return g
+
+
+def _case_no_tensors():
+    return graphs.Graph()
+
+
+def _case_no_nodes():
+    g, x = _one_input()
+    g.output(x)
+    return g
+
+
+def _case_rank():
+    g, x = _one_input((1, 2, 2, 2, 2))
+    g.output(g.leaky_relu("y", x))
+    return g
+
+
+def _case_zero_dim():
+    g, x = _one_input((1, 0, 4, 4))
+    g.output(g.leaky_relu("y", x))
+    return g
+
+
+def _case_dtype(dtype):
+    def make():
+        g, x = _one_input(dtype=dtype)
+        y = g.leaky_relu("y", x)
+        g.output(y)
+        return g
+    return make
+
+
+def _case_input_with_arena():
+    g, x = _one_input()
+    y = g.leaky_relu("y", x)
+    g.inputs.append(y)
+    g.output(y)
+    return g
+
+
+def _case_input_twice():
+    g, x = _one_input()
+    g.inputs.append(x)
+    g.output(g.leaky_relu("y", x))
+    return g
+
+
+def _case_concat_without_axis():
+    g, x = _one_input()
+    y = g.node("CONCAT", [x, x], "y", [1, 8, 4, 4])
+    g.output(y)
+    return g
+
+
+def _case_gather_three_inputs():
+    g, x = _one_input()
+    i = g.weight("i", np.zeros(1, np.int64), graphs.INT64)
+    y = g.node("GATHER", [x, i, i], "y", [1, 1, 4, 4], ("axis", 1))
+    g.output(y)
+    return g
+
+
+def _case_binary_with_attr():
+    g, x = _one_input()
+    y = g.node("ADD", [x, x], "y", g.shape(x), ("axis", 1))
+    g.output(y)
+    return g
+
+
+def _case_binary_absent_operand():
+    g, x = _one_input()
+    y = g.node("MUL", [x, 0], "y", g.shape(x))
+    g.output(y)
+    return g
+
+
+def _case_conv_absent_weight():
+    g, x = _one_input()
+    y = g.node("CONV", [x, 0, 0], "y", g.shape(x), ("conv", [1, 1], [0, 0, 0, 0], [1, 1], 1))
+    g.output(y)
+    return g
+
+
+def _case_clip_four_inputs():
+    g, x = _one_input()
+    y = g.node("CLIP", [x, 0, 0, 0], "y", g.shape(x))
+    g.output(y)
+    return g
+
+
+def _case_slice_two_inputs():
+    g, x = _one_input()
+    s = g.weight("s", np.zeros(1, np.int64), graphs.INT64)
+    y = g.node("SLICE", [x, s], "y", g.shape(x))
+    g.output(y)
+    return g
+
+
+def _case_slice_absent_ends():
+    g, x = _one_input()
+    s = g.weight("s", np.zeros(1, np.int64), graphs.INT64)
+    y = g.node("SLICE", [x, s, 0], "y", g.shape(x))
+    g.output(y)
+    return g
+
+
+def _case_pixel_block(block):
+    def make():
+        g, x = _one_input((1, 16, 4, 4))
+        y = g.node("DEPTH_TO_SPACE", [x], "y", [1, 4, 8, 8], None if block is None else ("pixel", block))
+        g.output(y)
+        return g
+    return make
+
+
+def _case_conv_attr(strides, pads, dil, groups):
+    def make():
+        g = _conv_graph()
+        g.nodes[0]["attr"] = ("conv", strides, pads, dil, groups)
+        return g
+    return make
+
+
+def _case_op(op):
+    def make():
+        g = _unary_graph()
+        g.nodes[0]["op"] = op
+        return g
+    return make
+
+
+def _case_two_outputs():
+    g = _unary_graph()
+    g.nodes[0]["outputs"].append(1)
+    return g
+
+
+def _case_output_is_weight():
+    g, x = _one_input()
+    w = g.weight_fp16("w", np.zeros((1, 4, 4, 4)))
+    g.nodes.append(dict(op=graphs.OPS["LEAKY_RELU"], inputs=[x], outputs=[w], attr=("activation", 0.1)))
+    g.output(w)
+    return g
+
+
+def _case_output_written_twice():
+    g, x = _one_input()
+    y = g.leaky_relu("y", x)
+    g.nodes.append(dict(op=graphs.OPS["LEAKY_RELU"], inputs=[x], outputs=[y], attr=("activation", 0.1)))
+    g.output(y)
+    return g
+
+
+def _case_graph_output_twice():
+    g = _unary_graph()
+    g.output(g.outputs[0])
+    return g
+
+
+def _case_graph_output_unknown():
+    g = _unary_graph()
+    g.outputs.append(77)
+    return g
+
+
+def _case_arena_misaligned():
+    g = _unary_graph()
+    g.tensors[1]["storage"][1] = 8
+    return g
+
+
+def _case_arena_death_past_end():
+    g = _unary_graph()
+    g.tensors[1]["storage"][4] = 5
+    return g
+
+
+def _case_int32_weight():
+    g = _conv_graph()
+    st = g.tensors[1]["storage"]
+    g.tensors[1]["dtype"] = graphs.INT32
+    g.tensors[1]["shape"] = [4, 4, 3, 3]
+    g.tensors[1]["storage"] = ("weight", st[1], 4 * 4 * 9 * 4)
+    g.weights.extend(b"\0" * (4 * 4 * 9 * 2))
+    return g
+
+
+def _case_empty_name():
+    g = _unary_graph()
+    g.tensors[0]["name"] = ""
+    return g
+
+
+def _case_duplicate_name():
+    g = _unary_graph()
+    g.tensors[1]["name"] = "x"
+    return g
+
+
+def _case_id_out_of_range():
+    g = _unary_graph()
+    g.tensors[1]["id"] = 9
+    return g
+
+
+REJECTIONS = [
+    ("weights_sha", _case_weights_sha, "missing SHA-256 provenance"),
+    ("no_tensors", _case_no_tensors, "tensor count"),
+    ("no_nodes", _case_no_nodes, "empty graph"),
+    ("rank5", _case_rank, "tensor rank"),
+    ("zero_dim", _case_zero_dim, "tensor extent overflow"),
+    ("dtype_unspecified", _case_dtype(0), "unsupported dtype"),
+    ("dtype_unknown", _case_dtype(7), "unsupported dtype"),
+    ("int64_activation", _case_dtype(graphs.INT64), "runtime int64 tensor"),
+    ("input_with_arena", _case_input_with_arena, "input ID or storage"),
+    ("input_twice", _case_input_twice, "input ID or storage"),
+    ("concat_no_axis", _case_concat_without_axis, "axis contract"),
+    ("gather_3_inputs", _case_gather_three_inputs, "axis contract"),
+    ("binary_attr", _case_binary_with_attr, "binary contract"),
+    ("binary_absent", _case_binary_absent_operand, "absent required operand"),
+    ("conv_absent_w", _case_conv_absent_weight, "absent required operand"),
+    ("clip_4_inputs", _case_clip_four_inputs, "clip contract"),
+    ("slice_2_inputs", _case_slice_two_inputs, "slice contract"),
+    ("slice_absent_ends", _case_slice_absent_ends, "absent required operand"),
+    ("unary_2_inputs", lambda: _unary_graph("ROUND", extra_inputs=(1,)), "unary contract"),
+    ("unary_attr", lambda: _unary_graph("RECIPROCAL", attr=("axis", 0)), "unary contract"),
+    ("pixel_no_attr", _case_pixel_block(None), "pixel layout contract"),
+    ("pixel_block0", _case_pixel_block(0), "invalid positive attribute"),
+    ("conv_groups0", _case_conv_attr([1, 1], [1, 1, 1, 1], [1, 1], 0), "invalid positive attribute"),
+    ("conv_3_strides", _case_conv_attr([1, 1, 1], [1, 1, 1, 1], [1, 1], 1), "attribute dimension count"),
+    ("conv_3_pads", _case_conv_attr([1, 1], [1, 1, 1], [1, 1], 1), "attribute dimension count"),
+    ("conv_stride0", _case_conv_attr([0, 1], [1, 1, 1, 1], [1, 1], 1), "invalid attribute dimension"),
+    ("conv_dil0", _case_conv_attr([1, 1], [1, 1, 1, 1], [0, 1], 1), "invalid attribute dimension"),
+    ("conv_pad_huge", _case_conv_attr([1, 1], [1 << 31, 1, 1 << 31, 1], [1, 1], 1), "invalid attribute dimension"),
+    ("op_unspecified", _case_op(0), "unknown operator"),
+    ("op_unknown", _case_op(42), "unknown operator"),
+    ("two_outputs", _case_two_outputs, "output ID"),
+    ("output_is_weight", _case_output_is_weight, "duplicate output or missing arena"),
+    ("output_written_twice", _case_output_written_twice, "duplicate output or missing arena"),
+    ("graph_output_twice", _case_graph_output_twice, "graph output"),
+    ("graph_output_unknown", _case_graph_output_unknown, "graph output"),
+    ("arena_misaligned", _case_arena_misaligned, "arena extent"),
+    ("arena_death", _case_arena_death_past_end, "arena extent"),
+    ("int32_weight", _case_int32_weight, "weight extent"),
+    ("empty_name", _case_empty_name, "duplicate tensor ID or name"),
+    ("duplicate_name", _case_duplicate_name, "duplicate tensor ID or name"),
+    ("id_out_of_range", _case_id_out_of_range, "tensor ID range"),
+]
+
+
+@pytest.mark.parametrize("make,message", [c[1:] for c in REJECTIONS], ids=[c[0] for c in REJECTIONS])
+def test_every_decode_rejection(tmp_path, make, message):
+    g = make()
+    g.write(tmp_path, "m")
+    with pytest.raises(mlvc_hip.MlvcError) as e:
+        mlvc_hip.aot_inspect(tmp_path, "m")
+    # require() prefixes its condition (aot_graph.cpp:12-18).
+    assert str(e.value).endswith("invalid AOT Protobuf graph: " + message), str(e.value)
+
+
+def test_reject_unparseable_files(tmp_path):
+    """parse_proto_bytes (aot_graph.cpp:95-106), labelled with the graph path (:296-298)."""
+    _conv_graph().write(tmp_path, "m")
+    (tmp_path / "aot" / "m" / "graph.pb").write_bytes(b"")
+    with pytest.raises(mlvc_hip.MlvcError, match="invalid Protobuf model message size: aot/m/graph.pb"):
+        mlvc_hip.aot_inspect(tmp_path, "m")
+    (tmp_path / "aot" / "m" / "graph.pb").write_bytes(b"\x0a\xff\x01abc")  # length past the end
+    with pytest.raises(mlvc_hip.MlvcError, match="invalid Protobuf model message: aot/m/graph.pb"):
+        mlvc_hip.aot_inspect(tmp_path, "m")
