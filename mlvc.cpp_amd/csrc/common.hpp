@@ -89,37 +89,41 @@ __device__ __forceinline__ std::uint32_t pack_f16(float a0, float a1)
     return __builtin_bit_cast(std::uint32_t, h);
 }
 
-// LeakyReLU of a packed pair of FP16 values (already rounded), as in
-// leaky_pair below.
+// LeakyReLU of a packed pair of FP16 values h (already rounded): the
+// reference's select, h < 0 ? fp16(fp32(h * alpha)) : h. The product is
+// computed for both lanes unconditionally and the choice is a per-lane
+// select, so the code is straight-line (no divergent branches around the
+// multiply). For 0 <= alpha <= 1 the select equals max(h, fp16(h * alpha))
+// (rounding is monotonic; NaN and -0 keep h), one packed max.
 __device__ __forceinline__ std::uint32_t leaky_h2(std::uint32_t hv, float alpha, bool max_form)
 {
     const half2_t h = __builtin_bit_cast(half2_t, hv);
-    if (max_form) {
-        const half2_t p = {static_cast<_Float16>(mul_f32(static_cast<float>(h[0]), alpha)),
-                           static_cast<_Float16>(mul_f32(static_cast<float>(h[1]), alpha))};
-        return __builtin_bit_cast(std::uint32_t, __builtin_elementwise_max(h, p));
-    }
-    const std::uint16_t h0 = static_cast<std::uint16_t>(hv), h1 = static_cast<std::uint16_t>(hv >> 16);
-    const std::uint16_t r0 = h2f(h0) < 0.0f ? leaky_f16(h2f(h0), alpha) : h0;
-    const std::uint16_t r1 = h2f(h1) < 0.0f ? leaky_f16(h2f(h1), alpha) : h1;
-    return r0 | (static_cast<std::uint32_t>(r1) << 16);
+    const float f0 = static_cast<float>(h[0]), f1 = static_cast<float>(h[1]);
+    const half2_t p = {static_cast<_Float16>(mul_f32(f0, alpha)), static_cast<_Float16>(mul_f32(f1, alpha))};
+    if (max_form) return __builtin_bit_cast(std::uint32_t, __builtin_elementwise_max(h, p));
+    const half2_t r = {f0 < 0.0f ? p[0] : h[0], f1 < 0.0f ? p[1] : h[1]};
+    return __builtin_bit_cast(std::uint32_t, r);
 }
 
-// Two FP32 accumulators -> packed FP16 pair after LeakyReLU on the rounded
-// values. For 0 <= alpha <= 1 this is max(h, fp16(h * alpha)), which equals
-// the select form because rounding is monotonic; otherwise the select form.
+// Two FP32 accumulators -> packed FP16 pair (RNE) after LeakyReLU on the
+// rounded values, as leaky_h2.
 __device__ __forceinline__ std::uint32_t leaky_pair(float a0, float a1, float alpha, bool max_form)
 {
-    const half2_t h = {static_cast<_Float16>(a0), static_cast<_Float16>(a1)};
-    if (max_form) {
-        const half2_t p = {static_cast<_Float16>(mul_f32(static_cast<float>(h[0]), alpha)),
-                           static_cast<_Float16>(mul_f32(static_cast<float>(h[1]), alpha))};
-        return __builtin_bit_cast(std::uint32_t, __builtin_elementwise_max(h, p));
-    }
-    const std::uint16_t h0 = __builtin_bit_cast(std::uint16_t, h[0]), h1 = __builtin_bit_cast(std::uint16_t, h[1]);
-    const std::uint16_t r0 = h2f(h0) < 0.0f ? leaky_f16(h2f(h0), alpha) : h0;
-    const std::uint16_t r1 = h2f(h1) < 0.0f ? leaky_f16(h2f(h1), alpha) : h1;
-    return r0 | (static_cast<std::uint32_t>(r1) << 16);
+    return leaky_h2(pack_f16(a0, a1), alpha, max_form);
+}
+
+// Epilogue modes fixed at compile time: 0 none, 1 LeakyReLU with
+// 0 <= alpha <= 1 (max form), 2 LeakyReLU with any other alpha (select form).
+inline int epi_mode(int epi_is_leaky, float alpha)
+{
+    return epi_is_leaky ? (alpha >= 0.0f && alpha <= 1.0f ? 1 : 2) : 0;
+}
+
+template <int MODE>
+__device__ __forceinline__ std::uint32_t epi_pair(float a0, float a1, float alpha)
+{
+    if constexpr (MODE == 0) return pack_f16(a0, a1);
+    else return leaky_h2(pack_f16(a0, a1), alpha, MODE == 1);
 }
 
 }  // namespace mlvc_hip

@@ -42,6 +42,19 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(ConvArgs a, int n)
 
 // ---------------------------------------------------------------- variants
 
+int cu_count()
+{
+    static int cus = [] {
+        int dev = 0, n = 256;
+        if (hipGetDevice(&dev) == hipSuccess) {
+            hipDeviceProp_t p;
+            if (hipGetDeviceProperties(&p, dev) == hipSuccess) n = p.multiProcessorCount;
+        }
+        return n;
+    }();
+    return cus;
+}
+
 }  // namespace conv
 
 namespace {
@@ -64,19 +77,6 @@ const std::vector<Variant>& variants()
 }
 
 int variant_count() { return static_cast<int>(variants().size()); }
-
-int cu_count()
-{
-    static int cus = [] {
-        int dev = 0, n = 256;
-        if (hipGetDevice(&dev) == hipSuccess) {
-            hipDeviceProp_t p;
-            if (hipGetDeviceProperties(&p, dev) == hipSuccess) n = p.multiProcessorCount;
-        }
-        return n;
-    }();
-    return cus;
-}
 
 bool flat_1x1(const mlvc_hip_conv_desc& d)
 {

@@ -338,6 +338,264 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void c
     }
 }
 
+// Streaming form for a single input chunk (ica <= 16, as in the frame stem:
+// 12 channels after SPACE_TO_DEPTH(2)). Same tile, K orders and rounding
+// points as conv_pair_kernel (bit-identical results), organised so that HBM
+// reads overlap compute instead of alternating with it:
+//   * a persistent grid (two workgroups per CU) walks the tiles; the 3x3
+//     weights stay in LDS and the 1x1 weight fragments in registers for the
+//     whole walk;
+//   * the input units and r of tile i + 1 are loaded into registers while
+//     tile i is computed;
+//   * each wave owns one row of 32 pixels: it stages that row's r into P
+//     and writes its own t there, and phase B reads only those rows, so P
+//     needs no barrier; the two barriers per tile guard the shared input
+//     halo tile;
+//   * phase B runs with the MFMA operands swapped (pixels as M, output
+//     channels as N; the same products and K order, so the same bits), which
+//     leaves 4 consecutive pixels of one channel in each lane: the rounded,
+//     activated results go into the wave's (now dead) P rows as a
+//     [channel][pixel] tile with 8-byte writes and leave as 16-byte rows.
+template <class C, int EA, int EB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void conv_pair_stream_kernel(PairArgs a)
+{
+    static_assert(C::TW == 32 && C::TH == 4 && C::NT == 1 && C::WN == 32, "one 32-pixel row per wave");
+    constexpr int IN0 = C::WA_LDS, PS0 = C::WA_LDS + C::IN_LDS, LDS_S = PS0 + C::BN * C::PS;
+    constexpr int XUNITS = 2 * C::IH_T * C::NSEG;  // 8 loads each
+    constexpr int kStgRow = 40;                    // output staging row (one channel, 32 pixels), halves
+    static_assert(C::OCB * kStgRow <= 32 * C::PS, "staging fits a wave's P rows");
+    static_assert(XUNITS <= C::kThreads && IN0 % 8 == 0 && PS0 % 8 == 0 && LDS_S * 2 <= 80 * 1024, "stream tile");
+    __shared__ __attribute__((aligned(16))) std::uint16_t lds[LDS_S];
+    std::uint16_t* const wa_s = lds;
+    std::uint16_t* const in_s = lds + IN0;
+    std::uint16_t* const ps = lds + PS0;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int koff = (lane >> 5) * 8, hsel = 4 * (lane >> 5);
+    const std::uint32_t hw = static_cast<std::uint32_t>(a.h) * a.w, hw2 = hw * 2u;
+    const int csrc = C::STG == 2 ? a.ica / 4 : a.ica;
+    const std::uint32_t plane_src = C::STG == 2 ? 4u * hw2 : hw2;  // bytes per source channel
+    const int sw = C::STG == 2 ? a.w * 2 : a.w;
+    const int G = static_cast<int>(gridDim.x);
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+    // Resident weights: the 3x3 chunk in LDS, the 1x1 fragments in registers.
+    {
+        const u32x4* ws = reinterpret_cast<const u32x4*>(a.wa);
+        for (int e = tid; e < C::WA_VEC; e += C::kThreads) reinterpret_cast<u32x4*>(wa_s)[e] = ws[e];
+    }
+    const u32x4* wb = reinterpret_cast<const u32x4*>(a.wb);
+    u32x4 wbr[C::KSB][C::MTB];
+#pragma unroll
+    for (int ks = 0; ks < C::KSB; ++ks)
+#pragma unroll
+        for (int mt = 0; mt < C::MTB; ++mt) wbr[ks][mt] = wb[(ks * C::MTB + mt) * 64 + lane];
+
+    struct Tile {
+        int b, ty0, tx0;
+    };
+    auto tile_of = [&](int v) {
+        const int item = xcd_order(v, a.nwg), tile = item % a.tiles;
+        return Tile{item / a.tiles, (tile / a.tiles_x) * C::TH, (tile % a.tiles_x) * C::TW};
+    };
+
+    // Input unit of this thread (tid < XUNITS): STG 2 (yi, sg, g) = source
+    // channels 2g, 2g + 1, rows 2iy, 2iy + 1, 32 bytes each; STG 1 (yi, sg,
+    // c8) = 8 channels x 16 bytes. Either way 8 loads.
+    const int uyi = tid % C::IH_T, usg = (tid / C::IH_T) % C::NSEG, ug = tid / (C::IH_T * C::NSEG);
+    // r unit of this lane (lane < 32): 8 channels x 8 pixels of this wave's row.
+    const int rc8 = lane % 8, rpx = (lane / 8) * 8;
+    u32x4 vin[8], rv[8];
+    auto fetch = [&](const Tile& t) {
+        if (tid < XUNITS) {
+            const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<std::uint16_t*>(a.x + static_cast<size_t>(t.b) * csrc * (plane_src / 2)), 0,
+                static_cast<int>(csrc * plane_src), kRawBufferFlags);
+            const int ix0 = t.tx0 - 1, xa = ix0 - (((ix0 % 8) + 8) % 8);
+            const int iy = t.ty0 - 1 + uyi, ix = xa + usg * 8;
+            const bool ok = iy >= 0 && iy < a.h && ix >= 0 && ix < a.w;
+            if constexpr (C::STG == 2) {
+                const std::uint32_t base = static_cast<std::uint32_t>(2 * iy * sw + 2 * ix) * 2u;
+#pragma unroll
+                for (int ql = 0; ql < 2; ++ql) {
+                    // Source channels past the input (the zero padding of the
+                    // last chunk) are not fetched at all.
+                    const bool real = 2 * ug + ql < csrc;
+#pragma unroll
+                    for (int dy = 0; dy < 2; ++dy)
+#pragma unroll
+                        for (int hh = 0; hh < 2; ++hh) {
+                            const std::uint32_t off = ok ? base + static_cast<std::uint32_t>(2 * ug + ql) * plane_src +
+                                                               static_cast<std::uint32_t>(dy * sw * 2 + hh * 16)
+                                                         : kOutOfRange;
+                            vin[(ql * 2 + dy) * 2 + hh] =
+                                real ? __builtin_amdgcn_raw_buffer_load_b128(rx, static_cast<int>(off), 0, 0) : u32x4{0u, 0u, 0u, 0u};
+                        }
+                }
+            } else {
+                const std::uint32_t base =
+                    ok ? static_cast<std::uint32_t>(iy * a.w + ix) * 2u + static_cast<std::uint32_t>(ug * 8) * hw2 : kOutOfRange;
+#pragma unroll
+                for (int k = 0; k < 8; ++k)
+                    vin[k] = __builtin_amdgcn_raw_buffer_load_b128(rx, static_cast<int>(ok ? base + k * hw2 : kOutOfRange), 0, 0);
+            }
+        }
+        if (lane < 32) {
+            const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
+                const_cast<std::uint16_t*>(a.r + static_cast<size_t>(t.b) * C::CR * hw), 0, static_cast<int>(C::CR * hw2),
+                kRawBufferFlags);
+            const int oy = t.ty0 + wave, ox = t.tx0 + rpx;
+            const bool ok = oy < a.h && ox < a.w;
+            const std::uint32_t base = (static_cast<std::uint32_t>(rc8 * 8) * hw + static_cast<std::uint32_t>(oy * a.w + ox)) * 2u;
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                rv[k] = __builtin_amdgcn_raw_buffer_load_b128(rr, static_cast<int>(ok ? base + k * hw2 : kOutOfRange), 0, 0);
+        }
+    };
+
+    int v = static_cast<int>(blockIdx.x);
+    if (v < a.nwg) fetch(tile_of(v));
+    for (; v < a.nwg; v += G) {
+        const Tile t = tile_of(v);
+        // The previous tile's phase A has finished reading the halo tile
+        // (and, the first time, the resident 3x3 weights are in place).
+        __syncthreads();
+        if (tid < XUNITS) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                u32x4 q;
+                if constexpr (C::STG == 2) {
+                    // Dword j%4 of source half j/4 is the (dx = 0, 1) pair of staged pixel j.
+                    const int hh = j >> 2, wd = j & 3;
+                    q = u32x4{vin[(0 * 2 + 0) * 2 + hh][wd], vin[(0 * 2 + 1) * 2 + hh][wd], vin[(1 * 2 + 0) * 2 + hh][wd],
+                              vin[(1 * 2 + 1) * 2 + hh][wd]};
+                } else {
+                    const bool up = j & 1;
+                    const int wd = j >> 1;
+                    q = u32x4{pack_half(vin[0][wd], vin[1][wd], up), pack_half(vin[2][wd], vin[3][wd], up),
+                              pack_half(vin[4][wd], vin[5][wd], up), pack_half(vin[6][wd], vin[7][wd], up)};
+                }
+                *reinterpret_cast<u32x4*>(&in_s[C::at(uyi, usg * 8 + j) + ug * 8]) = q;
+            }
+        }
+        if (lane < 32) {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const bool up = j & 1;
+                const int wd = j >> 1;
+                const u32x4 q = {pack_half(rv[0][wd], rv[1][wd], up), pack_half(rv[2][wd], rv[3][wd], up),
+                                 pack_half(rv[4][wd], rv[5][wd], up), pack_half(rv[6][wd], rv[7][wd], up)};
+                *reinterpret_cast<u32x4*>(&ps[(wave * 32 + rpx + j) * C::PS + C::OCA + rc8 * 8]) = q;
+            }
+        }
+        __syncthreads();
+        if (v + G < a.nwg) fetch(tile_of(v + G));
+
+        // ---- phase A: 3x3 conv, BM = 64 ----
+        floatx16 acc[C::MTA];
+#pragma unroll
+        for (int mt = 0; mt < C::MTA; ++mt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const floatx4 bv = *reinterpret_cast<const floatx4*>(a.ba + mt * 32 + 8 * j + hsel);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[mt][4 * j + i] = bv[i];
+            }
+        const int ix0 = t.tx0 - 1, col_off = ix0 - (ix0 - (((ix0 % 8) + 8) % 8));
+        const int pxi = (lane & 31) + col_off;
+#pragma unroll
+        for (int tap = 0; tap < 9; ++tap) {
+            const int ky = tap / 3, kx = tap % 3;
+            const half8 bv = *reinterpret_cast<const half8*>(&in_s[C::at(wave + ky, pxi + kx) + koff]);
+#pragma unroll
+            for (int mt = 0; mt < C::MTA; ++mt) {
+                const half8 av = *reinterpret_cast<const half8*>(&wa_s[((tap * C::MTA + mt) * 64 + lane) * 8]);
+                acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, acc[mt], 0, 0, 0);
+            }
+        }
+
+        // ---- t into this wave's P rows: rounded, activated, 4 channels per write ----
+        const int p = wave * 32 + (lane & 31);
+#pragma unroll
+        for (int mt = 0; mt < C::MTA; ++mt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const std::uint32_t lo = epi_pair<EA>(acc[mt][4 * j], acc[mt][4 * j + 1], a.alpha_a);
+                const std::uint32_t hi = epi_pair<EA>(acc[mt][4 * j + 2], acc[mt][4 * j + 3], a.alpha_a);
+                *reinterpret_cast<u32x2*>(&ps[p * C::PS + mt * 32 + 8 * j + hsel]) = u32x2{lo, hi};
+            }
+
+        // ---- phase B: 1x1 over [t ; r] of this wave's rows, transposed:
+        // lane l accumulates output channel mt*32 + l%32 for pixels
+        // 8j + 4*(l/32) + i of the row ----
+        floatx16 acc2[C::MTB];
+#pragma unroll
+        for (int mt = 0; mt < C::MTB; ++mt) {
+            const float bv = a.bb[mt * 32 + (lane & 31)];
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc2[mt][r] = bv;
+        }
+#pragma unroll
+        for (int ks = 0; ks < C::KSB; ++ks) {
+            const half8 pv = *reinterpret_cast<const half8*>(&ps[p * C::PS + ks * 16 + koff]);
+#pragma unroll
+            for (int mt = 0; mt < C::MTB; ++mt)
+                acc2[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(pv, __builtin_bit_cast(half8, wbr[ks][mt]), acc2[mt], 0, 0, 0);
+        }
+
+        // ---- out: [channel][pixel] tile in this wave's P rows (the last
+        // reads of them are above, in this wave), 16-byte NCHW rows ----
+        std::uint16_t* const stg = ps + wave * 32 * C::PS;
+#pragma unroll
+        for (int mt = 0; mt < C::MTB; ++mt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const std::uint32_t lo = epi_pair<EB>(acc2[mt][4 * j], acc2[mt][4 * j + 1], a.alpha_b);
+                const std::uint32_t hi = epi_pair<EB>(acc2[mt][4 * j + 2], acc2[mt][4 * j + 3], a.alpha_b);
+                *reinterpret_cast<u32x2*>(&stg[(mt * 32 + (lane & 31)) * kStgRow + 8 * j + hsel]) = u32x2{lo, hi};
+            }
+        const int oy = t.ty0 + wave;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int e = lane + 64 * k, oc = e >> 2, px = (e & 3) * 8;
+            const u32x4 hv = *reinterpret_cast<const u32x4*>(&stg[oc * kStgRow + px]);
+            if (oy < a.h && t.tx0 + px < a.w)
+                *reinterpret_cast<u32x4*>(a.y + (static_cast<size_t>(t.b) * C::OCB + oc) * hw + static_cast<size_t>(oy) * a.w +
+                                          t.tx0 + px) = hv;
+        }
+    }
+}
+
+template <class C, int EA, int EB>
+void launch_pair_stream_epi(const PairArgs& a, hipStream_t s)
+{
+    // Two workgroups per CU (the LDS budget), a multiple of the 8 XCDs.
+    int g = 2 * cu_count();
+    if (g > a.nwg) g = a.nwg;
+    if (g >= 8) g -= g % 8;
+    hipLaunchKernelGGL((conv_pair_stream_kernel<C, EA, EB>), dim3(static_cast<unsigned>(g)), dim3(C::kThreads), 0, s, a);
+}
+
+template <class C, int EA>
+void launch_pair_stream_b(const PairArgs& a, hipStream_t s)
+{
+    switch (epi_mode(a.epi_b == MLVC_EPI_LEAKY_RELU, a.alpha_b)) {
+    case 0: launch_pair_stream_epi<C, EA, 0>(a, s); break;
+    case 1: launch_pair_stream_epi<C, EA, 1>(a, s); break;
+    default: launch_pair_stream_epi<C, EA, 2>(a, s); break;
+    }
+}
+
+template <class C>
+void launch_pair_stream(const PairArgs& a, hipStream_t s)
+{
+    switch (epi_mode(a.epi_a == MLVC_EPI_LEAKY_RELU, a.alpha_a)) {
+    case 0: launch_pair_stream_b<C, 0>(a, s); break;
+    case 1: launch_pair_stream_b<C, 1>(a, s); break;
+    default: launch_pair_stream_b<C, 2>(a, s); break;
+    }
+}
+
 template <class C>
 void launch_pair(const PairArgs& a, hipStream_t s)
 {
@@ -431,10 +689,16 @@ int mlvc_hip_convpair_launch(const mlvc_hip_convpair_desc* d, mlvc_hip_stream s)
         const long long nwg = static_cast<long long>(a.tiles) * d->n;
         if (nwg > 0x7FFFFFFF) throw std::runtime_error("convpair: grid too large");
         a.nwg = static_cast<int>(nwg);
-        if (d->in_s2d_block == 2)
+        if (a.nchunks == 1) {
+            if (d->in_s2d_block == 2)
+                launch_pair_stream<PairCfg<kPairTH, kPairTW, 2>>(a, to_stream(s));
+            else
+                launch_pair_stream<PairCfg<kPairTH, kPairTW, 1>>(a, to_stream(s));
+        } else if (d->in_s2d_block == 2) {
             launch_pair<PairCfg<kPairTH, kPairTW, 2>>(a, to_stream(s));
-        else
+        } else {
             launch_pair<PairCfg<kPairTH, kPairTW, 1>>(a, to_stream(s));
+        }
         check(hipGetLastError(), "convpair launch");
     });
 }

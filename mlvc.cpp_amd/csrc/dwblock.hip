@@ -40,7 +40,10 @@ namespace {
 
 constexpr int kTH = 4, kTW = 8, kP = kTH * kTW;  // 32 pixels per workgroup
 constexpr int kYS = kP + 8;                       // y staging row stride (halves)
-constexpr int kRing = 16;                         // weight fragments in flight per wave
+#ifndef MLVC_DW_RING
+#define MLVC_DW_RING 16
+#endif
+constexpr int kRing = MLVC_DW_RING;               // weight fragments in flight per wave
 constexpr int kRawBufferFlags = 0x00020000;       // raw buffer resource word 3 (gfx950)
 constexpr int kOutOfRange = 0x40000000;           // byte offset past every staged tensor (< 2^30 bytes)
 

@@ -141,19 +141,24 @@ def test_standalone_layout_and_eltwise(tmp_path, rng):
         assert (gg == ww).all(), f"output {i} differs"  # one rounding per op on both sides
 
 
-@pytest.mark.parametrize("s2d,ica,h,w,acts", [(2, 12, 14, 40, (True, True)), (0, 16, 9, 24, (True, False)),
-                                              (0, 40, 6, 16, (False, True)), (2, 24, 5, 8, (True, True))])
-def test_fused_conv_pair(tmp_path, monkeypatch, s2d, ica, h, w, acts):
+# ica <= 16 runs the streaming kernel (persistent grid of two workgroups per
+# CU): 150x488 has 608 tiles of 4x32, more than the grid, with ragged last
+# rows and columns; n = 2 walks tiles of two images.
+@pytest.mark.parametrize("s2d,ica,h,w,acts,n", [(2, 12, 14, 40, (True, True), 1), (0, 16, 9, 24, (True, False), 1),
+                                                (0, 40, 6, 16, (False, True), 1), (2, 24, 5, 8, (True, True), 1),
+                                                (2, 12, 150, 488, (True, True), 1), (2, 12, 10, 72, (True, False), 2),
+                                                (0, 8, 7, 40, (False, True), 2)])
+def test_fused_conv_pair(tmp_path, monkeypatch, s2d, ica, h, w, acts, n):
     """3x3 conv [+LeakyReLU] -> CONCAT(t, r) -> 1x1 [+LeakyReLU] runs as one
     launch, matches the oracle and equals the unfused schedule bit for bit."""
     rng = np.random.default_rng(ica + h)
     g = graphs.Graph()
     if s2d:
-        x0 = g.input("x", [1, ica // 4, 2 * h, 2 * w])
+        x0 = g.input("x", [n, ica // 4, 2 * h, 2 * w])
         x = g.pixel("SPACE_TO_DEPTH", "xs", x0, 2)
     else:
-        x = g.input("x", [1, ica, h, w])
-    r = g.input("r", [1, 64, h, w])
+        x = g.input("x", [n, ica, h, w])
+    r = g.input("r", [n, 64, h, w])
     wa = g.weight_fp16("wa", rng.normal(0, 1 / np.sqrt(9 * ica), (64, ica, 3, 3)))
     ba = g.weight_fp16("ba", rng.normal(0, 0.1, (64,)))
     t = g.conv("t", x, wa, ba, (1, 1), (1, 1, 1, 1))
@@ -167,8 +172,8 @@ def test_fused_conv_pair(tmp_path, monkeypatch, s2d, ica, h, w, acts):
         y = g.leaky_relu("ya", y, 0.2)
     g.output(y)
     g.write(tmp_path, "m")
-    ins = [graphs.half(rng.uniform(-1, 1, s)) for s in ([1, ica // 4, 2 * h, 2 * w] if s2d else [1, ica, h, w],
-                                                        [1, 64, h, w])]
+    ins = [graphs.half(rng.uniform(-1, 1, s)) for s in ([n, ica // 4, 2 * h, 2 * w] if s2d else [n, ica, h, w],
+                                                        [n, 64, h, w])]
     want = mlvc_oracle.OraclePlan(tmp_path, "m").run(ins)[0]
     fused = mlvc_hip.Backend(tmp_path, "hip")
     fused.load("m")
@@ -176,7 +181,7 @@ def test_fused_conv_pair(tmp_path, monkeypatch, s2d, ica, h, w, acts):
     assert len(kinds) == 1 and kinds[0].startswith("convpair"), kinds
     got = fused.run(ins)[0]
     fused.close()
-    assert_parity(got, want, f"conv pair s2d={s2d} ica={ica} {h}x{w}")
+    assert_parity(got, want, f"conv pair s2d={s2d} ica={ica} {n}x{h}x{w}")
     monkeypatch.setenv("MLVC_HIP_DISABLE_FUSION", "1")
     plain = mlvc_hip.Backend(tmp_path, "hip")
     plain.load("m")
