@@ -88,7 +88,7 @@ __device__ __forceinline__ void lds_barrier()
 __device__ __forceinline__ float lo_h(std::uint32_t v) { return h2f(static_cast<std::uint16_t>(v & 0xFFFFu)); }
 __device__ __forceinline__ float hi_h(std::uint32_t v) { return h2f(static_cast<std::uint16_t>(v >> 16)); }
 
-template <int C, int E>
+template <int C, int E, int MODE>
 __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArgs a)
 {
     using B = BlockCfg<C, E>;
@@ -116,21 +116,6 @@ __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArg
         f -= NF1;
         return w2[((wave * MT2 + f % MT2) * KS2 + f / MT2) * 64 + lane];
     };
-    u32x4 ring[kRing];
-#pragma unroll
-    for (int f = 0; f < kRing; ++f) ring[f] = f < NF ? frag(f) : u32x4{0u, 0u, 0u, 0u};
-
-    // Expand accumulators seeded with b1: lane holds rows 8j + hsel + (0..3).
-    floatx16 acc1[MT1];
-#pragma unroll
-    for (int m = 0; m < MT1; ++m)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const floatx4 bv = *reinterpret_cast<const floatx4*>(a.b1 + (wave * MT1 + m) * 32 + 8 * j + hsel);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc1[m][4 * j + i] = bv[i];
-        }
-
     // ---- 1. depthwise halo rows of channel c straight into registers ------
     // Thread (c, g): output rows g*ORT .. g*ORT + ORT - 1 of the tile, input
     // rows y0 + g*ORT - 1 .. + ORT. Per row: the dword holding columns
@@ -153,10 +138,35 @@ __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArg
         xm[r] = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
         xr[r] = __builtin_amdgcn_raw_buffer_load_b32(rx, off + 16, 0, 0);
     }
+    // Taps as separate 16-bit loads (one register each, nothing to unpack
+    // before the depthwise stage, so issuing them waits for nothing).
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<std::uint16_t*>(a.dw_w), 0, C * 9 * 2,
+                                                                        kRawBufferFlags);
     std::uint16_t wdw[9];
 #pragma unroll
-    for (int t = 0; t < 9; ++t) wdw[t] = a.dw_w[c * 9 + t];
+    for (int t = 0; t < 9; ++t) wdw[t] = __builtin_amdgcn_raw_buffer_load_b16(rw, (c * 9 + t) * 2, 0, 0);
     const float bdw = a.dw_b[c];
+    // The depthwise operands are requested first: loads complete in issue
+    // order for the wait counter, so the depthwise stage then waits for
+    // them only, and runs while the weight ring below is still in flight.
+    __builtin_amdgcn_sched_barrier(0);
+
+    // The weight ring, then the expand bias and the residual rows.
+    u32x4 ring[kRing];
+#pragma unroll
+    for (int f = 0; f < kRing; ++f) ring[f] = f < NF ? frag(f) : u32x4{0u, 0u, 0u, 0u};
+
+    // Expand accumulators seeded with b1: lane holds rows 8j + hsel + (0..3).
+    floatx16 acc1[MT1];
+#pragma unroll
+    for (int m = 0; m < MT1; ++m)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const floatx4 bv = *reinterpret_cast<const floatx4*>(a.b1 + (wave * MT1 + m) * 32 + 8 * j + hsel);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc1[m][4 * j + i] = bv[i];
+        }
+
     // Residual rows for the output stage, loaded ahead of use.
     u32x4 res[RV];
 #pragma unroll
@@ -232,15 +242,14 @@ __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArg
             for (int i = 0; i < 4; ++i) acc2[m][4 * j + i] = bv[i];
         }
     {
-        const bool max_form = a.alpha >= 0.0f && a.alpha <= 1.0f;
         typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 #pragma unroll
         for (int m = 0; m < MT1; ++m) {
             const int mt = wave * MT1 + m;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const std::uint32_t lo = leaky_pair(acc1[m][4 * j], acc1[m][4 * j + 1], a.alpha, max_form);
-                const std::uint32_t hi = leaky_pair(acc1[m][4 * j + 2], acc1[m][4 * j + 3], a.alpha, max_form);
+                const std::uint32_t lo = epi_pair<MODE>(acc1[m][4 * j], acc1[m][4 * j + 1], a.alpha);
+                const std::uint32_t hi = epi_pair<MODE>(acc1[m][4 * j + 2], acc1[m][4 * j + 3], a.alpha);
                 *reinterpret_cast<u32x2*>(&es[pl * EST + mt * 32 + 8 * j + hsel]) = u32x2{lo, hi};
             }
         }
@@ -291,7 +300,11 @@ __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArg
 template <int C, int E>
 void launch(const DwBlockArgs& a, dim3 grid, hipStream_t s)
 {
-    hipLaunchKernelGGL((dwblock_kernel<C, E>), grid, dim3(BlockCfg<C, E>::T), 0, s, a);
+    // LeakyReLU form fixed at compile time (max form for 0 <= alpha <= 1).
+    if (epi_mode(1, a.alpha) == 1)
+        hipLaunchKernelGGL((dwblock_kernel<C, E, 1>), grid, dim3(BlockCfg<C, E>::T), 0, s, a);
+    else
+        hipLaunchKernelGGL((dwblock_kernel<C, E, 2>), grid, dim3(BlockCfg<C, E>::T), 0, s, a);
 }
 
 }  // namespace
