@@ -20,8 +20,8 @@
 //   for every pixel range.
 //
 // Both directions are HBM-bound byte/half streams: one thread converts 8
-// model columns (frame -> model) or a 2x4 luma block with its 2 U and 2 V
-// samples (model -> frame), with 2- to 16-byte accesses where the shapes
+// model columns (frame -> model) or a 2x16 luma block with its 8 U and 8 V
+// samples (model -> frame), with 8- and 16-byte accesses where the shapes
 // keep them aligned and a per-element path otherwise.
 
 #include "common.hpp"
@@ -121,7 +121,7 @@ __global__ __launch_bounds__(kYuvThreads) void yuv_to_model_rotated_kernel(const
 }
 
 constexpr int kToYuvThreads = 128;
-constexpr int kChromaPerThread = 2;  // 2x4 luma pixels, 2 U and 2 V samples per thread
+constexpr int kChromaPerThread = 8;  // 2x16 luma pixels, 8 U and 8 V samples per thread
 
 // value / pixel_range as the CPU backend computes it; x / 1 is exact, so the
 // unit-range instantiation has no IEEE division.
@@ -134,10 +134,12 @@ __device__ __forceinline__ float scaled(std::uint16_t h, float range)
         return h2f(h) / range;
 }
 
-// One thread: chroma samples [2t, 2t + 2) of chroma row uy, i.e. luma rows
-// 2uy, 2uy + 1 and columns [4t, 4t + 4) (grid x: column groups, y: chroma
-// rows).
-template <bool UNIT>
+// One thread: chroma samples [8t, 8t + 8) of chroma row uy, i.e. luma rows
+// 2uy, 2uy + 1 and columns [16t, 16t + 16) (grid x: column groups, y:
+// chroma rows). VEC (the launch checks the alignment): every row segment is
+// two 16-byte loads, the luma rows leave as 16-byte stores and U / V as
+// 8-byte stores; otherwise element by element.
+template <bool UNIT, bool VEC>
 __global__ __launch_bounds__(kToYuvThreads) void model_to_yuv_kernel(const std::uint16_t* __restrict__ x,
                                                                      std::uint8_t* __restrict__ yuv, int w, int h,
                                                                      int mw, int mh, int pad_left, int pad_top,
@@ -156,24 +158,27 @@ __global__ __launch_bounds__(kToYuvThreads) void model_to_yuv_kernel(const std::
     const size_t r0 = static_cast<size_t>(pad_top + 2 * uy) * mw + col0;
     const size_t r1 = r0 + mw;
     float s[3][2][LPT];
-    // One branch around all six row loads, so they are all in flight before
-    // the first wait (a branch per load would wait after each).
-    if (n == CPT && (col0 % LPT) == 0 && (mw % LPT) == 0) {
-        uint2 q[3][2];
+    if (VEC && n == CPT) {
+        // All twelve loads are issued before the first use.
+        u32x4 q[3][2][2];
 #pragma unroll
         for (int c = 0; c < 3; ++c)
 #pragma unroll
             for (int r = 0; r < 2; ++r)
-                q[c][r] = *reinterpret_cast<const uint2*>(x + static_cast<size_t>(c) * plane + (r ? r1 : r0));
+#pragma unroll
+                for (int k = 0; k < 2; ++k)
+                    q[c][r][k] = *reinterpret_cast<const u32x4*>(x + static_cast<size_t>(c) * plane + (r ? r1 : r0) + 8 * k);
 #pragma unroll
         for (int c = 0; c < 3; ++c)
 #pragma unroll
-            for (int r = 0; r < 2; ++r) {
-                s[c][r][0] = scaled<UNIT>(static_cast<std::uint16_t>(q[c][r].x & 0xFFFFu), range);
-                s[c][r][1] = scaled<UNIT>(static_cast<std::uint16_t>(q[c][r].x >> 16), range);
-                s[c][r][2] = scaled<UNIT>(static_cast<std::uint16_t>(q[c][r].y & 0xFFFFu), range);
-                s[c][r][3] = scaled<UNIT>(static_cast<std::uint16_t>(q[c][r].y >> 16), range);
-            }
+            for (int r = 0; r < 2; ++r)
+#pragma unroll
+                for (int k = 0; k < 2; ++k)
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) {
+                        s[c][r][8 * k + 2 * d] = scaled<UNIT>(static_cast<std::uint16_t>(q[c][r][k][d] & 0xFFFFu), range);
+                        s[c][r][8 * k + 2 * d + 1] = scaled<UNIT>(static_cast<std::uint16_t>(q[c][r][k][d] >> 16), range);
+                    }
     } else {
 #pragma unroll
         for (int c = 0; c < 3; ++c)
@@ -199,13 +204,18 @@ __global__ __launch_bounds__(kToYuvThreads) void model_to_yuv_kernel(const std::
     std::uint8_t* yo = yuv + static_cast<size_t>(2 * uy) * w + 2 * ux0;
     std::uint8_t* uo = yuv + ysz + static_cast<size_t>(uy) * uw + ux0;
     std::uint8_t* vo = uo + uvsz;
-    if (n == CPT && (w % LPT) == 0) {
+    auto pack4 = [](const std::uint8_t* b) {
+        return static_cast<std::uint32_t>(b[0]) | (static_cast<std::uint32_t>(b[1]) << 8) |
+               (static_cast<std::uint32_t>(b[2]) << 16) | (static_cast<std::uint32_t>(b[3]) << 24);
+    };
+    if (VEC && n == CPT) {
 #pragma unroll
         for (int r = 0; r < 2; ++r)
-            *reinterpret_cast<std::uint32_t*>(yo + static_cast<size_t>(r) * w) =
-                yb[r][0] | (yb[r][1] << 8) | (yb[r][2] << 16) | (static_cast<std::uint32_t>(yb[r][3]) << 24);
-        *reinterpret_cast<std::uint16_t*>(uo) = static_cast<std::uint16_t>(ub[0] | (ub[1] << 8));
-        *reinterpret_cast<std::uint16_t*>(vo) = static_cast<std::uint16_t>(vb[0] | (vb[1] << 8));
+            *reinterpret_cast<u32x4*>(yo + static_cast<size_t>(r) * w) =
+                u32x4{pack4(&yb[r][0]), pack4(&yb[r][4]), pack4(&yb[r][8]), pack4(&yb[r][12])};
+        typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+        *reinterpret_cast<u32x2*>(uo) = u32x2{pack4(&ub[0]), pack4(&ub[4])};
+        *reinterpret_cast<u32x2*>(vo) = u32x2{pack4(&vb[0]), pack4(&vb[4])};
     } else {
         for (int k = 0; k < n; ++k) {
             yo[2 * k] = yb[0][2 * k];
@@ -311,12 +321,20 @@ int mlvc_hip_model_to_yuv420(const void* x, uint8_t* yuv, int w, int h, int mw, 
         } else {
             const int groups = (w / 2 + kChromaPerThread - 1) / kChromaPerThread;
             const dim3 grid((groups + kToYuvThreads - 1) / kToYuvThreads, h / 2);
+            // 16-byte model row segments (base, plane, row and active-area
+            // origin on 8 halves) and 16-byte luma / 8-byte chroma stores
+            // (base on 16 bytes, w on 16 columns, so Y, U and V rows and
+            // plane starts keep that alignment).
+            const bool vec = (reinterpret_cast<std::uintptr_t>(x) & 15u) == 0 && (reinterpret_cast<std::uintptr_t>(yuv) & 15u) == 0 &&
+                             mw % 8 == 0 && pad_left % 8 == 0 && w % 16 == 0;
+            auto go = [&](auto kernel) {
+                hipLaunchKernelGGL(kernel, grid, dim3(kToYuvThreads), 0, to_stream(s), xi, yuv, w, h, mw, mh, pad_left,
+                                   pad_top, pixel_range);
+            };
             if (pixel_range == 1.0F)
-                hipLaunchKernelGGL(model_to_yuv_kernel<true>, grid, dim3(kToYuvThreads), 0, to_stream(s), xi, yuv, w, h,
-                                   mw, mh, pad_left, pad_top, pixel_range);
+                vec ? go(model_to_yuv_kernel<true, true>) : go(model_to_yuv_kernel<true, false>);
             else
-                hipLaunchKernelGGL(model_to_yuv_kernel<false>, grid, dim3(kToYuvThreads), 0, to_stream(s), xi, yuv, w, h,
-                                   mw, mh, pad_left, pad_top, pixel_range);
+                vec ? go(model_to_yuv_kernel<false, true>) : go(model_to_yuv_kernel<false, false>);
         }
         check(hipGetLastError(), "codec I/O kernel launch");
     });
