@@ -248,6 +248,13 @@ int mlvc_hip_gather(const void* data, const void* indices, int indices_int64, si
 /* x [n, 2G, hw] -> y [n, G, hw] = fp16(fp16(clamp(gate, lo, hi)) * linear)
  * (reglu_nhwc, kernels_scalar.cpp:304-322). */
 int mlvc_hip_reglu(const void* x, void* y, int n, int gate_channels, size_t hw, float lo, float hi, mlvc_hip_stream s);
+/* Device tables used by the kernels below (the feature update's gate
+ * table), computed once per device on stream s, which is waited for. No
+ * counterpart in the reference (its kernels compute the gate directly).
+ * Launchers prepare them on first use, except under graph capture, where
+ * they fail: a caller that captures calls this first. */
+int mlvc_hip_prepare_tables(mlvc_hip_stream s);
+
 /* Recurrent feature update (feature_update[_outputs]_nhwc,
  * kernels_scalar.cpp:324-405): x [n, 3C, hw], history [n, C, hw], scale [C]
  * -> feature [n, 2C, hw] = scaled | blended; scaled / blended [n, C, hw]

@@ -161,6 +161,9 @@ public:
         allocate_io();
         upload_parameters();
         if (tuning_enabled()) tune();
+        // Kernel tables are computed before capture (nothing synchronous
+        // may run while the stream is capturing).
+        hip_check(mlvc_hip_prepare_tables(stream_), "device tables");
         capture();
         initialized_ = bindings_.empty();
     }

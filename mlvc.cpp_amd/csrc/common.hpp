@@ -51,6 +51,11 @@ __device__ __forceinline__ int xcd_order(int id, int n)
 
 inline hipStream_t to_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
+namespace conv {
+// Compute units of the current device (queried once).
+int cu_count();
+}  // namespace conv
+
 __device__ __forceinline__ float h2f(std::uint16_t h)
 {
     return static_cast<float>(__builtin_bit_cast(_Float16, h));

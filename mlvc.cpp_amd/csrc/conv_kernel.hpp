@@ -44,9 +44,6 @@ constexpr int kRawBufferFlags = 0x00020000;
 // adding up to 7 channel planes; raw buffer loads there return zeros.
 constexpr std::uint32_t kOutOfRange = 0x80000000u;
 
-// Compute units of the current device (queried once).
-int cu_count();
-
 struct ConvArgs {
     const std::uint16_t* x;
     const std::uint16_t* x2;

@@ -26,6 +26,7 @@
 #include "mlvc_hip_device.h"
 
 #include <algorithm>
+#include <mutex>
 
 #pragma clang fp contract(off)
 
@@ -308,14 +309,45 @@ __global__ __launch_bounds__(kBlock) void reglu_kernel(const u16* __restrict__ x
 //   scaled = fp16(fp16(sc * blended) * scale).
 // feature [N, 2C, HW] = scaled | blended; scaled_out / blended_out [N, C, HW]
 // are written when non-null.
-template <bool VEC>
-__global__ __launch_bounds__(kBlock) void feature_kernel(const u16* __restrict__ x, const u16* __restrict__ hist,
-                                                         const u16* __restrict__ scale, u16* __restrict__ feature,
-                                                         u16* __restrict__ scaled_out, u16* __restrict__ blended_out, int n, int ch,
-                                                         size_t hw)
+//
+// fp16(sigmoid(v)) of an FP16 gate v is a function of 16 bits: it is read
+// from a table computed once per device by the same device code
+// (sigmoid_lut_kernel), held in LDS, so the two gates per element cost a
+// table read instead of a polynomial exponential and a division. The table
+// covers v in [0, 16) (bits 0x0000-0x4BFF) and (-18, -0] (0x8000-0xCC7F);
+// other gates (rare: |v| large, NaN) take the arithmetic path.
+constexpr int kSigPos = 0x4C00, kSigNeg = 0x4C80, kSigLutN = kSigPos + kSigNeg;
+__device__ __attribute__((aligned(16))) u16 g_sigmoid_lut[kSigLutN];
+
+__global__ __launch_bounds__(kBlock) void sigmoid_lut_kernel()
 {
+    const int i = blockIdx.x * kBlock + threadIdx.x;
+    if (i >= kSigLutN) return;
+    const u16 h = static_cast<u16>(i < kSigPos ? i : 0x8000 + (i - kSigPos));
+    g_sigmoid_lut[i] = rnd(sigmoid(h2f(h)));
+}
+
+__device__ __forceinline__ float gate(const u16* lut, u16 h)
+{
+    const int idx = h < kSigPos ? h : (h >= 0x8000 && h < 0x8000 + kSigNeg ? kSigPos + (h - 0x8000) : -1);
+    return idx >= 0 ? h2f(lut[idx]) : r16(sigmoid(h2f(h)));
+}
+
+constexpr int kFeatureBlock = 1024;
+
+template <bool VEC>
+__global__ __launch_bounds__(kFeatureBlock) void feature_kernel(const u16* __restrict__ x, const u16* __restrict__ hist,
+                                                                const u16* __restrict__ scale, u16* __restrict__ feature,
+                                                                u16* __restrict__ scaled_out, u16* __restrict__ blended_out, int n,
+                                                                int ch, size_t hw)
+{
+    __shared__ __attribute__((aligned(16))) u16 lut[kSigLutN];
+    for (int i = threadIdx.x; i < kSigLutN / 8; i += kFeatureBlock)
+        reinterpret_cast<uint4*>(lut)[i] = reinterpret_cast<const uint4*>(g_sigmoid_lut)[i];
+    __syncthreads();
     const size_t p8 = (hw + 7) / 8, total = static_cast<size_t>(n) * ch * p8;
-    for (size_t t = blockIdx.x * static_cast<size_t>(kBlock) + threadIdx.x; t < total; t += static_cast<size_t>(gridDim.x) * kBlock) {
+    for (size_t t = blockIdx.x * static_cast<size_t>(kFeatureBlock) + threadIdx.x; t < total;
+         t += static_cast<size_t>(gridDim.x) * kFeatureBlock) {
         const size_t p0 = (t % p8) * 8, plane = t / p8, c = plane % ch, b = plane / ch;
         const int cnt = static_cast<int>(std::min<size_t>(8, hw - p0));
         u16 va[8], vb[8], vc[8], vh[8], so[8], bo[8];
@@ -326,8 +358,8 @@ __global__ __launch_bounds__(kBlock) void feature_kernel(const u16* __restrict__
         const float s = h2f(scale[c]);
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-            const float sb = r16(sigmoid(h2f(vb[j])));
-            const float sc = r16(sigmoid(h2f(vc[j])));
+            const float sb = gate(lut, vb[j]);
+            const float sc = gate(lut, vc[j]);
             const float wb = r16(sb * h2f(vh[j]));
             const float inv = r16(1.0f - sb);
             const float wa = r16(inv * h2f(va[j]));
@@ -475,12 +507,39 @@ void launch(K kernel, size_t work, hipStream_t s, A... args)
     check(hipGetLastError(), "kernel launch");
 }
 
+// Device tables (the gate table of the feature update), computed once per
+// device on stream s and waited for. Not under graph capture: a caller that
+// captures prepares them first (mlvc_hip_prepare_tables).
+void prepare_tables(hipStream_t s)
+{
+    static std::mutex mu;
+    static bool ready[64] = {};
+    int dev = 0;
+    check(hipGetDevice(&dev), "hipGetDevice");
+    if (dev < 0 || dev >= 64) throw std::runtime_error("device tables: device index out of range");
+    std::lock_guard<std::mutex> lock(mu);
+    if (ready[dev]) return;
+    hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+    check(hipStreamIsCapturing(s, &status), "hipStreamIsCapturing");
+    if (status != hipStreamCaptureStatusNone)
+        throw std::runtime_error("device tables are not prepared: call mlvc_hip_prepare_tables before graph capture");
+    hipLaunchKernelGGL(sigmoid_lut_kernel, dim3((kSigLutN + kBlock - 1) / kBlock), dim3(kBlock), 0, s);
+    check(hipGetLastError(), "table kernel launch");
+    check(hipStreamSynchronize(s), "table kernel");
+    ready[dev] = true;
+}
+
 }  // namespace
 }  // namespace mlvc_hip
 
 using namespace mlvc_hip;
 
 extern "C" {
+
+int mlvc_hip_prepare_tables(mlvc_hip_stream s)
+{
+    return guard([&] { prepare_tables(to_stream(s)); });
+}
 
 int mlvc_hip_unary(const void* x, void* y, size_t count, int op, float lo, float hi, mlvc_hip_stream s)
 {
@@ -636,8 +695,18 @@ int mlvc_hip_feature_update(const void* x, const void* history, const void* scal
         auto* pf = static_cast<u16*>(feature);
         auto* ps = static_cast<u16*>(scaled);
         auto* pb = static_cast<u16*>(blended);
-        if (vec) launch(feature_kernel<true>, work, to_stream(s), px, ph, pc, pf, ps, pb, n, channels, hw);
-        else launch(feature_kernel<false>, work, to_stream(s), px, ph, pc, pf, ps, pb, n, channels, hw);
+        prepare_tables(to_stream(s));
+        // Every block copies the gate table into LDS first: a grid of the
+        // blocks the device holds at once (two per CU) walks the work.
+        const unsigned grid = static_cast<unsigned>(
+            std::max<size_t>(1, std::min<size_t>((work + kFeatureBlock - 1) / kFeatureBlock, 2 * static_cast<size_t>(conv::cu_count()))));
+        if (vec)
+            hipLaunchKernelGGL(feature_kernel<true>, dim3(grid), dim3(kFeatureBlock), 0, to_stream(s), px, ph, pc, pf, ps, pb, n,
+                               channels, hw);
+        else
+            hipLaunchKernelGGL(feature_kernel<false>, dim3(grid), dim3(kFeatureBlock), 0, to_stream(s), px, ph, pc, pf, ps, pb, n,
+                               channels, hw);
+        check(hipGetLastError(), "feature_update launch");
     });
 }
 

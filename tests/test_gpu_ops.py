@@ -231,6 +231,26 @@ def test_feature_update(dev, ch, hw, outputs):
         assert np.array_equal(dev.get16(bl, (ch, hw)), from_nhwc(want[2], ch))
 
 
+def test_feature_update_every_gate(dev):
+    """Both gates of the feature update take every non-NaN FP16 value (the
+    kernel reads most of them from its table, the rest through the
+    arithmetic path), bit for bit against the oracle."""
+    ch, hw = 16, 4096
+    rng = np.random.default_rng(11)
+    allh = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    allh = np.where(np.isnan(allh.view(np.float16)), np.uint16(0), allh).astype(np.uint16)
+    x = np.concatenate([rand16(rng, (ch, hw), -4, 4), allh.reshape(ch, hw), rng.permutation(allh).reshape(ch, hw)])
+    hist = rand16(rng, (ch, hw), -2, 2)
+    scale = rand16(rng, ch, 0.5, 1.5)
+    want = O.Ops().feature_update(to_nhwc(x), to_nhwc(hist), scale, hw, ch, outputs=True)
+    feat = dev.alloc(2 * ch * hw * 2)
+    dev.check(dev.lib.mlvc_hip_feature_update(dev.put(x), dev.put(hist), dev.put(scale), feat, None, None, 1, ch, hw, None))
+    got, ref = dev.get16(feat, (2 * ch, hw)), from_nhwc(want[0], 2 * ch)
+    same = (got == ref) | (np.isnan(got.view(np.float16)) & np.isnan(ref.view(np.float16)))
+    bad = np.argwhere(~same)
+    assert bad.size == 0, f"{len(bad)} values differ, first at {bad[:4].tolist()}"
+
+
 @pytest.mark.parametrize("hw", [8 * 12, 5 * 7])
 @pytest.mark.parametrize("q", [16, 8])
 def test_quant_tails(dev, q, hw):
