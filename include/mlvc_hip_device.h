@@ -76,7 +76,14 @@ int mlvc_hip_graph_destroy(mlvc_hip_graph graph);
  *   out_d2s_block > 1: the output is written through DEPTH_TO_SPACE(block)
  *                      (CRD), y is [n, oc/b^2, oh*b, ow*b].
  */
-enum { MLVC_EPI_NONE = 0, MLVC_EPI_LEAKY_RELU = 1, MLVC_EPI_RESIDUAL_ADD = 2 };
+enum { MLVC_EPI_NONE = 0, MLVC_EPI_LEAKY_RELU = 1, MLVC_EPI_RESIDUAL_ADD = 2, MLVC_EPI_REGLU = 3 };
+/* MLVC_EPI_REGLU (the reference's 1x1 conv with a ReGLU epilogue,
+ * backends/cpu/src/fusion_matcher.cpp:258-302): the conv computes oc = 2G
+ * channels, rounded to FP16, and writes y [n, G, oh, ow] =
+ * fp16(fp16(clip(gate, clip_lo, clip_hi)) * linear). The weight and bias rows
+ * are given in blocks of 64: 32 gate rows g..g+31 followed by the 32 linear
+ * rows G+g..G+g+31 (g = 32 * block), so G must be a multiple of 32; no
+ * DEPTH_TO_SPACE output. */
 
 typedef struct mlvc_hip_conv_desc {
     int n, ic, ih, iw;                 /* conv input geometry (after fusion maps) */
@@ -90,6 +97,7 @@ typedef struct mlvc_hip_conv_desc {
     const float* bias;                 /* fp32 widening of the fp16 bias, length mlvc_hip_conv_bias_len */
     int epilogue;
     float alpha;
+    float clip_lo, clip_hi;            /* MLVC_EPI_REGLU bounds */
     const void* residual;              /* [n, oc, oh, ow] */
     void* y;
     int out_d2s_block;

@@ -1317,6 +1317,53 @@ private:
         pending_uploads_.push_back({b.ptr, std::move(braw)});
     }
 
+    // try_pointwise_reglu (fusion_matcher.cpp:258-302): a 1x1 stride-1
+    // unpadded conv whose output only feeds SLICE [0,G) and SLICE [G,2G)
+    // (nodes i+1, i+2) -> CLIP(gate) (i+3) -> MUL(clipped, linear) (i+4).
+    // Returns the MUL output, or 0. G is a multiple of 32 here (the kernel
+    // pairs 32 gate rows with 32 linear rows per 64-row block).
+    TensorId pointwise_reglu(const aot::Node& n, float& lo, float& hi) const
+    {
+        const auto& ns = nodes();
+        const std::size_t i = n.index;
+        if (i + 5 > ns.size() || n.conv().groups != 1) return 0;
+        const auto& a = n.conv();
+        const auto& ws = desc(n.inputs[1]).shape;
+        if (ws[2] != 1 || ws[3] != 1 || a.strides[0] != 1 || a.strides[1] != 1 || a.pads[0] || a.pads[1]) return 0;
+        const TensorId x = n.outputs[0];
+        if (!internal_only(x, 2) || !fp16_4d(x)) return 0;
+        const std::int64_t g = desc(x).shape[1] / 2;
+        if (desc(x).shape[1] % 2 || g % 32) return 0;
+        if (!channel_slice(ns[i + 1], x, 0, g) || !channel_slice(ns[i + 2], x, g, 2 * g)) return 0;
+        const TensorId gate = ns[i + 1].outputs[0], lin = ns[i + 2].outputs[0];
+        if (!internal_only(gate, 1) || !internal_only(lin, 1)) return 0;
+        if (!clip_constants(ns[i + 3], lo, hi) || ns[i + 3].inputs[0] != gate) return 0;
+        const TensorId clipped = ns[i + 3].outputs[0];
+        if (!internal_only(clipped, 1) || !pair(ns[i + 4], Op::MUL, clipped, lin)) return 0;
+        const auto& s = desc(x).shape;
+        const TensorId y = ns[i + 4].outputs[0];
+        if (!fp16_of(y, {s[0], g, s[2], s[3]})) return 0;
+        return y;
+    }
+
+    // Weight and bias rows of a ReGLU conv in the kernel's pairing order:
+    // 64-row blocks of 32 gate rows (g..g+31) then the matching linear rows.
+    static void reglu_row_order(Launch& L, int oc, std::size_t row_len)
+    {
+        const int g = oc / 2;
+        std::vector<std::uint16_t> w(L.w_oihw.size());
+        std::vector<float> b(L.bias_oc.size());
+        for (int r = 0; r < oc; ++r) {
+            const int blk = r / 64, k = r % 64;
+            const int src = k < 32 ? blk * 32 + k : g + blk * 32 + (k - 32);
+            std::copy_n(L.w_oihw.begin() + static_cast<std::ptrdiff_t>(src * row_len), row_len,
+                        w.begin() + static_cast<std::ptrdiff_t>(r * row_len));
+            b[static_cast<std::size_t>(r)] = L.bias_oc[static_cast<std::size_t>(src)];
+        }
+        L.w_oihw = std::move(w);
+        L.bias_oc = std::move(b);
+    }
+
     template <typename SingleFn>
     void lower_conv(Launch& L, const aot::Node& n, std::map<TensorId, std::size_t>& producer, const std::vector<bool>& folded,
                     std::vector<bool>& done, SingleFn internal_single, std::map<TensorId, std::size_t>& first_consumer,
@@ -1367,7 +1414,20 @@ private:
         }
         // Epilogue (fusion_matcher.cpp:352-411).
         TensorId out = n.outputs[0];
-        if (fuse && n.index + 1 < ns.size() && internal_single(out)) {
+        bool reglu = false;
+        if (fuse && !L.x2 && d.in_s2d_block <= 1) {
+            float lo = 0.0F, hi = 0.0F;
+            if (TensorId y = pointwise_reglu(n, lo, hi)) {
+                d.epilogue = MLVC_EPI_REGLU;
+                d.clip_lo = lo;
+                d.clip_hi = hi;
+                for (std::size_t k = n.index + 1; k < n.index + 5; ++k) done[k] = true;
+                out = y;
+                reglu = true;
+                tags += "+reglu";
+            }
+        }
+        if (!reglu && fuse && n.index + 1 < ns.size() && internal_single(out)) {
             const aot::Node& nx = ns[n.index + 1];
             if (nx.op == Op::LEAKY_RELU && nx.inputs[0] == out) {
                 d.epilogue = MLVC_EPI_LEAKY_RELU;
@@ -1387,7 +1447,7 @@ private:
             }
         }
         // Output side: a DEPTH_TO_SPACE that is the only consumer.
-        if (fuse && internal_single(out)) {
+        if (!reglu && fuse && internal_single(out)) {
             const aot::Node& c = ns[first_consumer[out]];
             if (c.op == Op::DEPTH_TO_SPACE && c.inputs[0] == out && !done[c.index]) {
                 d.out_d2s_block = c.block_size();
@@ -1413,11 +1473,13 @@ private:
         // Pack weights into the variant's fragment order, widen the bias.
         L.w_oihw = weight_fp16(n.inputs[1]);
         L.bias_oc = bias_f32(n, d.oc, static_cast<std::size_t>(d.oc));
+        if (reglu) reglu_row_order(L, d.oc, static_cast<std::size_t>(d.ic) * d.kh * d.kw);
         pack_conv(L, L.packed, L.bias, d);
-        // Algorithmic work: 2*N*OC*OH*OW*IC*KH*KW FLOPs; bytes = each tensor once.
+        // Algorithmic work: 2*N*OC*OH*OW*IC*KH*KW FLOPs; bytes = each tensor once
+        // (a ReGLU epilogue writes OC/2 channels).
         L.flops = 2.0 * d.n * d.oc * d.oh * d.ow * static_cast<double>(d.ic) * d.kh * d.kw;
         L.bytes = 2.0 * (static_cast<double>(d.n) * d.ic * d.ih * d.iw + static_cast<double>(d.oc) * d.ic * d.kh * d.kw + d.oc +
-                         static_cast<double>(d.n) * d.oc * d.oh * d.ow * (L.res ? 2.0 : 1.0));
+                         static_cast<double>(d.n) * d.oc * d.oh * d.ow * (L.res ? 2.0 : reglu ? 0.5 : 1.0));
     }
 
     // 3x3 s1 p1 conv (input plain or a folded SPACE_TO_DEPTH(2)) [-> LEAKY_RELU]

@@ -102,6 +102,8 @@ void validate(const mlvc_hip_conv_desc& d, bool pointers)
     if (d.x2 && (d.ic_split <= 0 || d.ic_split >= d.ic)) throw std::runtime_error("conv: invalid concat split");
     if (d.out_d2s_block > 1 && d.oc % (d.out_d2s_block * d.out_d2s_block) != 0)
         throw std::runtime_error("conv: invalid depth_to_space fusion");
+    if (d.epilogue == MLVC_EPI_REGLU && (d.oc % 64 != 0 || d.out_d2s_block > 1))
+        throw std::runtime_error("conv: ReGLU epilogue needs 64-channel gate/linear blocks and no depth_to_space");
     if (!pointers) return;
     if (d.epilogue == MLVC_EPI_RESIDUAL_ADD && !d.residual) throw std::runtime_error("conv: residual missing");
     if (!d.x || !d.y || !d.packed_w || !d.bias) throw std::runtime_error("conv: null tensor");
@@ -128,6 +130,8 @@ void kernel_geometry(const mlvc_hip_conv_desc& d, int& ih, int& iw, int& oh, int
 bool eligible(const mlvc_hip_conv_desc& d, const Variant& k)
 {
     if (k.bm == 0 || k.kh != d.kh || k.kw != d.kw || k.s != d.stride_h || k.s != d.stride_w) return false;
+    // ReGLU pairs gate and linear rows inside 64-row blocks of one tile.
+    if (d.epilogue == MLVC_EPI_REGLU && k.bm % 64 != 0) return false;
     if (d.kh == 1 && (d.pad_h || d.pad_w)) return false;
     int ih, iw, oh, ow;
     kernel_geometry(d, ih, iw, oh, ow);
@@ -266,7 +270,10 @@ int mlvc_hip_conv_launch(const mlvc_hip_conv_desc* desc, mlvc_hip_stream s)
         a.pw = d.pad_w;
         a.epi = d.epilogue;
         a.alpha = d.alpha;
+        a.lo = d.clip_lo;
+        a.hi = d.clip_hi;
         if (k.bm == 0) {
+            if (d.epilogue == MLVC_EPI_REGLU) throw std::runtime_error("conv: no tile variant runs this ReGLU conv");
             a.ih = d.ih; a.iw = d.iw; a.oh = d.oh; a.ow = d.ow;
             const size_t total = static_cast<size_t>(d.n) * d.oc * d.oh * d.ow;
             const unsigned blocks = static_cast<unsigned>(std::min<size_t>((total + 255) / 256, 65535));

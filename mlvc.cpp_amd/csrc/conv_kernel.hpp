@@ -55,6 +55,7 @@ struct ConvArgs {
     int ic, ih, iw, oc, oh, ow, kh, kw, sh, sw, ph, pw;
     int epi;
     float alpha;
+    float lo, hi;  // MLVC_EPI_REGLU clip bounds
     int tiles_x, nchunks;
     int tiles, ocbs, nwg;  // pixel tiles per image, output-channel blocks, workgroups (tiles*ocbs*n)
 };
@@ -143,6 +144,17 @@ __device__ __forceinline__ void store_output(const ConvArgs& a, std::uint16_t h,
     } else {
         a.y[(static_cast<size_t>(b * a.oc + oc) * a.oh + oy) * a.ow + ox] = h;
     }
+}
+
+// ReGLU of a rounded (gate, linear) pair: fp16(fp16(clip(gate)) * linear),
+// the clip as MINPS / MAXPS selects (a NaN gate gives hi, then stays), the
+// product a plain FP32 multiply rounded once.
+__device__ __forceinline__ std::uint16_t reglu_h(std::uint16_t g, std::uint16_t l, float lo, float hi)
+{
+    float c = h2f(g);
+    c = c < hi ? c : hi;
+    c = c > lo ? c : lo;
+    return f2h(mul_f32(h2f(f2h(c)), h2f(l)));
 }
 
 template <int BM_, int TH_, int TW_, int KH_, int KW_, int S_, int KC_, int STG_, bool DB_, int WM_ = 1, int WNW_ = 4,
@@ -558,6 +570,42 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
                 lds[ocl * C::EPI_ROW + pl] = f2h(acc[mt][nt][r]);
             }
     __syncthreads();
+
+    // ReGLU: the tile's rows 64k + i (gate) and 64k + 32 + i (linear) give
+    // output channel ocb * BM/2 + 32k + i of the G-channel output.
+    if (a.epi == MLVC_EPI_REGLU) {
+        const int half = a.oc / 2;
+        const size_t hw_out = static_cast<size_t>(a.oh) * a.ow;
+        if (a.ow % 8 == 0) {
+            constexpr int GROUPS = C::BN / 8;
+            for (int u = tid; u < (C::BM / 2) * GROUPS; u += C::kThreads) {
+                const int g = u % GROUPS, ol = u / GROUPS, rg = (ol / 32) * 64 + ol % 32;
+                const int oc = ocb * (C::BM / 2) + ol;
+                const int pl = g * 8, oy = ty0 + pl / C::TW, ox = tx0 + pl % C::TW;
+                if (oc >= half || oy >= a.oh || ox >= a.ow) continue;
+                const u32x4 hg = *reinterpret_cast<const u32x4*>(&lds[rg * C::EPI_ROW + pl]);
+                const u32x4 hl = *reinterpret_cast<const u32x4*>(&lds[(rg + 32) * C::EPI_ROW + pl]);
+                u32x4 o;
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    o[k] = reglu_h(static_cast<std::uint16_t>(hg[k]), static_cast<std::uint16_t>(hl[k]), a.lo, a.hi) |
+                           (static_cast<std::uint32_t>(reglu_h(static_cast<std::uint16_t>(hg[k] >> 16),
+                                                               static_cast<std::uint16_t>(hl[k] >> 16), a.lo, a.hi))
+                            << 16);
+                *reinterpret_cast<u32x4*>(a.y + (static_cast<size_t>(b) * half + oc) * hw_out + static_cast<size_t>(oy) * a.ow + ox) = o;
+            }
+        } else {
+            for (int e = tid; e < (C::BM / 2) * C::BN; e += C::kThreads) {
+                const int ol = e / C::BN, pl = e - ol * C::BN, rg = (ol / 32) * 64 + ol % 32;
+                const int oc = ocb * (C::BM / 2) + ol;
+                const int oy = ty0 + pl / C::TW, ox = tx0 + pl % C::TW;
+                if (oc < half && oy < a.oh && ox < a.ow)
+                    a.y[(static_cast<size_t>(b) * half + oc) * hw_out + static_cast<size_t>(oy) * a.ow + ox] =
+                        reglu_h(lds[rg * C::EPI_ROW + pl], lds[(rg + 32) * C::EPI_ROW + pl], a.lo, a.hi);
+            }
+        }
+        return;
+    }
 
     // Stage 2: the epilogue acts on the rounded value. Vector path: 8
     // consecutive pixels of a channel per thread, 16-byte loads and stores.

@@ -188,3 +188,42 @@ def test_fused_conv_pair(tmp_path, monkeypatch, s2d, ica, h, w, acts, n):
     ref = plain.run(ins)[0]
     plain.close()
     assert (got == ref).all()
+
+
+# 1x1 conv -> SLICE [0,G) / [G,2G) -> CLIP(gate) -> MUL(clipped, linear): one
+# launch with the ReGLU epilogue (the reference's pointwise ReGLU fusion),
+# G-channel output; flattened and ragged pixel counts, two images, G = 32,
+# 64 and 96 (several 64-row blocks, a partial last output-channel block).
+@pytest.mark.parametrize("ic,g,h,w,n,lo,hi", [(64, 32, 16, 24, 1, -1.0, 6.0), (48, 64, 7, 13, 2, 0.0, 4.0),
+                                              (32, 96, 12, 20, 1, -2.0, 2.0)])
+def test_conv_reglu_epilogue(tmp_path, monkeypatch, ic, g, h, w, n, lo, hi):
+    rng = np.random.default_rng(ic + g + h)
+    gr = graphs.Graph()
+    x = gr.input("x", [n, ic, h, w])
+    wt = gr.weight_fp16("w", rng.normal(0, 1 / np.sqrt(ic), (2 * g, ic, 1, 1)))
+    bt = gr.weight_fp16("b", rng.normal(0, 0.2, (2 * g,)))
+    c = gr.conv("c", x, wt, bt)
+    i64 = lambda name, v: gr.weight(name, np.array([v], np.int64), graphs.INT64)  # noqa: E731
+    gate = gr.node("SLICE", [c, i64("s0", 0), i64("e0", g), i64("a0", 1)], "gate", [n, g, h, w])
+    lin = gr.node("SLICE", [c, i64("s1", g), i64("e1", 2 * g), i64("a1", 1)], "lin", [n, g, h, w])
+    clipped = gr.node("CLIP", [gate, gr.weight_fp16("lo", np.array([lo])), gr.weight_fp16("hi", np.array([hi]))], "clipped",
+                      [n, g, h, w])
+    y = gr.node("MUL", [clipped, lin], "y", [n, g, h, w])
+    gr.output(y)
+    gr.write(tmp_path, "m")
+    ins = [graphs.half(rng.uniform(-3, 3, (n, ic, h, w)))]
+    want = mlvc_oracle.OraclePlan(tmp_path, "m").run(ins)[0]
+    fused = mlvc_hip.Backend(tmp_path, "hip")
+    fused.load("m")
+    kinds = [l["kind"] for l in fused.launches()]
+    assert len(kinds) == 1 and kinds[0].endswith("+reglu"), kinds
+    got = fused.run(ins)[0]
+    fused.close()
+    assert_parity(got, want, f"conv+reglu ic={ic} g={g} {n}x{h}x{w}")
+    monkeypatch.setenv("MLVC_HIP_DISABLE_FUSION", "1")
+    plain = mlvc_hip.Backend(tmp_path, "hip")
+    plain.load("m")
+    ref = plain.run(ins)[0]
+    plain.close()
+    assert (got == ref).all()
+
