@@ -76,7 +76,10 @@ int mlvc_hip_graph_destroy(mlvc_hip_graph graph);
  *   out_d2s_block > 1: the output is written through DEPTH_TO_SPACE(block)
  *                      (CRD), y is [n, oc/b^2, oh*b, ow*b].
  */
-enum { MLVC_EPI_NONE = 0, MLVC_EPI_LEAKY_RELU = 1, MLVC_EPI_RESIDUAL_ADD = 2, MLVC_EPI_REGLU = 3 };
+enum { MLVC_EPI_NONE = 0, MLVC_EPI_LEAKY_RELU = 1, MLVC_EPI_RESIDUAL_ADD = 2, MLVC_EPI_REGLU = 3, MLVC_EPI_CLAMP = 4 };
+/* MLVC_EPI_CLAMP (the reference's GEMM kClamp epilogue, fusion_matcher.cpp:
+ * 378-389, kernels_x86_avx2.cpp:196-198): y = max(min(fp16(acc), clip_hi),
+ * clip_lo), NaN giving clip_hi as in the vector lanes. */
 /* MLVC_EPI_REGLU (the reference's 1x1 conv with a ReGLU epilogue,
  * backends/cpu/src/fusion_matcher.cpp:258-302): the conv computes oc = 2G
  * channels, rounded to FP16, and writes y [n, G, oh, ow] =
@@ -97,7 +100,7 @@ typedef struct mlvc_hip_conv_desc {
     const float* bias;                 /* fp32 widening of the fp16 bias, length mlvc_hip_conv_bias_len */
     int epilogue;
     float alpha;
-    float clip_lo, clip_hi;            /* MLVC_EPI_REGLU bounds */
+    float clip_lo, clip_hi;            /* MLVC_EPI_CLAMP / MLVC_EPI_REGLU bounds */
     const void* residual;              /* [n, oc, oh, ow] */
     void* y;
     int out_d2s_block;

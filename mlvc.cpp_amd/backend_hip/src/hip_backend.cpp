@@ -1435,6 +1435,14 @@ private:
                 done[nx.index] = true;
                 out = nx.outputs[0];
                 tags += "+lrelu";
+            } else if (float lo = 0.0F, hi = 0.0F; clip_constants(nx, lo, hi) && nx.inputs[0] == out &&
+                                                   desc(nx.outputs[0]).shape == desc(out).shape) {
+                d.epilogue = MLVC_EPI_CLAMP;
+                d.clip_lo = lo;
+                d.clip_hi = hi;
+                done[nx.index] = true;
+                out = nx.outputs[0];
+                tags += "+clip";
             } else if (nx.op == Op::ADD && (nx.inputs[0] == out || nx.inputs[1] == out)) {
                 const TensorId r = nx.inputs[0] == out ? nx.inputs[1] : nx.inputs[0];
                 if (r != out && !is_weight(r) && desc(r).dtype == aot::DataType::FP16 && desc(r).shape == desc(out).shape) {

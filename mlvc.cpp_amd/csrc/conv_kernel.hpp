@@ -55,7 +55,7 @@ struct ConvArgs {
     int ic, ih, iw, oc, oh, ow, kh, kw, sh, sw, ph, pw;
     int epi;
     float alpha;
-    float lo, hi;  // MLVC_EPI_REGLU clip bounds
+    float lo, hi;  // MLVC_EPI_CLAMP / MLVC_EPI_REGLU clip bounds
     int tiles_x, nchunks;
     int tiles, ocbs, nwg;  // pixel tiles per image, output-channel blocks, workgroups (tiles*ocbs*n)
 };
@@ -122,10 +122,28 @@ __device__ __forceinline__ std::uint16_t load_input(const ConvArgs& a, int b, in
     return a.x[(static_cast<size_t>(b * a.ic + c) * a.ih + iy) * a.iw + ix];
 }
 
+// Clamp epilogue on a rounded value: max(min(h, hi), lo) as the reference's
+// vector GEMM epilogue computes it (MINPS / MAXPS operand order: a NaN gives
+// hi). The bounds are FP16 values, so the result needs no further rounding.
+__device__ __forceinline__ std::uint16_t clamp_h(std::uint16_t h, float lo, float hi)
+{
+    float c = h2f(h);
+    c = c < hi ? c : hi;
+    c = c > lo ? c : lo;
+    return f2h(c);
+}
+__device__ __forceinline__ std::uint32_t clamp_h2(std::uint32_t h, float lo, float hi)
+{
+    return clamp_h(static_cast<std::uint16_t>(h), lo, hi) |
+           (static_cast<std::uint32_t>(clamp_h(static_cast<std::uint16_t>(h >> 16), lo, hi)) << 16);
+}
+
 __device__ __forceinline__ std::uint16_t finish(const ConvArgs& a, float acc, int b, int oc, int oy, int ox)
 {
     std::uint16_t h = f2h(acc);
-    if (a.epi == MLVC_EPI_LEAKY_RELU) {
+    if (a.epi == MLVC_EPI_CLAMP) {
+        h = clamp_h(h, a.lo, a.hi);
+    } else if (a.epi == MLVC_EPI_LEAKY_RELU) {
         const float f = h2f(h);
         if (f < 0.0f) h = leaky_f16(f, a.alpha);
     } else if (a.epi == MLVC_EPI_RESIDUAL_ADD) {
@@ -536,6 +554,10 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
                     } else {
                         h01 = pack_f16(v[0], v[1]);
                         h23 = pack_f16(v[2], v[3]);
+                        if (a.epi == MLVC_EPI_CLAMP) {
+                            h01 = clamp_h2(h01, a.lo, a.hi);
+                            h23 = clamp_h2(h23, a.lo, a.hi);
+                        }
                         if (a.epi == MLVC_EPI_RESIDUAL_ADD && inside) {
                             std::uint16_t r[4];
 #pragma unroll
@@ -620,6 +642,9 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
             if (a.epi == MLVC_EPI_LEAKY_RELU) {
 #pragma unroll
                 for (int k = 0; k < 4; ++k) h[k] = leaky_h2(h[k], a.alpha, max_form);
+            } else if (a.epi == MLVC_EPI_CLAMP) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) h[k] = clamp_h2(h[k], a.lo, a.hi);
             } else if (a.epi == MLVC_EPI_RESIDUAL_ADD) {
                 const u32x4 r = *reinterpret_cast<const u32x4*>(a.res + o);
 #pragma unroll
@@ -640,6 +665,8 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
             if (a.epi == MLVC_EPI_LEAKY_RELU) {
                 const float f = h2f(h);
                 if (f < 0.0f) h = leaky_f16(f, a.alpha);
+            } else if (a.epi == MLVC_EPI_CLAMP) {
+                h = clamp_h(h, a.lo, a.hi);
             } else if (a.epi == MLVC_EPI_RESIDUAL_ADD) {
                 h = f2h(h2f(h) + h2f(a.res[(static_cast<size_t>(b * a.oc + oc) * a.oh + oy) * a.ow + ox]));
             }

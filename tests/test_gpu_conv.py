@@ -227,3 +227,36 @@ def test_conv_reglu_epilogue(tmp_path, monkeypatch, ic, g, h, w, n, lo, hi):
     plain.close()
     assert (got == ref).all()
 
+
+# conv -> CLIP: one launch with the clamp epilogue (the reference's kClamp
+# GEMM epilogue), 3x3 and 1x1, with both bounds or only the upper one.
+@pytest.mark.parametrize("k,lo,hi", [(3, -0.5, 0.75), (1, None, 0.25), (3, 0.0, 6.0)])
+def test_conv_clip_epilogue(tmp_path, monkeypatch, k, lo, hi):
+    rng = np.random.default_rng(k + 17)
+    n, ic, h, w, oc = 1, 24, 9, 20, 40
+    gr = graphs.Graph()
+    x = gr.input("x", [n, ic, h, w])
+    wt = gr.weight_fp16("w", rng.normal(0, 1 / np.sqrt(ic * k * k), (oc, ic, k, k)))
+    bt = gr.weight_fp16("b", rng.normal(0, 0.2, (oc,)))
+    p = k // 2
+    c = gr.conv("c", x, wt, bt, (1, 1), (p, p, p, p))
+    lo_id = gr.weight_fp16("lo", np.array([lo])) if lo is not None else 0
+    y = gr.node("CLIP", [c, lo_id, gr.weight_fp16("hi", np.array([hi]))], "y", [n, oc, h, w])
+    gr.output(y)
+    gr.write(tmp_path, "m")
+    ins = [graphs.half(rng.uniform(-2, 2, (n, ic, h, w)))]
+    want = mlvc_oracle.OraclePlan(tmp_path, "m").run(ins)[0]
+    fused = mlvc_hip.Backend(tmp_path, "hip")
+    fused.load("m")
+    kinds = [l["kind"] for l in fused.launches()]
+    assert len(kinds) == 1 and kinds[0].endswith("+clip"), kinds
+    got = fused.run(ins)[0]
+    fused.close()
+    assert_parity(got, want, f"conv{k}+clip")
+    monkeypatch.setenv("MLVC_HIP_DISABLE_FUSION", "1")
+    plain = mlvc_hip.Backend(tmp_path, "hip")
+    plain.load("m")
+    ref = plain.run(ins)[0]
+    plain.close()
+    assert (got == ref).all()
+
