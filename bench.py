@@ -247,9 +247,35 @@ def cpu_baseline(model_dir, bindings, shape, budget_s: float):
         el = time.perf_counter() - t0
         if el >= budget_s or frames >= 64:
             break
-    return {"value": frames / el, "unit": "frames/s", "cores": plan.threads, "kind": "port",
+    return {"value": frames / el, "unit": "frames/s", "cores": plan.threads, "kind": "port", **host_cpu(),
             "sample": f"{frames} consecutive frames of {CONFIG} (recurrent state carried) after 1 warm-up frame, "
                       f"{el:.1f} s wall, oracle AVX2+FMA+F16C path, {plan.threads} threads"}
+
+
+COLD_FLUSH_BYTES = 512 << 20
+
+
+def spread(ms) -> dict:
+    """Median and 10th/90th percentiles of per-frame times (ms)."""
+    import numpy as np
+
+    q = np.percentile(np.asarray(ms, dtype=np.float64), [50, 10, 90])
+    return {"median": float(q[0]), "p10": float(q[1]), "p90": float(q[2]), "frames": len(ms)}
+
+
+def host_cpu() -> dict:
+    """CPU model, hardware thread count and the threads this process may use."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "hardware_concurrency": os.cpu_count(),
+            "usable_threads": len(os.sched_getaffinity(0))}
 
 
 PMC_REPS = 10
@@ -326,6 +352,8 @@ def main() -> int:
     ap.add_argument("--codec-frames", type=int, default=60)
     ap.add_argument("--no-realops", action="store_true", help="skip the real-model operator measurements")
     ap.add_argument("--realops-frames", type=int, default=50)
+    ap.add_argument("--cold-frames", type=int, default=50,
+                    help="frames timed with L2 and MALL flushed before each (0: skip)")
     ap.add_argument("--api-frames", type=int, default=30,
                     help="frames timed through run() (host frame in, host reconstruction out)")
     ap.add_argument("--pmc-pass", default=None, metavar="I,J,...",
@@ -370,6 +398,16 @@ def main() -> int:
         launches = gpu.launches()
         conv_flops = sum(l["flops"] for l in launches)
         frame_bytes = sum(l["bytes"] for l in launches)
+        # Per-frame spread (events around every frame of a back-to-back run),
+        # then cold frames: a 512 MiB device copy before each frame, outside
+        # its events, evicts L2 (4 MB per XCD) and the 256 MB MALL.
+        each = gpu.time_frames_each(args.steps)
+        cold = gpu.time_frames_each(args.cold_frames, COLD_FLUSH_BYTES) if args.cold_frames > 0 else None
+        frame_ms = spread(each)
+        cold_ms = dict(spread(cold), flush_bytes=COLD_FLUSH_BYTES) if cold is not None else None
+        log(f"per frame: median {frame_ms['median']:.3f} ms (p10 {frame_ms['p10']:.3f}, p90 {frame_ms['p90']:.3f})"
+            + (f"; cold (L2 + MALL flushed) median {cold_ms['median']:.3f} ms (p10 {cold_ms['p10']:.3f}, "
+               f"p90 {cold_ms['p90']:.3f})" if cold_ms else ""))
         rows = kernel_table(gpu, args.kernel_reps)
         dom = max(rows, key=lambda r: r["ms"])
         dom_t = dom["ms"] * 1e-3
@@ -438,6 +476,8 @@ def main() -> int:
         "conv_tflops": conv_tflops,
         "conv_mfma_peak_frac": conv_tflops / PEAK_MFMA_TFLOPS,
         "gpu_event_ms_per_step": gpu_ms / args.steps,
+        "frame_ms": frame_ms,
+        "cold_frame_ms": cold_ms,
         "run_api_frames_per_s": api_fps,
         "roofline": roof,
         "cpu_baseline": base,

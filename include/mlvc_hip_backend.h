@@ -101,6 +101,11 @@ int mlvc_hip_backend_upload_inputs(mlvc_backend* backend, const void* const* inp
  * host copies) and returns the elapsed GPU time between events recorded on
  * the backend's stream around them. */
 int mlvc_hip_backend_time_frames(mlvc_backend* backend, int frames, float* ms);
+/* The same replays with events recorded just before and after every frame:
+ * ms_each[f] is frame f's GPU time (1 <= frames <= 4096). flush_bytes > 0
+ * runs a device-to-device copy of flush_bytes / 2 bytes before each frame,
+ * outside its events, so each frame starts with cold L2 and MALL. */
+int mlvc_hip_backend_time_frames_each(mlvc_backend* backend, int frames, size_t flush_bytes, float* ms_each);
 /* Copies the current external outputs to the host. */
 int mlvc_hip_backend_download_outputs(mlvc_backend* backend, uint16_t* const* outputs);
 /* Kernel launches of one frame. info: name, kernel variant, FLOPs and

@@ -286,6 +286,14 @@ int mlvc_hip_backend_time_frames(mlvc_backend* backend, int frames, float* ms)
     return guard([&] { *ms = hip(backend).time_frames(frames); });
 }
 
+int mlvc_hip_backend_time_frames_each(mlvc_backend* backend, int frames, size_t flush_bytes, float* ms_each)
+{
+    return guard([&] {
+        if (!ms_each) throw std::runtime_error("time_frames_each: null output");
+        hip(backend).time_frames_each(frames, flush_bytes, ms_each);
+    });
+}
+
 int mlvc_hip_backend_download_outputs(mlvc_backend* backend, uint16_t* const* outputs)
 {
     return guard([&] {

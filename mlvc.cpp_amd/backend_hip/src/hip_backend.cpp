@@ -178,6 +178,8 @@ public:
         for (auto g : graphs_) mlvc_hip_graph_destroy(g);
         mlvc_hip_event_destroy(ev0_);
         mlvc_hip_event_destroy(ev1_);
+        for (auto e : frame_evs_) mlvc_hip_event_destroy(e);
+        if (flush_buf_) mlvc_hip_free(flush_buf_);
         mlvc_hip_stream_destroy(stream_);
     }
 
@@ -442,6 +444,42 @@ public:
         float ms = 0.0F;
         hip_check(mlvc_hip_event_elapsed_ms(ev0_, ev1_, &ms), "event timing");
         return ms;
+    }
+
+    // Per-frame GPU times of `frames` replays submitted back to back: events
+    // are recorded just before and just after every frame. With
+    // flush_bytes > 0, a device-to-device copy of flush_bytes / 2 bytes runs
+    // before each frame, outside its events, so every frame starts with its
+    // weights and activations evicted from L2 and the MALL (a cold frame).
+    void time_frames_each(int frames, std::size_t flush_bytes, float* ms_each)
+    {
+        if (!initialized_) fail("reset_state() must be called before running frames");
+        if (frames <= 0 || frames > 4096) fail("time_frames_each: frames must be in 1..4096");
+        select();
+        while (frame_evs_.size() < 2 * static_cast<std::size_t>(frames)) {
+            mlvc_hip_event e = nullptr;
+            hip_check(mlvc_hip_event_create(&e), "event creation");
+            frame_evs_.push_back(e);
+        }
+        if (flush_bytes > 0 && flush_bytes != flush_bytes_) {
+            if (flush_buf_) hip_check(mlvc_hip_free(flush_buf_), "flush buffer release");
+            flush_buf_ = nullptr;
+            flush_bytes_ = 0;
+            hip_check(mlvc_hip_malloc(&flush_buf_, flush_bytes), "flush buffer allocation");
+            flush_bytes_ = flush_bytes;
+        }
+        const std::size_t half = flush_bytes / 2;
+        auto* fb = static_cast<std::uint8_t*>(flush_buf_);
+        for (int f = 0; f < frames; ++f) {
+            if (half) hip_check(mlvc_hip_memcpy_d2d(fb + half, fb, half, stream_), "cache flush copy");
+            hip_check(mlvc_hip_event_record(frame_evs_[2 * f], stream_), "event record");
+            hip_check(mlvc_hip_graph_launch(graphs_[static_cast<std::size_t>(parity_)], stream_), "graph launch");
+            advance();
+            hip_check(mlvc_hip_event_record(frame_evs_[2 * f + 1], stream_), "event record");
+        }
+        hip_check(mlvc_hip_event_synchronize(frame_evs_[2 * frames - 1]), "event sync");
+        for (int f = 0; f < frames; ++f)
+            hip_check(mlvc_hip_event_elapsed_ms(frame_evs_[2 * f], frame_evs_[2 * f + 1], &ms_each[f]), "event timing");
     }
 
     void download_outputs(const std::vector<std::uint16_t*>& outputs)
@@ -2118,6 +2156,9 @@ private:
     aot::LoadedGraph graph_;
     mlvc_hip_stream stream_ = nullptr;
     mlvc_hip_event ev0_ = nullptr, ev1_ = nullptr;
+    std::vector<mlvc_hip_event> frame_evs_;  // time_frames_each: start/stop per frame
+    void* flush_buf_ = nullptr;              // time_frames_each: cache-flush copy buffer
+    std::size_t flush_bytes_ = 0;
     std::vector<Binding> bindings_;
     std::map<TensorId, std::size_t> state_in_, state_out_;
     std::vector<TensorId> ext_in_, ext_out_;
@@ -2179,6 +2220,10 @@ void HipBackend::submit_decoder(std::size_t slot, int q) { require_plan("submit_
 Yuv420FrameView HipBackend::decoder_output_yuv(std::size_t slot) const { return require_plan("decoder_output_yuv()").decoder_output_yuv(slot); }
 void HipBackend::wait_codec_slot(std::size_t slot) { require_plan("wait_codec_slot()").wait_codec_slot(slot); }
 float HipBackend::time_frames(int frames) { return require_plan("time_frames()").time_frames(frames); }
+void HipBackend::time_frames_each(int frames, std::size_t flush_bytes, float* ms_each)
+{
+    require_plan("time_frames_each()").time_frames_each(frames, flush_bytes, ms_each);
+}
 void HipBackend::download_outputs(const std::vector<std::uint16_t*>& outputs) { require_plan("download_outputs()").download_outputs(outputs); }
 std::size_t HipBackend::launch_count() const { return require_plan("launch_count()").launch_count(); }
 LaunchInfo HipBackend::launch_info(std::size_t index) const { return require_plan("launch_info()").launch_info(index); }

@@ -55,6 +55,7 @@ public:
     // Device-resident measurement helpers (inputs as raw host bytes).
     void upload_inputs(const std::vector<const void*>& inputs);
     float time_frames(int frames);
+    void time_frames_each(int frames, std::size_t flush_bytes, float* ms_each);
     void download_outputs(const std::vector<std::uint16_t*>& outputs);
     std::size_t launch_count() const;
     LaunchInfo launch_info(std::size_t index) const;

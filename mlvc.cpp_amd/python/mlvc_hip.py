@@ -72,6 +72,7 @@ def backend_lib() -> C.CDLL:
         lib.mlvc_backend_available.argtypes = [C.c_char_p, C.c_size_t]
         lib.mlvc_hip_backend_upload_inputs.argtypes = [C.c_void_p, C.POINTER(C.c_void_p)]
         lib.mlvc_hip_backend_time_frames.argtypes = [C.c_void_p, C.c_int, C.POINTER(C.c_float)]
+        lib.mlvc_hip_backend_time_frames_each.argtypes = [C.c_void_p, C.c_int, C.c_size_t, C.POINTER(C.c_float)]
         lib.mlvc_hip_backend_download_outputs.argtypes = [C.c_void_p, C.POINTER(_u16p)]
         lib.mlvc_hip_backend_launch_count.argtypes = [C.c_void_p, C.POINTER(C.c_int)]
         lib.mlvc_hip_backend_launch_info.argtypes = [C.c_void_p, C.c_int, C.c_char_p, C.c_size_t, C.c_char_p,
@@ -296,6 +297,14 @@ class Backend:
         ms = C.c_float()
         _check(self._lib.mlvc_hip_backend_time_frames(self._h, frames, C.byref(ms)))
         return ms.value
+
+    def time_frames_each(self, frames: int, flush_bytes: int = 0) -> np.ndarray:
+        """Per-frame GPU ms of `frames` back-to-back replays; flush_bytes > 0
+        evicts the caches with a device copy before each (untimed)."""
+        ms = np.zeros(frames, dtype=np.float32)
+        _check(self._lib.mlvc_hip_backend_time_frames_each(
+            self._h, frames, flush_bytes, ms.ctypes.data_as(C.POINTER(C.c_float))))
+        return ms
 
     def download_outputs(self) -> list[np.ndarray]:
         outs = [np.empty(s, dtype=np.uint16) for s in self.out_shapes]

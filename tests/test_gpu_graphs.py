@@ -115,6 +115,33 @@ def test_device_resident_replay_matches_run(tmp_path):
     b.close()
 
 
+def test_per_frame_timing_replays_the_same_frames(tmp_path):
+    """time_frames_each (with and without the cache-flush copy between frames)
+    advances the recurrent state exactly as run() does and returns one
+    positive time per frame."""
+    config = "mlvc_s_tiny"
+    bindings, _ = _write(tmp_path, config)
+    a = mlvc_hip.Backend(tmp_path, "hip")
+    a.load(config, bindings)
+    b = mlvc_hip.Backend(tmp_path, "hip")
+    b.load(config, bindings)
+    x = mlvc_hip.synth_input(config, 0, 0, a.in_shapes[0])
+    a.reset_state()
+    b.reset_state()
+    for _ in range(5):
+        want = a.run([x])
+    b.upload_inputs([x])
+    warm = b.time_frames_each(3)
+    cold = b.time_frames_each(2, 8 << 20)
+    assert warm.shape == (3,) and cold.shape == (2,)
+    assert (warm > 0).all() and (cold > 0).all()
+    assert (b.download_outputs()[0] == want[0]).all()
+    with pytest.raises(mlvc_hip.MlvcError, match="frames"):
+        b.time_frames_each(0)
+    a.close()
+    b.close()
+
+
 @pytest.mark.parametrize("config", ["mlvc_s_tiny", "mlvc_tiny", "dwblock_92x160_c128", "dwblock_46x80_c256"])
 def test_fused_and_unfused_schedules_bit_identical(tmp_path, monkeypatch, config):
     """Every GPU fusion (S2D/CONCAT loads, epilogues, D2S stores, the fused
