@@ -62,7 +62,7 @@ def test_recurrent_free_running(tmp_path, config, frames):
     gpu.close()
 
 
-@pytest.mark.parametrize("config,frames", [("mlvc_s_tiny", 3), ("mlvc_s_640x368", 3)])
+@pytest.mark.parametrize("config,frames", [("mlvc_s_tiny", 3), ("mlvc_s_640x368", 8), ("mlvc_1920x1088", 32)])
 def test_recurrent_teacher_forced(tmp_path, config, frames):
     _write(tmp_path, config)
     # Unbound: ref_in is an ordinary input and ref_out an ordinary output.
@@ -79,7 +79,20 @@ def test_recurrent_teacher_forced(tmp_path, config, frames):
     gpu.close()
 
 
-def test_mlvc_1920x1088_two_frames(tmp_path):
+# Free-running bound of the 1920x1088 graph: twice the per-frame FP16 bar.
+DRIFT_MAX_REL, DRIFT_MEAN_REL = 2e-2, 2e-3
+
+
+def test_mlvc_1920x1088_free_running(tmp_path):
+    """The 1920x1088 graph over 32 frames, each backend carrying its own
+    recurrent state. Frame 0 (both states zero) meets the FP16 bar. After it
+    each side feeds its own FP16 rounding back through the 64-channel state,
+    so the difference grows for about ten frames and then levels off (recon
+    mean |d| about 1.3e-3 of RMS, against a flat 6.8e-4 when the GPU is fed
+    the oracle's state every frame, which test_recurrent_teacher_forced holds
+    to the FP16 bar). Every frame stays within twice the bar, and the last
+    eight frames' mean error is no larger than the eight before them, give or
+    take 5%: the drift is bounded, not growing."""
     config = "mlvc_1920x1088"
     bindings, _ = _write(tmp_path, config)
     gpu = mlvc_hip.Backend(tmp_path, "hip")
@@ -87,9 +100,17 @@ def test_mlvc_1920x1088_two_frames(tmp_path):
     ref = mlvc_oracle.OraclePlan(tmp_path, config, bindings)
     gpu.reset_state()
     ref.reset_state()
-    for f in range(2):
+    means = []
+    for f in range(32):
         x = mlvc_hip.synth_input(config, 0, f, gpu.in_shapes[0])
-        assert_parity(gpu.run([x])[0], ref.run([x])[0], f"{config} frame {f}")
+        got, want = gpu.run([x])[0], ref.run([x])[0]
+        if f == 0:
+            assert_parity(got, want, f"{config} frame 0")
+        st = mlvc_oracle.parity_stats(got, want)
+        assert st["finite"], f"{config} frame {f}: non-finite output"
+        assert st["max_rel"] <= DRIFT_MAX_REL and st["mean_rel"] <= DRIFT_MEAN_REL, f"{config} frame {f}: {st}"
+        means.append(st["mean_rel"])
+    assert np.mean(means[24:]) <= 1.05 * np.mean(means[16:24]), means
     gpu.close()
 
 
