@@ -131,14 +131,10 @@ int mlvc_aot_inspect(const char* model_dir, const char* model_name, int* nodes, 
  * metadata.pb checked against model_bundle.pb, ModelConfig::validate,
  * :50-91) as a JSON object of the ModelConfig members plus the derived
  * feature / latent / hyperprior dimensions; -1 with the reference's message
- * on any mismatch. mlvc_model_q_index_shift: ModelConfig::q_index_shift
- * (:136-147); mlvc_model_frame_in_gop: ModelConfig::frame_in_gop
- * (:128-135). mlvc_model_verify_bundle: every artifact of model_bundle.pb
+ * on any mismatch. mlvc_model_verify_bundle: every artifact of model_bundle.pb
  * present with its recorded size and SHA-256 (the check of the reference's
  * packager, tools/python/mlvc_tools/package.py:97-145, done in C++). */
 int mlvc_model_config_json(const char* model_dir, char* buf, size_t len);
-int mlvc_model_q_index_shift(const char* model_dir, int frame, int* shift);
-int mlvc_model_frame_in_gop(const char* model_dir, int frame, int* gop_frame);
 int mlvc_model_verify_bundle(const char* model_dir);
 
 /* ---- seeded synthetic graphs (graph.pb / weights.bin / metadata.pb) ---- */

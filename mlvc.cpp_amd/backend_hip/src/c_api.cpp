@@ -370,15 +370,6 @@ int mlvc_model_config_json(const char* model_dir, char* buf, size_t len)
     });
 }
 
-int mlvc_model_q_index_shift(const char* model_dir, int frame, int* shift)
-{
-    return guard([&] { *shift = mlvc::load_model_config(std::filesystem::path(model_dir)).q_index_shift(frame); });
-}
-
-int mlvc_model_frame_in_gop(const char* model_dir, int frame, int* gop_frame)
-{
-    return guard([&] { *gop_frame = mlvc::load_model_config(std::filesystem::path(model_dir)).frame_in_gop(frame); });
-}
 
 int mlvc_model_verify_bundle(const char* model_dir)
 {

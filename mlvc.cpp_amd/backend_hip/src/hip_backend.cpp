@@ -27,12 +27,15 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdio>
 #include <cstdlib>
 #include <cstring>
 #include <fstream>
 #include <map>
 #include <set>
 #include <stdexcept>
+
+#include <unistd.h>
 
 namespace mlvc::hip_backend {
 namespace {
@@ -70,6 +73,21 @@ std::size_t elem_count(const std::vector<std::int64_t>& s)
     std::size_t n = 1;
     for (auto d : s) n *= static_cast<std::size_t>(d);
     return n;
+}
+
+// Bytes of a tensor from its descriptor. Computed here from the schema-3
+// types only (aot_graph.hpp:36-41, 98-103), so the backend builds against
+// the reference's runtime headers, which declare no such helper.
+std::size_t desc_bytes(const aot::TensorDescriptor& t)
+{
+    std::size_t elem = 0;
+    switch (t.dtype) {
+    case aot::DataType::FP16: elem = 2; break;
+    case aot::DataType::INT32: elem = 4; break;
+    case aot::DataType::INT64: elem = 8; break;
+    default: fail("unsupported tensor data type");
+    }
+    return elem * elem_count(t.shape);
 }
 
 struct DeviceMem {
@@ -267,8 +285,8 @@ public:
             sl.io.resize(ids.size());
             for (std::size_t i = 0; i < ids.size(); ++i)
                 if (encoder || static_cast<int>(i) != q) {
-                    sl.io[i] = HostMem(aot::tensor_bytes(desc(ids[i])));
-                    std::memset(sl.io[i].ptr, 0, aot::tensor_bytes(desc(ids[i])));
+                    sl.io[i] = HostMem(desc_bytes(desc(ids[i])));
+                    std::memset(sl.io[i].ptr, 0, desc_bytes(desc(ids[i])));
                 }
             hip_check(mlvc_hip_event_create(&sl.done), "event creation");
         }
@@ -307,7 +325,7 @@ public:
         enqueue_q(sl, shifted_q);
         hip_check(mlvc_hip_graph_launch(graphs_[static_cast<std::size_t>(parity_)], stream_), "graph launch");
         for (std::size_t i = 0; i < ext_out_.size(); ++i)
-            hip_check(mlvc_hip_memcpy_d2h(sl.io[i].ptr, ptr(ext_out_[i], parity_), aot::tensor_bytes(desc(ext_out_[i])), stream_),
+            hip_check(mlvc_hip_memcpy_d2h(sl.io[i].ptr, ptr(ext_out_[i], parity_), desc_bytes(desc(ext_out_[i])), stream_),
                       "output download");
         finish_submit(sl);
     }
@@ -318,7 +336,7 @@ public:
         std::vector<TensorView> v;
         for (std::size_t i = 0; i < ext_out_.size(); ++i) {
             const auto& d = desc(ext_out_[i]);
-            v.push_back(TensorView::from_raw(d.name, d.shape, public_dtype(d.dtype), sl.io[i].ptr, aot::tensor_bytes(d)));
+            v.push_back(TensorView::from_raw(d.name, d.shape, public_dtype(d.dtype), sl.io[i].ptr, desc_bytes(d)));
         }
         return v;
     }
@@ -330,7 +348,7 @@ public:
         for (std::size_t i = 0; i < ext_in_.size(); ++i) {
             if (static_cast<int>(i) == codec_q_) continue;
             const auto& d = desc(ext_in_[i]);
-            v.push_back(MutableTensorView::from_raw(d.name, d.shape, public_dtype(d.dtype), sl.io[i].ptr, aot::tensor_bytes(d)));
+            v.push_back(MutableTensorView::from_raw(d.name, d.shape, public_dtype(d.dtype), sl.io[i].ptr, desc_bytes(d)));
         }
         return v;
     }
@@ -344,7 +362,7 @@ public:
         select();
         for (std::size_t i = 0; i < ext_in_.size(); ++i) {
             if (static_cast<int>(i) == codec_q_) continue;
-            hip_check(mlvc_hip_memcpy_h2d(input_buf_.at(ext_in_[i]).ptr, sl.io[i].ptr, aot::tensor_bytes(desc(ext_in_[i])), stream_),
+            hip_check(mlvc_hip_memcpy_h2d(input_buf_.at(ext_in_[i]).ptr, sl.io[i].ptr, desc_bytes(desc(ext_in_[i])), stream_),
                       "input upload");
         }
         enqueue_q(sl, shifted_q);
@@ -395,7 +413,7 @@ public:
             const Tensor& t = inputs[i];
             t.validate();
             const auto& d = desc(ext_in_[i]);
-            if (t.shape != d.shape || t.data_type() != public_dtype(d.dtype) || t.byte_size() != aot::tensor_bytes(d))
+            if (t.shape != d.shape || t.data_type() != public_dtype(d.dtype) || t.byte_size() != desc_bytes(d))
                 fail("graph input shape, dtype, or byte size mismatch");
             check_gather_indices(i, t.raw_data());
             std::memcpy(in_stage_[i].ptr, t.raw_data(), t.byte_size());
@@ -425,7 +443,7 @@ public:
         for (std::size_t i = 0; i < inputs.size(); ++i) check_gather_indices(i, inputs[i]);
         select();
         for (std::size_t i = 0; i < inputs.size(); ++i)
-            hip_check(mlvc_hip_memcpy_h2d(input_buf_.at(ext_in_[i]).ptr, inputs[i], aot::tensor_bytes(desc(ext_in_[i])), stream_),
+            hip_check(mlvc_hip_memcpy_h2d(input_buf_.at(ext_in_[i]).ptr, inputs[i], desc_bytes(desc(ext_in_[i])), stream_),
                       "input upload");
         hip_check(mlvc_hip_stream_synchronize(stream_), "stream sync");
     }
@@ -489,7 +507,7 @@ public:
         // Outputs of the last frame were produced with the previous parity.
         const int produced = bindings_.empty() ? 0 : parity_ ^ 1;
         for (std::size_t i = 0; i < outputs.size(); ++i)
-            hip_check(mlvc_hip_memcpy_d2h(outputs[i], ptr(ext_out_[i], produced), aot::tensor_bytes(desc(ext_out_[i])), stream_),
+            hip_check(mlvc_hip_memcpy_d2h(outputs[i], ptr(ext_out_[i], produced), desc_bytes(desc(ext_out_[i])), stream_),
                       "output download");
         hip_check(mlvc_hip_stream_synchronize(stream_), "stream sync");
     }
@@ -549,7 +567,7 @@ private:
             Binding nb;
             nb.in = in;
             nb.out = out;
-            nb.bytes = aot::tensor_bytes(desc(in));
+            nb.bytes = desc_bytes(desc(in));
             bindings_.push_back(std::move(nb));
             state_in_[in] = bindings_.size() - 1;
             state_out_[out] = bindings_.size() - 1;
@@ -1126,10 +1144,13 @@ private:
                 if ((i < 0 ? i + static_cast<std::int64_t>(L.dim) : i) < 0 || (i < 0 ? i + static_cast<std::int64_t>(L.dim) : i) >=
                                                                                    static_cast<std::int64_t>(L.dim))
                     fail("GATHER index out of range");
-            auto raw = weight_bytes(ix);
-            DeviceMem m(raw.size());
-            pending_uploads_.push_back({m.ptr, std::move(raw)});
-            const_buf_.emplace(ix, std::move(m));
+            // Several GATHERs may share one index initializer: upload it once.
+            if (!const_buf_.count(ix)) {
+                auto raw = weight_bytes(ix);
+                DeviceMem m(raw.size());
+                pending_uploads_.push_back({m.ptr, std::move(raw)});
+                const_buf_.emplace(ix, std::move(m));
+            }
             L.idx64 = true;
         } else {
             const auto& g = graph_.descriptor.inputs;
@@ -1796,13 +1817,13 @@ private:
         for (auto& kv : live) order.push_back(kv.first);
         std::sort(order.begin(), order.end(), [&](TensorId a, TensorId b) {
             if (live[a].first != live[b].first) return live[a].first < live[b].first;
-            return aot::tensor_bytes(desc(a)) > aot::tensor_bytes(desc(b));
+            return desc_bytes(desc(a)) > desc_bytes(desc(b));
         });
         struct Placed { std::size_t off, size, first, last; };
         std::vector<Placed> placed;
         std::size_t peak = 256;
         for (TensorId id : order) {
-            const std::size_t sz = (aot::tensor_bytes(desc(id)) + 255) / 256 * 256;
+            const std::size_t sz = (desc_bytes(desc(id)) + 255) / 256 * 256;
             const auto [f, l] = live[id];
             std::vector<std::pair<std::size_t, std::size_t>> busy;
             for (const Placed& p : placed)
@@ -1823,11 +1844,11 @@ private:
 
     void allocate_io()
     {
-        for (TensorId id : ext_in_) input_buf_.emplace(id, DeviceMem(aot::tensor_bytes(desc(id))));
+        for (TensorId id : ext_in_) input_buf_.emplace(id, DeviceMem(desc_bytes(desc(id))));
         for (auto& b : bindings_)
             for (auto& buf : b.buf) buf = DeviceMem(b.bytes);
-        for (TensorId id : ext_in_) in_stage_.emplace_back(aot::tensor_bytes(desc(id)));
-        for (TensorId id : ext_out_) out_stage_.emplace_back(aot::tensor_bytes(desc(id)));
+        for (TensorId id : ext_in_) in_stage_.emplace_back(desc_bytes(desc(id)));
+        for (TensorId id : ext_out_) out_stage_.emplace_back(desc_bytes(desc(id)));
     }
 
     void upload_parameters()
@@ -1992,15 +2013,20 @@ private:
     {
         select();
         hip_check(mlvc_hip_zero(arena_.ptr, arena_bytes_, stream_), "arena clear");
-        for (auto& [id, buf] : input_buf_) hip_check(mlvc_hip_zero(buf.ptr, aot::tensor_bytes(desc(id)), stream_), "input clear");
+        for (auto& [id, buf] : input_buf_) hip_check(mlvc_hip_zero(buf.ptr, desc_bytes(desc(id)), stream_), "input clear");
         for (auto& b : bindings_)
             for (auto& buf : b.buf) hip_check(mlvc_hip_zero(buf.ptr, b.bytes, stream_), "state clear");
         constexpr int kWarm = 2, kReps = 5;
         // MLVC_HIP_TUNE_FILE=<path>: choices listed there ("<model>:<launch>
-        // <variant>" per line) are taken without timing, and every choice is
-        // written back, so separate processes (one counter pass each, or a
-        // benchmark and its profile) run the same kernels.
+        // <variant>" per line) are taken without timing, so separate
+        // processes (one counter pass each, or a benchmark and its profile)
+        // run the same kernels. The file is only read, unless
+        // MLVC_HIP_TUNE_WRITE=1 asks for every choice to be written back
+        // (to a temporary file renamed into place, so a reader never sees a
+        // partial file).
         const char* tune_file = std::getenv("MLVC_HIP_TUNE_FILE");
+        const char* tune_write = std::getenv("MLVC_HIP_TUNE_WRITE");
+        const bool write_back = tune_file && tune_write && std::string(tune_write) == "1";
         std::map<std::string, std::string> chosen;
         if (tune_file) {
             std::ifstream in(tune_file);
@@ -2025,7 +2051,11 @@ private:
                         best = v;
                         best_ms = 0.0F;
                     }
-                if (best_ms == 0.0F) cand.clear();
+                if (best_ms == 0.0F)
+                    cand.clear();
+                else
+                    std::fprintf(stderr, "hip: tuning file names variant %s for %s, which cannot run it; timing the candidates\n",
+                                 it->second.c_str(), key.c_str());
             }
             for (int v : cand) {
                 mlvc_hip_conv_desc d = planned;
@@ -2061,9 +2091,17 @@ private:
             chosen[key] = mlvc_hip_conv_variant_name(best);
         }
         hip_check(mlvc_hip_stream_synchronize(stream_), "stream sync");
-        if (tune_file) {
-            std::ofstream out(tune_file, std::ios::trunc);
-            for (const auto& [launch, variant] : chosen) out << launch << ' ' << variant << '\n';
+        if (write_back) {
+            const std::string tmp = std::string(tune_file) + ".tmp" + std::to_string(static_cast<long>(::getpid()));
+            {
+                std::ofstream out(tmp, std::ios::trunc);
+                for (const auto& [launch, variant] : chosen) out << launch << ' ' << variant << '\n';
+                if (!out.flush()) fail("cannot write tuning file " + tmp);
+            }
+            if (std::rename(tmp.c_str(), tune_file) != 0) {
+                std::remove(tmp.c_str());
+                fail(std::string("cannot replace tuning file ") + tune_file);
+            }
         }
     }
 
@@ -2095,7 +2133,7 @@ private:
     void enqueue_downloads()
     {
         for (std::size_t i = 0; i < ext_out_.size(); ++i)
-            hip_check(mlvc_hip_memcpy_d2h(out_stage_[i].ptr, ptr(ext_out_[i], parity_), aot::tensor_bytes(desc(ext_out_[i])), stream_),
+            hip_check(mlvc_hip_memcpy_d2h(out_stage_[i].ptr, ptr(ext_out_[i], parity_), desc_bytes(desc(ext_out_[i])), stream_),
                       "output download");
     }
 

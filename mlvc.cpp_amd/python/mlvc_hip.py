@@ -85,8 +85,6 @@ def backend_lib() -> C.CDLL:
         lib.mlvc_aot_inspect.argtypes = [C.c_char_p, C.c_char_p, C.POINTER(C.c_int), C.POINTER(C.c_int),
                                          C.POINTER(C.c_uint64), C.POINTER(C.c_uint64)]
         lib.mlvc_model_config_json.argtypes = [C.c_char_p, C.c_char_p, C.c_size_t]
-        lib.mlvc_model_q_index_shift.argtypes = [C.c_char_p, C.c_int, C.POINTER(C.c_int)]
-        lib.mlvc_model_frame_in_gop.argtypes = [C.c_char_p, C.c_int, C.POINTER(C.c_int)]
         lib.mlvc_model_verify_bundle.argtypes = [C.c_char_p]
         _lib = lib
     return _lib
@@ -371,20 +369,6 @@ def model_config(model_dir) -> dict:
     buf = C.create_string_buffer(8192)
     _check(backend_lib().mlvc_model_config_json(str(model_dir).encode(), buf, len(buf)))
     return json.loads(buf.value.decode())
-
-
-def q_index_shift(model_dir, frame: int) -> int:
-    """ModelConfig::q_index_shift (reference core/src/model.cpp:136-147)."""
-    out = C.c_int()
-    _check(backend_lib().mlvc_model_q_index_shift(str(model_dir).encode(), frame, C.byref(out)))
-    return out.value
-
-
-def frame_in_gop(model_dir, frame: int) -> int:
-    """ModelConfig::frame_in_gop (reference core/src/model.cpp:128-135)."""
-    out = C.c_int()
-    _check(backend_lib().mlvc_model_frame_in_gop(str(model_dir).encode(), frame, C.byref(out)))
-    return out.value
 
 
 def verify_bundle(model_dir) -> None:

@@ -4,8 +4,10 @@
 //
 // Same contract as the reference's core/include/mlvc/core/model.hpp:10-46
 // and core/src/model.cpp: ModelConfig (members, validate(), derived feature /
-// latent / hyperprior dimensions, frame_in_gop, q_index_shift),
-// load_model_config and embedded_model_profiles. verify_model_bundle is an
+// latent / hyperprior dimensions), load_model_config and
+// embedded_model_profiles. The reference's per-frame GOP and QP-shift
+// schedule (frame_in_gop, q_index_shift) belongs to the codec pipeline, not
+// to a backend, and is not declared here. verify_model_bundle is an
 // addition: it checks the bundle's artifact list (path, size, SHA-256)
 // against the files.
 
@@ -46,8 +48,6 @@ struct ModelConfig {
     int latent_width() const;
     int hyperprior_height() const;
     int hyperprior_width() const;
-    int frame_in_gop(int absolute_frame) const;
-    int q_index_shift(int frame_index) const;
 };
 
 ModelConfig load_model_config(const ModelAssetReader& assets);

@@ -103,7 +103,6 @@ struct LoadedGraph {
 };
 
 std::size_t dtype_bytes(DataType dtype);
-std::size_t tensor_bytes(const TensorDescriptor& tensor);
 
 GraphDescriptor decode_graph_binary(std::span<const std::byte> bytes);
 LoadedGraph load_aot_graph(const ModelAssetReader& assets, const std::string& model_name);

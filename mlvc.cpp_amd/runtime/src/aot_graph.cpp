@@ -224,14 +224,6 @@ std::size_t dtype_bytes(DataType dtype)
     }
 }
 
-std::size_t tensor_bytes(const TensorDescriptor& t)
-{
-    std::size_t n = dtype_bytes(t.dtype);
-    for (const std::int64_t d : t.shape)
-        n *= static_cast<std::size_t>(d);
-    return n;
-}
-
 GraphDescriptor decode_graph_binary(std::span<const std::byte> bytes)
 {
     return decode(wire::parse_model_file(bytes, "graph.pb", wire::parse_graph));

@@ -86,24 +86,6 @@ int ModelConfig::hyperprior_width() const
     return divide_up(model_width, static_cast<std::int64_t>(downsample_latent) * downsample_hyperprior);
 }
 
-// Frame number within its GOP: periodic I-frames restart the count.
-int ModelConfig::frame_in_gop(int absolute_frame) const
-{
-    if (absolute_frame < 0) throw std::runtime_error("frame index must be non-negative");
-    return iframe_period && *iframe_period > 0 ? absolute_frame % *iframe_period : absolute_frame;
-}
-
-// QP shift of a frame (model.cpp:130-142): the map is read one entry ahead,
-// cyclically, so frame 0 takes entry 1 and the last frame of a cycle entry 0.
-int ModelConfig::q_index_shift(int frame_index) const
-{
-    if (frame_index < 0) throw std::runtime_error("frame index must be non-negative");
-    if (frame_index_map.empty() || qp_shift.empty()) throw std::runtime_error("model metadata has no QP shift mapping");
-    const std::size_t n = frame_index_map.size();
-    const std::size_t entry = (static_cast<std::size_t>(frame_index) % n + 1U) % n;
-    return qp_shift.at(static_cast<std::size_t>(frame_index_map.at(entry)));
-}
-
 ModelConfig load_model_config(const ModelAssetReader& assets)
 {
     const wire::ModelMetadata m = read_metadata(assets);

@@ -343,10 +343,13 @@ void build_ops_zoo(GraphBuilder& g, Rng& rng, SyntheticModel& info)
     // input, INT64 channel and column indices.
     const Id row = g.gather("q_row", w16("table", {72, 24, 1, 1}, 0.5, 1.5), q, 0);       // [1,24,1,1]
     const Id gq = g.binary(Op::MUL, "q_scaled", x, row);
-    const Id gi = g.gather("chan_pick", gq, g.weight_int64("chan_pick/idx", {3}, {5, -1, 0}), 1);   // [1,3,12,20]
+    const Id pick = g.weight_int64("chan_pick/idx", {3}, {5, -1, 0});
+    const Id gi = g.gather("chan_pick", gq, pick, 1);                                     // [1,3,12,20]
     const Id gw = g.gather("col_pick", k2, g.weight_int64("col_pick/idx", {2}, {19, 3}), 3);        // [1,24,18,2]
+    // A second GATHER sharing the first one's index initializer.
+    const Id gs = g.gather("chan_pick_shared", b2, pick, 1);                              // [1,3,12,20]
     const Id bz = g.binary(Op::MUL, "z_batch", k4, w16("zb", {4, 1, 1, 1}, -1, 1));
-    for (Id o : {k1, s2, k3, gi, gw, bz}) g.output(o);
+    for (Id o : {k1, s2, k3, gi, gw, bz, gs}) g.output(o);
     info.external_inputs = {{1, 24, 12, 20}, {1}, {2, 8, 6, 10}};
     info.external_input_names = {"x", "q_index_shifted", "z"};
     info.input_lo = {-2.0, 0.0, -2.0};

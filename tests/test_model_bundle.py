@@ -2,9 +2,8 @@
 
 Mirrors the reference's expectations:
   - core/src/model.cpp:34-48 (validate_bundle_manifest), :50-91 (ModelConfig::validate),
-    :128-147 (frame_in_gop, q_index_shift), :150-183 (load_model_config);
+    :150-183 (load_model_config);
   - tests/unit/runtime_decoupling_tests.cpp:108-160 (the synthetic 64x64 bundle) and :296-300;
-  - tests/unit/codec_tests.cpp:132-143 (GOP and QP-shift schedule of a 64-frame I-period model);
   - tools/python/mlvc_tools/package.py:97-143 (artifact size and SHA-256 checks).
 
 The metadata and bundle files are written here with a small protobuf encoder (field numbers of
@@ -168,33 +167,6 @@ def test_derived_dimensions_round_up(tmp_path):
     assert c["feature_hw"] == [333, 334] and c["latent_hw"] == [143, 143] and c["hyperprior_hw"] == [29, 29]
 
 
-def test_gop_and_qp_shift_schedule(tmp_path):
-    """codec_tests.cpp:132-143: with a 64-frame I-period, frame_in_gop(0,1,63,64,65) = 0,1,63,0,1 and
-    q_index_shift(frame_in_gop(f)) = 8, 0, 8 for f = 0, 1, 64. The map/shift table here is an 8-entry
-    hierarchical schedule that produces those values (the real model's table is not in the tree)."""
-    d = write_model(tmp_path / "m", iframe_period=64, frame_index_map=[0, 1, 0, 2, 0, 2, 0, 2],
-                    qp_shift=[0, 8, 4], qp_num=64, total_qp_num=72)
-    assert [mlvc_hip.frame_in_gop(d, f) for f in (0, 1, 63, 64, 65)] == [0, 1, 63, 0, 1]
-    assert [mlvc_hip.q_index_shift(d, mlvc_hip.frame_in_gop(d, f)) for f in (0, 1, 64)] == [8, 0, 8]
-    # The entry used for frame f is map[(f % n + 1) % n] (model.cpp:136-147).
-    n = 8
-    table = [0, 1, 0, 2, 0, 2, 0, 2]
-    for f in range(0, 40):
-        assert mlvc_hip.q_index_shift(d, f) == [0, 8, 4][table[(f % n + 1) % n]]
-
-
-def test_no_iframe_period_keeps_absolute_frame(tmp_path):
-    d = write_model(tmp_path / "m", iframe_period=None)
-    assert mlvc_hip.model_config(d)["iframe_period"] is None
-    assert [mlvc_hip.frame_in_gop(d, f) for f in (0, 5, 1000)] == [0, 5, 1000]
-
-
-def test_negative_frame_rejected(tmp_path):
-    d = write_model(tmp_path / "m")
-    assert "frame index must be non-negative" in _error(mlvc_hip.q_index_shift, d, -1)
-    assert "frame index must be non-negative" in _error(mlvc_hip.frame_in_gop, d, -3)
-
-
 # ---- ModelConfig::validate --------------------------------------------------------------------
 
 @pytest.mark.parametrize("overrides,message", [
@@ -299,7 +271,6 @@ def test_synthetic_codec_directory(tmp_path):
     c = mlvc_hip.model_config(d)
     assert c["model_version"] == "synthetic-v1" and c["feature_channels"] == 64
     assert c["frame_index_map"] == [0, 1, 2, 3] and c["qp_shift"] == [0, 8, 4, 8]
-    assert [mlvc_hip.q_index_shift(d, f) for f in range(6)] == [8, 4, 8, 0, 8, 4]
     mlvc_hip.verify_bundle(d)
     for rel in ("aot/MLVCEncoder/graph.pb", "aot/MLVCEncoder/weights.bin", "aot/MLVCDecoder/graph.pb",
                 "aot/MLVCDecoder/weights.bin", "metadata.pb"):
