@@ -360,10 +360,76 @@ void block_scalar(std::size_t m, std::size_t n, std::size_t k, const u16* lhs, s
     }
 }
 
-void run_block(int isa, std::size_t m, std::size_t n, std::size_t k, const u16* lhs, std::size_t lhs_stride,
-               const u16* packed, u16* dst, const Epilogue& e, std::size_t row0)
+// isa 2 (test-only, not a reference path): a model of the GPU kernels' FP32
+// summation order, used to measure how far a different accumulation order
+// alone moves the outputs. The GPU convs take K as (16-channel step, tap):
+// for each step of up to 16 input channels, each tap's 16 products form one
+// v_mfma_f32_32x32x16_f16 step, which adds their sum to the FP32 accumulator.
+// Here each such group is summed in double (the FP16 x FP16 products are
+// exact) and added to the bias-seeded FP32 accumulator with one rounding.
+// The FP16 rounding and the epilogue are the scalar kernel's. This models
+// the order and the rounding points of the matrix-core sum; it does not
+// claim the GPU's bits.
+void block_mfma_order(std::size_t m, std::size_t n, std::size_t k, std::size_t ic, const u16* lhs,
+                      std::size_t lhs_stride, const u16* packed, u16* dst, const Epilogue& e, std::size_t row0,
+                      const double* wconv)
 {
-    if (isa == 0 && n % 16 == 0)
+    const std::size_t blk = 16 + k * 16, taps = k / ic, nblk = (n + 15) / 16;
+    // wconv: the packed weights (without the bias rows) already in double,
+    // [block][k][16]; converted here when the caller has none.
+    thread_local std::vector<double> wd, ad;
+    if (!wconv) {
+        wd.resize(nblk * k * 16);
+        for (std::size_t b = 0; b < nblk; ++b)
+            for (std::size_t i = 0; i < k * 16; ++i) wd[b * k * 16 + i] = h2f(packed[b * blk + 16 + i]);
+        wconv = wd.data();
+    }
+    ad.resize(k);
+    for (std::size_t mi = 0; mi < m; ++mi) {
+        const u16* a = lhs + mi * lhs_stride;
+        for (std::size_t kk = 0; kk < k; ++kk) ad[kk] = h2f(a[kk]);
+        for (std::size_t b = 0; b < nblk; ++b) {
+            const std::size_t vn = std::min<std::size_t>(16, n - b * 16);
+            double acc[16];
+            for (std::size_t j = 0; j < 16; ++j) acc[j] = j < vn ? h2f(packed[b * blk + j]) : 0.0;
+            for (std::size_t c0 = 0; c0 < ic; c0 += 16) {
+                const std::size_t cn = std::min<std::size_t>(16, ic - c0);
+                for (std::size_t t = 0; t < taps; ++t) {
+                    double sum[16] = {};
+                    for (std::size_t i = 0; i < cn; ++i) {
+                        const std::size_t kk = t * ic + c0 + i;
+                        const double av = ad[kk];
+                        const double* wr = wconv + (b * k + kk) * 16;
+                        for (std::size_t j = 0; j < 16; ++j) sum[j] += av * wr[j];
+                    }
+                    for (std::size_t j = 0; j < 16; ++j) acc[j] = static_cast<float>(acc[j] + sum[j]);
+                }
+            }
+            for (std::size_t j = 0; j < vn; ++j) {
+                u16 hv = f2h(static_cast<float>(acc[j]));
+                if (e.kind == kClamp) {
+                    hv = f2h(std::min(std::max(h2f(hv), e.cmin), e.cmax));
+                } else if (e.kind == kLeaky) {
+                    const float fv = h2f(hv);
+                    if (fv < 0.0F) hv = f2h(fv * e.alpha);
+                } else if (e.kind == kResidual && e.residual) {
+                    hv = f2h(h2f(hv) + h2f(e.residual[(row0 + mi) * n + b * 16 + j]));
+                }
+                dst[mi * n + b * 16 + j] = hv;
+            }
+        }
+    }
+}
+
+// ic: input channels per tap (k / ic taps) and wconv: the weights in double
+// (or null); only the isa 2 model uses them.
+void run_block(int isa, std::size_t m, std::size_t n, std::size_t k, const u16* lhs, std::size_t lhs_stride,
+               const u16* packed, u16* dst, const Epilogue& e, std::size_t row0, std::size_t ic = 0,
+               const double* wconv = nullptr)
+{
+    if (isa == 2)
+        block_mfma_order(m, n, k, ic ? ic : k, lhs, lhs_stride, packed, dst, e, row0, wconv);
+    else if (isa == 0 && n % 16 == 0)
         block_avx2(m, n, k, lhs, lhs_stride, packed, dst, e, row0);
     else
         block_scalar(m, n, k, lhs, lhs_stride, packed, dst, e, row0);
@@ -372,20 +438,20 @@ void run_block(int isa, std::size_t m, std::size_t n, std::size_t k, const u16* 
 constexpr std::size_t kRows = 24;
 
 void gemm_nhwc(Pool& pool, int isa, std::size_t m, std::size_t n, std::size_t k, const u16* lhs,
-               const u16* packed, u16* dst, const Epilogue& e)
+               const u16* packed, u16* dst, const Epilogue& e, const double* wconv = nullptr)
 {
     const std::size_t tiles = (m + kRows - 1) / kRows;
     pool.parallel_for(tiles, 1, [&](std::size_t t0, std::size_t t1) {
         for (std::size_t t = t0; t < t1; ++t) {
             const std::size_t m0 = t * kRows, mc = std::min(kRows, m - m0);
-            run_block(isa, mc, n, k, lhs + m0 * k, k, packed, dst + m0 * n, e, m0);
+            run_block(isa, mc, n, k, lhs + m0 * k, k, packed, dst + m0 * n, e, m0, k, wconv);
         }
     });
 }
 
 void spatial_conv_nhwc(Pool& pool, int isa, const u16* in, const u16* packed, u16* out, int bn, int ic,
                        int ih, int iw, int oc, int oh, int ow, int kh, int kw, int sh, int sw, int ph,
-                       int pw, const Epilogue& e)
+                       int pw, const Epilogue& e, const double* wconv = nullptr)
 {
     const std::size_t total = static_cast<std::size_t>(bn) * oh * ow;
     const std::size_t kdim = static_cast<std::size_t>(kh) * kw * ic;
@@ -412,7 +478,7 @@ void spatial_conv_nhwc(Pool& pool, int isa, const u16* in, const u16* packed, u1
                     }
             }
             run_block(isa, mc, static_cast<std::size_t>(oc), kdim, col.data(), kdim, packed,
-                      out + m0 * static_cast<std::size_t>(oc), e, m0);
+                      out + m0 * static_cast<std::size_t>(oc), e, m0, static_cast<std::size_t>(ic), wconv);
         }
     });
 }
@@ -1057,6 +1123,7 @@ struct ConvInfo {
     bool depthwise = false, is1x1 = false;
     int n = 0, ic = 0, ih = 0, iw = 0, oc = 0, oh = 0, ow = 0, kh = 0, kw = 0, sh = 1, sw = 1, ph = 0, pw = 0;
     std::vector<u16> packed;
+    std::vector<double> wconv;  // isa 2 only: the packed weights in double, [16-column block][k][16]
 };
 // FusedStepKind of fusion_matcher.hpp:12-20.
 enum StepKind { kSingle = 0, kConvEpi = 1, kRegluStep = 2, kFeature = 3, kFeatureOutputs = 4, kY0 = 5, kY1 = 6 };
@@ -1077,8 +1144,9 @@ class Plan {
 public:
     Plan(const std::string& dir, const std::string& model, const std::vector<std::pair<std::size_t, std::size_t>>& bind,
          int threads, int isa, bool fuse)
-        : pool_(threads > 0 ? threads : default_threads()), isa_(isa)
+        : pool_(threads > 0 ? threads : default_threads()), isa_(isa == 2 ? 0 : isa), conv_isa_(isa)
     {
+        if (isa < 0 || isa > 2) throw std::runtime_error("oracle: isa must be 0, 1 or 2");
         g_ = parse_graph(read_file(dir + "/aot/" + model + "/graph.pb"));
         weights_ = read_file(dir + "/aot/" + model + "/weights.bin");
         bufs_.resize(g_.t.size());
@@ -1194,6 +1262,12 @@ private:
             c.is1x1 = c.kh == 1 && c.kw == 1 && c.sh == 1 && c.sw == 1 && c.ph == 0 && c.pw == 0;
             c.packed.resize(packed_conv_elems(static_cast<std::size_t>(c.oc), static_cast<std::size_t>(c.ic), static_cast<std::size_t>(c.kh), static_cast<std::size_t>(c.kw)));
             pack_conv(w.data(), b.empty() ? nullptr : b.data(), static_cast<std::size_t>(c.oc), static_cast<std::size_t>(c.ic), static_cast<std::size_t>(c.kh), static_cast<std::size_t>(c.kw), c.packed.data());
+            if (conv_isa_ == 2) {
+                const std::size_t k = static_cast<std::size_t>(c.kh) * c.kw * c.ic, nblk = (static_cast<std::size_t>(c.oc) + 15) / 16;
+                c.wconv.resize(nblk * k * 16);
+                for (std::size_t bb = 0; bb < nblk; ++bb)
+                    for (std::size_t i = 0; i < k * 16; ++i) c.wconv[bb * k * 16 + i] = h2f(c.packed[bb * (16 + k * 16) + 16 + i]);
+            }
         } else if (groups == c.ic && c.oc == c.ic && ws[1] == 1) {
             c.depthwise = true;
             c.packed.resize(packed_dw_elems(static_cast<std::size_t>(c.ic), static_cast<std::size_t>(c.kh), static_cast<std::size_t>(c.kw)));
@@ -1718,9 +1792,11 @@ private:
         if (c.depthwise) {
             depthwise_nhwc(pool_, isa_, ip, c.packed.data(), op, c.n, c.ic, c.ih, c.iw, c.oh, c.ow, c.kh, c.kw, c.sh, c.sw, c.ph, c.pw);
         } else if (c.is1x1) {
-            gemm_nhwc(pool_, isa_, static_cast<std::size_t>(c.n) * c.oh * c.ow, static_cast<std::size_t>(c.oc), static_cast<std::size_t>(c.ic), ip, c.packed.data(), op, e);
+            gemm_nhwc(pool_, conv_isa_, static_cast<std::size_t>(c.n) * c.oh * c.ow, static_cast<std::size_t>(c.oc), static_cast<std::size_t>(c.ic), ip, c.packed.data(), op, e,
+                      c.wconv.empty() ? nullptr : c.wconv.data());
         } else {
-            spatial_conv_nhwc(pool_, isa_, ip, c.packed.data(), op, c.n, c.ic, c.ih, c.iw, c.oc, c.oh, c.ow, c.kh, c.kw, c.sh, c.sw, c.ph, c.pw, e);
+            spatial_conv_nhwc(pool_, conv_isa_, ip, c.packed.data(), op, c.n, c.ic, c.ih, c.iw, c.oc, c.oh, c.ow, c.kh, c.kw, c.sh, c.sw, c.ph, c.pw, e,
+                              c.wconv.empty() ? nullptr : c.wconv.data());
         }
     }
 
@@ -1849,6 +1925,7 @@ private:
 
     Pool pool_;
     int isa_;
+    int conv_isa_;  // isa_, or 2 for the GPU summation-order model (groups == 1 convs only)
     Graph g_;
     std::vector<std::uint8_t> weights_;
     std::vector<std::vector<u16>> bufs_;

@@ -26,7 +26,11 @@ extern "C" {
 const char* oracle_last_error(void);
 
 /* ISA selector: 0 = AVX2+FMA+F16C path (reference default on x86),
- * 1 = scalar path (reference MLVC_CPU_ISA=scalar). */
+ * 1 = scalar path (reference MLVC_CPU_ISA=scalar),
+ * 2 = not a reference path: the AVX2 plan with every groups == 1 conv summed
+ *     in the GPU kernels' order (16-channel steps, taps inside, each group of
+ *     16 products added to the FP32 accumulator with one rounding). Used
+ *     only to measure the effect of summation order alone. */
 
 /* ---- graph level: CpuExecutionPlan (execution_plan.cpp:241-254) ---- */
 /* bindings: n_bindings pairs (graph input index, graph output index). */

@@ -79,8 +79,16 @@ def test_recurrent_teacher_forced(tmp_path, config, frames):
     gpu.close()
 
 
-# Free-running bound of the 1920x1088 graph: twice the per-frame FP16 bar.
-DRIFT_MAX_REL, DRIFT_MEAN_REL = 2e-2, 2e-3
+# Free-running bound of the 1920x1088 graph, from summation order alone. The
+# oracle's GPU-order model (isa 2: each conv summed as 16-channel steps with
+# taps inside, every 16-product group added to the FP32 accumulator once),
+# run free-running against the reference order on the CPU over these 32
+# frames, levels at recon mean |d|/RMS 1.33e-3-1.34e-3 from frame ~12 with
+# max |d|/RMS <= 1.06e-2; teacher-forced it gives 6.8e-4 recon / 4.0e-4
+# state, as the GPU does (tests/test_oracle_order_drift.py runs the same
+# comparison on the 640x368 graph). The bounds are those figures with 12%
+# (mean) and 40% (max) headroom.
+DRIFT_MAX_REL, DRIFT_MEAN_REL = 1.5e-2, 1.5e-3
 
 
 def test_mlvc_1920x1088_free_running(tmp_path):
@@ -88,11 +96,14 @@ def test_mlvc_1920x1088_free_running(tmp_path):
     recurrent state. Frame 0 (both states zero) meets the FP16 bar. After it
     each side feeds its own FP16 rounding back through the 64-channel state,
     so the difference grows for about ten frames and then levels off (recon
-    mean |d| about 1.3e-3 of RMS, against a flat 6.8e-4 when the GPU is fed
+    mean |d| about 1.33e-3 of RMS, against a flat 6.8e-4 when the GPU is fed
     the oracle's state every frame, which test_recurrent_teacher_forced holds
-    to the FP16 bar). Every frame stays within twice the bar, and the last
-    eight frames' mean error is no larger than the eight before them, give or
-    take 5%: the drift is bounded, not growing."""
+    to the FP16 bar). A CPU model of the GPU's summation order shows the same
+    curve against the reference order, so the excess over the per-frame bar
+    is summation order fed back through the state, not a bias of one layer.
+    Every frame stays within the order-only bound above, and the last eight
+    frames' mean error is no larger than the eight before them, give or take
+    5%: the drift is bounded, not growing."""
     config = "mlvc_1920x1088"
     bindings, _ = _write(tmp_path, config)
     gpu = mlvc_hip.Backend(tmp_path, "hip")
