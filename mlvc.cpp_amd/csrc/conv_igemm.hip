@@ -133,6 +133,11 @@ bool eligible(const mlvc_hip_conv_desc& d, const Variant& k)
     // ReGLU pairs gate and linear rows inside 64-row blocks of one tile.
     if (d.epilogue == MLVC_EPI_REGLU && k.bm % 64 != 0) return false;
     if (d.kh == 1 && (d.pad_h || d.pad_w)) return false;
+    // The weight-streaming kernel: plain NCHW input staged as 16-byte rows,
+    // no ReGLU, DEPTH_TO_SPACE(2) or none, 8-aligned output rows.
+    if (k.ws_ic && (d.x2 || d.in_s2d_block > 1 || d.epilogue == MLVC_EPI_REGLU || d.out_d2s_block > 2 ||
+                    d.iw % 8 != 0 || d.ow % 8 != 0))
+        return false;
     int ih, iw, oh, ow;
     kernel_geometry(d, ih, iw, oh, ow);
     const bool flat = ih == 1 && oh == 1 && d.kh == 1 && d.kw == 1;
@@ -303,6 +308,7 @@ int mlvc_hip_conv_launch(const mlvc_hip_conv_desc* desc, mlvc_hip_stream s)
             const std::uint64_t src_plane = static_cast<std::uint64_t>(a.ih) * a.iw * 4 * 2;
             const bool s2d_vec = k.launch_s2d && a.s2d == 2 && (reinterpret_cast<std::uintptr_t>(d.x) & 15u) == 0 &&
                                  a.iw % 8 == 0 && (static_cast<std::uint64_t>(d.ic / 4) + k.kc / 4 + 1) * src_plane < (1ull << 31);
+            if (k.ws_ic && !vec) throw std::runtime_error("conv: variant needs 16-byte row staging");
             (s2d_vec ? k.launch_s2d : vec ? k.launch_vec : k.launch_scalar)(a, grid, to_stream(s));
         }
         check(hipGetLastError(), "conv kernel launch");

@@ -1,6 +1,6 @@
 // 3x3 stride-1 tile variants of the MFMA conv kernel (conv_kernel.hpp).
 
-#include "conv_kernel.hpp"
+#include "conv_ws.hpp"
 
 namespace mlvc_hip {
 namespace conv {
@@ -36,6 +36,14 @@ const Variant kTable[] = {
     MLVC_VARIANT_DB(128, 8, 32, 3, 3, 1, 16),
     MLVC_VARIANT_DB(128, 4, 64, 3, 3, 1, 16),
     MLVC_VARIANT_DB(64, 4, 64, 3, 3, 1, 16),
+    MLVC_VARIANT_OCC(32, 2, 64, 3, 3, 1, 16, 4),
+    MLVC_VARIANT_WO(32, 2, 32, 3, 3, 1, 16, 1, 2, 4),
+    MLVC_VARIANT_WO(64, 2, 32, 3, 3, 1, 16, 1, 2, 4),
+    MLVC_VARIANT_WS(256, 4, 32, 128, 2),
+    MLVC_VARIANT_WS(128, 4, 32, 128, 2),
+    MLVC_VARIANT_WS(256, 4, 32, 64, 2),
+    MLVC_VARIANT_WS(128, 4, 32, 64, 2),
+    MLVC_VARIANT_WS(256, 2, 32, 128, 2),
 };
 }  // namespace
 

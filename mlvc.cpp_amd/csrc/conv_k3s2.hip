@@ -18,6 +18,10 @@ const Variant kTable[] = {
     MLVC_VARIANT(128, 2, 64, 3, 3, 2, 16),
     MLVC_VARIANT(64, 4, 32, 3, 3, 2, 32),
     MLVC_VARIANT(64, 8, 16, 3, 3, 2, 32),
+    MLVC_VARIANT_WO(32, 2, 32, 3, 3, 2, 16, 1, 2, 4),
+    MLVC_VARIANT_WO(64, 2, 32, 3, 3, 2, 16, 1, 2, 4),
+    MLVC_VARIANT_WO(64, 2, 32, 3, 3, 2, 16, 2, 1, 4),
+    MLVC_VARIANT_OCC(32, 2, 64, 3, 3, 2, 16, 4),
 };
 }  // namespace
 

@@ -320,11 +320,11 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
 #pragma unroll
         for (int i = 0; i < C::UNITS_PER_T; ++i) {
             const int u = tid + i * C::kThreads;
-            const int yi = u % C::IH_T, sg = (u / C::IH_T) % C::NSEG;
+            const int sg = u % C::NSEG, yi = (u / C::NSEG) % C::IH_T;
             const int iy = iy0 + yi, ix = xa + sg * 8;
             const bool ok = u < C::UNITS && iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw;
             pix_off[i] = ok ? static_cast<std::uint32_t>(iy * a.iw + ix) * 2u : kOutOfRange;
-            unit_c8[i] = u / (C::NSEG * C::IH_T);  // units: rows fastest, then segments, then channel groups
+            unit_c8[i] = u / (C::NSEG * C::IH_T);  // units: segments fastest, then rows, then channel groups
         }
     }
     auto fetch = [&](int chunk, int stage) {
@@ -422,7 +422,7 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
             for (int i = 0; i < C::UNITS_PER_T; ++i) {
                 const int u = tid + i * C::kThreads;
                 if (u < C::UNITS) {
-                    const int yi = u % C::IH_T, sg = (u / C::IH_T) % C::NSEG, c8 = u / (C::NSEG * C::IH_T);
+                    const int sg = u % C::NSEG, yi = (u / C::NSEG) % C::IH_T, c8 = u / (C::NSEG * C::IH_T);
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
                         const bool up = j & 1;
@@ -681,6 +681,9 @@ struct Variant {
     void (*launch_scalar)(const ConvArgs&, dim3, hipStream_t);
     void (*launch_vec)(const ConvArgs&, dim3, hipStream_t);
     void (*launch_s2d)(const ConvArgs&, dim3, hipStream_t);  // SPACE_TO_DEPTH(2) staging, or null
+    // Weight-streaming kernel (conv_ws.hpp) staging ws_ic input channels
+    // per pass; 0 for conv_mfma_kernel variants.
+    int ws_ic = 0;
 };
 
 template <class C>
@@ -702,6 +705,11 @@ void launch_mfma(const ConvArgs& a, dim3 grid, hipStream_t s)
     Variant{"mfma_bm" #BM "_" #TH "x" #TW "_k" #KH "x" #KW "_s" #S "_kc" #KC "_occ" #OCC, BM, TH, TW, KH, KW, S, KC,  \
             &launch_mfma<Cfg<BM, TH, TW, KH, KW, S, KC, 0, false, 1, 4, OCC>>,                                      \
             &launch_mfma<Cfg<BM, TH, TW, KH, KW, S, KC, 1, false, 1, 4, OCC>>, nullptr}
+// Waves and occupancy both set (small tiles: more workgroups per CU).
+#define MLVC_VARIANT_WO(BM, TH, TW, KH, KW, S, KC, WM, WNW, OCC)                                                    \
+    Variant{"mfma_bm" #BM "_" #TH "x" #TW "_k" #KH "x" #KW "_s" #S "_kc" #KC "_w" #WM "x" #WNW "_occ" #OCC, BM, TH, \
+            TW, KH, KW, S, KC, &launch_mfma<Cfg<BM, TH, TW, KH, KW, S, KC, 0, false, WM, WNW, OCC>>,                      \
+            &launch_mfma<Cfg<BM, TH, TW, KH, KW, S, KC, 1, false, WM, WNW, OCC>>, nullptr}
 // With SPACE_TO_DEPTH(2) vector staging.
 #define MLVC_VARIANT_S2D(BM, TH, TW, KH, KW, S, KC)                                                          \
     Variant{"mfma_bm" #BM "_" #TH "x" #TW "_k" #KH "x" #KW "_s" #S "_kc" #KC, BM, TH, TW, KH, KW, S, KC,        \

@@ -1,0 +1,289 @@
+// Weight-streaming MFMA implicit GEMM for the MFMA-bound KxK convs.
+//
+//   D[oc, p] = bias[oc] + sum_k W[oc, k] X[k, p],  k = (16-channel step, tap)
+//
+// Same product order and rounding as conv_mfma_kernel (conv_kernel.hpp), so
+// every variant of a kernel size gives the same bits; different data flow:
+//   * the input halo of the tile is staged into LDS channel-last,
+//     [row][pixel][SC + 8], SC channels per pass (all of them in one pass
+//     when IC <= SC), from 16-byte NCHW row segments transposed in
+//     registers; the K loop then runs all (16-channel step, tap) steps of
+//     the pass with no barrier;
+//   * the waves split the output channels (wave w owns m-tiles
+//     w*MT .. w*MT + MT - 1) and each streams its own A fragments (weights
+//     pre-packed in fragment order, [ocb][c16][tap][m-tile][lane][8]) from
+//     L2 straight into a register ring three steps deep, so weights never
+//     pass through LDS and no two waves of a workgroup fetch the same ones;
+//   * every wave covers all BN pixels, reading its B fragments from the
+//     staged halo;
+//   * two workgroups per CU (halo <= 80 KB, 128 accumulator registers), so
+//     one workgroup's staging and epilogue overlap the other's MFMAs.
+// The conv kernel it competes with stages 16 input channels of weights and
+// input per chunk through registers and LDS with two barriers each; per
+// 128x256 tile that re-reads every weight once per 16 channels for each
+// workgroup, which phase timing showed to be 70% of its staging traffic.
+
+#pragma once
+
+#include "conv_kernel.hpp"
+
+namespace mlvc_hip {
+namespace conv {
+
+template <int BM_, int TH_, int TW_, int SC_, int OCC_ = 2>
+struct WsCfg {
+    static constexpr int BM = BM_, TH = TH_, TW = TW_, SC = SC_, OCC = OCC_;
+    static constexpr int KH = 3, KW = 3, TAPS = 9, S = 1;
+    static constexpr int WAVES = 4, kThreads = 256;
+    static constexpr int BN = TH * TW, MTT = BM / 32, MT = MTT / WAVES, NT = BN / 32;
+    static constexpr int IH_T = TH + 2, IW_T = TW + 2;
+    static constexpr int NSEG = (IW_T + 14) / 8, IW_S = NSEG * 8;
+    static constexpr int PST = SC + 8;               // halves per staged pixel
+    static constexpr int ROW = IW_S * PST + 8;       // rows start 4 banks apart
+    static constexpr int IN_LDS = IH_T * ROW;
+    static constexpr int UNITS = (SC / 8) * IH_T * NSEG;  // 8 channels x 8 columns each
+    static constexpr int UNITS_PER_T = (UNITS + kThreads - 1) / kThreads;
+    static constexpr int EPI_ROW = BN + 8, EPI_LDS = BM * EPI_ROW;
+    static constexpr int D2S_LDS = BM * BN;  // [BM/4][2TH][2TW]
+    static constexpr int EPI_MAX = EPI_LDS > D2S_LDS ? EPI_LDS : D2S_LDS;
+    static constexpr int LDS = IN_LDS > EPI_MAX ? IN_LDS : EPI_MAX;
+    static constexpr int RING = 3;                   // A-fragment prefetch distance in k-steps
+    static_assert(BM % 128 == 0 && MT >= 1 && BN % 32 == 0 && TW % 8 == 0 && SC % 16 == 0, "tile shape");
+    static_assert(TAPS % RING == 0, "ring slots are static per tap");
+    static_assert(LDS * 2 * OCC <= 160 * 1024, "LDS budget");
+    __device__ static constexpr int at(int row, int x) { return row * ROW + x * PST; }
+};
+
+template <class C>
+__global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::OCC))) void conv_ws_kernel(ConvArgs a)
+{
+    __shared__ __attribute__((aligned(16))) std::uint16_t lds[C::LDS];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int item = xcd_order(blockIdx.x, a.nwg);
+    const int ocb = item % a.ocbs, tile = (item / a.ocbs) % a.tiles, b = item / (a.ocbs * a.tiles);
+    const int tx0 = (tile % a.tiles_x) * C::TW, ty0 = (tile / a.tiles_x) * C::TH;
+    const int iy0 = ty0 - a.ph, ix0 = tx0 - a.pw;
+    const int xa = ix0 - (((ix0 % 8) + 8) % 8);  // first staged column, 8-aligned
+    const int col_off = ix0 - xa;
+    const int mt0 = wave * C::MT, hsel = 4 * (lane >> 5);
+    const int nsteps16 = a.nchunks;  // 16-channel steps over all input channels
+
+    // Halo of channels [cb, cb + SC) into LDS, 16-byte NCHW row segments
+    // transposed in registers. Unit u: 8 consecutive channels x 8 columns of
+    // one halo row (segments fastest, then rows, then channel groups). Raw
+    // buffer loads: rows and columns outside the image and channels past IC
+    // read zeros.
+    const size_t hw = static_cast<size_t>(a.ih) * a.iw;
+    const std::uint32_t hw2 = static_cast<std::uint32_t>(hw) * 2u;
+    const std::uint16_t* x_img = a.x + static_cast<size_t>(b) * a.ic * hw;
+    const __amdgpu_buffer_rsrc_t rx =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<std::uint16_t*>(x_img), 0, static_cast<int>(a.ic * hw2), kRawBufferFlags);
+    auto stage = [&](int cb) {
+        constexpr int BATCH = 2;  // units in flight per thread (bounds the staging registers)
+#pragma unroll
+        for (int i0 = 0; i0 < C::UNITS_PER_T; i0 += BATCH) {
+            u32x4 v[BATCH][8];
+#pragma unroll
+            for (int ii = 0; ii < BATCH; ++ii) {
+                const int u = tid + (i0 + ii) * C::kThreads;
+                const int sg = u % C::NSEG, yi = (u / C::NSEG) % C::IH_T, c8 = u / (C::NSEG * C::IH_T);
+                const int iy = iy0 + yi, ix = xa + sg * 8;
+                const bool ok = i0 + ii < C::UNITS_PER_T && u < C::UNITS && iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw;
+                const std::uint32_t off =
+                    ok ? static_cast<std::uint32_t>(iy * a.iw + ix) * 2u + static_cast<std::uint32_t>(cb + c8 * 8) * hw2 : kOutOfRange;
+#pragma unroll
+                for (int k = 0; k < 8; ++k)
+                    v[ii][k] = __builtin_amdgcn_raw_buffer_load_b128(rx, static_cast<int>(off == kOutOfRange ? off : off + k * hw2), 0, 0);
+            }
+#pragma unroll
+            for (int ii = 0; ii < BATCH; ++ii) {
+                const int u = tid + (i0 + ii) * C::kThreads;
+                if (i0 + ii >= C::UNITS_PER_T || u >= C::UNITS) continue;
+                const int sg = u % C::NSEG, yi = (u / C::NSEG) % C::IH_T, c8 = u / (C::NSEG * C::IH_T);
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const bool up = j & 1;
+                    const int wd = j >> 1;
+                    const u32x4 t = {pack_half(v[ii][0][wd], v[ii][1][wd], up), pack_half(v[ii][2][wd], v[ii][3][wd], up),
+                                     pack_half(v[ii][4][wd], v[ii][5][wd], up), pack_half(v[ii][6][wd], v[ii][7][wd], up)};
+                    *reinterpret_cast<u32x4*>(&lds[C::at(yi, sg * 8 + j) + c8 * 8]) = t;
+                }
+            }
+        }
+    };
+
+    // A fragment (step, m-tile) of this wave, steps s = c16 * 9 + tap; a
+    // ring RING steps deep that runs on across staging passes.
+    const u32x4* wbase = reinterpret_cast<const u32x4*>(a.w) +
+                         (static_cast<size_t>(ocb) * nsteps16 * C::TAPS * C::MTT + mt0) * 64 + lane;
+    auto frag = [&](int s, int mt) { return wbase[(static_cast<size_t>(s) * C::MTT + mt) * 64]; };
+    const int total = nsteps16 * C::TAPS;
+
+    stage(0);
+    u32x4 ring[C::RING][C::MT];
+#pragma unroll
+    for (int s = 0; s < C::RING; ++s)
+#pragma unroll
+        for (int mt = 0; mt < C::MT; ++mt) ring[s][mt] = frag(s, mt);
+    floatx16 acc[C::MT][C::NT];
+#pragma unroll
+    for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const floatx4 bv = *reinterpret_cast<const floatx4*>(a.bias + ocb * C::BM + (mt0 + mt) * 32 + 8 * j + hsel);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int nt = 0; nt < C::NT; ++nt) acc[mt][nt][4 * j + i] = bv[i];
+        }
+    int pbase[C::NT];
+#pragma unroll
+    for (int nt = 0; nt < C::NT; ++nt) {
+        const int p = nt * 32 + (lane & 31);
+        pbase[nt] = C::at(p / C::TW, p % C::TW + col_off) + (lane >> 5) * 8;
+    }
+    __syncthreads();
+
+    // ---- K loop: 16-channel step outer, tap inner, in passes of SC channels;
+    // no barrier inside a pass.
+    for (int cb = 0; cb < nsteps16 * 16; cb += C::SC) {
+        if (cb > 0) {
+            __syncthreads();  // every wave is done with the previous pass's halo
+            stage(cb);
+            __syncthreads();
+        }
+        const int c16_end = min(nsteps16, (cb + C::SC) / 16);
+        for (int c16 = cb / 16; c16 < c16_end; ++c16) {
+            const int coff = c16 * 16 - cb;
+#pragma unroll
+            for (int tap = 0; tap < C::TAPS; ++tap) {
+                const int s = c16 * C::TAPS + tap;
+                const int ky = tap / C::KW, kx = tap % C::KW;
+                half8 bv[C::NT];
+#pragma unroll
+                for (int nt = 0; nt < C::NT; ++nt)
+                    bv[nt] = *reinterpret_cast<const half8*>(&lds[pbase[nt] + C::at(ky, kx) + coff]);
+                half8 av[C::MT];
+#pragma unroll
+                for (int mt = 0; mt < C::MT; ++mt) {
+                    av[mt] = __builtin_bit_cast(half8, ring[tap % C::RING][mt]);
+                    if (s + C::RING < total) ring[tap % C::RING][mt] = frag(s + C::RING, mt);
+                }
+#pragma unroll
+                for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+                    for (int nt = 0; nt < C::NT; ++nt)
+                        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[mt], bv[nt], acc[mt][nt], 0, 0, 0);
+            }
+        }
+    }
+
+    // ---- epilogue (as conv_mfma_kernel): round, then the epilogue on the
+    // rounded value. Lane l of accumulator (mt, nt) holds channels oc0 + i,
+    // oc0 = ocb*BM + (mt0+mt)*32 + 8j + 4*(l/32), of tile pixel nt*32 + l%32.
+    // The result goes through LDS and leaves as 16-byte rows: plain outputs
+    // as [channel][pixel]; with DEPTH_TO_SPACE(2) the 4 channels of a lane
+    // are the (dy, dx) block of output channel oc0/4, staged as
+    // [channel][2*TH rows][2*TW columns].
+    const bool max_form = a.alpha >= 0.0f && a.alpha <= 1.0f;
+    __syncthreads();  // every wave is done reading the halo
+    if (a.d2s == 2) {
+        constexpr int W2 = 2 * C::TW, ROWS = 2 * C::TH;
+#pragma unroll
+        for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < C::NT; ++nt) {
+                const int p = nt * 32 + (lane & 31), py = p / C::TW, px = p % C::TW;
+                const int oy = ty0 + py, ox = tx0 + px;
+                const bool inside = oy < a.oh && ox < a.ow;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int ocl = (mt0 + mt) * 32 + 8 * j + hsel, oc0 = ocb * C::BM + ocl;
+                    const float v[4] = {acc[mt][nt][4 * j], acc[mt][nt][4 * j + 1], acc[mt][nt][4 * j + 2], acc[mt][nt][4 * j + 3]};
+                    std::uint32_t h01, h23;
+                    if (a.epi == MLVC_EPI_LEAKY_RELU) {
+                        h01 = leaky_pair(v[0], v[1], a.alpha, max_form);
+                        h23 = leaky_pair(v[2], v[3], a.alpha, max_form);
+                    } else {
+                        h01 = pack_f16(v[0], v[1]);
+                        h23 = pack_f16(v[2], v[3]);
+                        if (a.epi == MLVC_EPI_CLAMP) {
+                            h01 = clamp_h2(h01, a.lo, a.hi);
+                            h23 = clamp_h2(h23, a.lo, a.hi);
+                        }
+                        if (a.epi == MLVC_EPI_RESIDUAL_ADD && inside) {
+                            std::uint16_t r[4];
+#pragma unroll
+                            for (int i = 0; i < 4; ++i)
+                                r[i] = oc0 + i < a.oc ? a.res[(static_cast<size_t>(b * a.oc + oc0 + i) * a.oh + oy) * a.ow + ox] : 0;
+                            h01 = f2h(lo_f16(h01) + h2f(r[0])) | (static_cast<std::uint32_t>(f2h(hi_f16(h01) + h2f(r[1]))) << 16);
+                            h23 = f2h(lo_f16(h23) + h2f(r[2])) | (static_cast<std::uint32_t>(f2h(hi_f16(h23) + h2f(r[3]))) << 16);
+                        }
+                    }
+                    std::uint16_t* st = &lds[((ocl / 4) * ROWS + 2 * py) * W2 + 2 * px];
+                    *reinterpret_cast<std::uint32_t*>(st) = h01;
+                    *reinterpret_cast<std::uint32_t*>(st + W2) = h23;
+                }
+            }
+        __syncthreads();
+        // 16-byte row pieces: W2/8 per staged row, rows of every channel.
+        constexpr int PIECES = W2 / 8, UNITS = (C::BM / 4) * ROWS * PIECES;
+        const int OW2 = a.ow * 2, OH2 = a.oh * 2, occ = a.oc / 4;
+        for (int u = tid; u < UNITS; u += C::kThreads) {
+            const int pc = u % PIECES, r = (u / PIECES) % ROWS, cl = u / (PIECES * ROWS);
+            const int c = ocb * (C::BM / 4) + cl, gy = 2 * ty0 + r, gx = 2 * tx0 + pc * 8;
+            if (c >= occ || gy >= OH2 || gx >= OW2) continue;
+            *reinterpret_cast<u32x4*>(a.y + (static_cast<size_t>(b * occ + c) * OH2 + gy) * OW2 + gx) =
+                *reinterpret_cast<const u32x4*>(&lds[(cl * ROWS + r) * W2 + pc * 8]);
+        }
+        return;
+    }
+#pragma unroll
+    for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < C::NT; ++nt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+                const int ocl = (mt0 + mt) * 32 + 8 * (r >> 2) + hsel + (r & 3);
+                lds[ocl * C::EPI_ROW + nt * 32 + (lane & 31)] = f2h(acc[mt][nt][r]);
+            }
+    __syncthreads();
+    constexpr int GROUPS = C::BN / 8;
+    for (int u = tid; u < C::BM * GROUPS; u += C::kThreads) {
+        const int g = u % GROUPS, ocl = u / GROUPS, oc = ocb * C::BM + ocl;
+        const int pl = g * 8, oy = ty0 + pl / C::TW, ox = tx0 + pl % C::TW;
+        if (oc >= a.oc || oy >= a.oh || ox >= a.ow) continue;
+        u32x4 h = *reinterpret_cast<const u32x4*>(&lds[ocl * C::EPI_ROW + pl]);
+        const size_t o = (static_cast<size_t>(b * a.oc + oc) * a.oh + oy) * a.ow + ox;
+        if (a.epi == MLVC_EPI_LEAKY_RELU) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) h[k] = leaky_h2(h[k], a.alpha, max_form);
+        } else if (a.epi == MLVC_EPI_CLAMP) {
+#pragma unroll
+            for (int k = 0; k < 4; ++k) h[k] = clamp_h2(h[k], a.lo, a.hi);
+        } else if (a.epi == MLVC_EPI_RESIDUAL_ADD) {
+            const u32x4 r = *reinterpret_cast<const u32x4*>(a.res + o);
+#pragma unroll
+            for (int k = 0; k < 4; ++k)
+                h[k] = f2h(lo_f16(h[k]) + lo_f16(r[k])) | (static_cast<std::uint32_t>(f2h(hi_f16(h[k]) + hi_f16(r[k]))) << 16);
+        }
+        *reinterpret_cast<u32x4*>(a.y + o) = h;
+    }
+}
+
+template <class C>
+void launch_ws(const ConvArgs& a, dim3 grid, hipStream_t s)
+{
+    hipLaunchKernelGGL(conv_ws_kernel<C>, grid, dim3(C::kThreads), 0, s, a);
+}
+
+// Variant entry: weights packed with kc = 16 ([ocb][c16][tap][m-tile][lane][8]);
+// eligible for plain NCHW inputs with 16-byte rows (the vector launch slot),
+// staged SC channels per pass; no scalar or SPACE_TO_DEPTH staging.
+#define MLVC_VARIANT_WS(BM, TH, TW, SC, OCC)                                                                   \
+    Variant{"ws_bm" #BM "_" #TH "x" #TW "_k3x3_s1_sc" #SC "_occ" #OCC, BM, TH, TW, 3, 3, 1, 16, nullptr,          \
+            &launch_ws<WsCfg<BM, TH, TW, SC, OCC>>, nullptr, SC}
+
+}  // namespace conv
+}  // namespace mlvc_hip

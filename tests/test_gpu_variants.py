@@ -43,6 +43,10 @@ CASES = [
     ("many_tiles_1x1", 1, 128, 512, 512, 64, 1, 1, 0, dict(concat_ic=64, epilogue="lrelu")),
 ]
 
+# Geometries the weight-streaming 3x3 kernel (conv_ws.hpp) takes: NCHW inputs
+# with rows of a multiple of 8 pixels, no concat or SPACE_TO_DEPTH staging.
+WS_CASES = {"mid_4x8", "shuffle_8x16", "many_tiles_s1", "many_tiles_d2s", "residual_d2s"}
+
 
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
 def test_every_variant(tmp_path, monkeypatch, case):
@@ -69,3 +73,5 @@ def test_every_variant(tmp_path, monkeypatch, case):
             assert (got == first[1]).all(), f"{name}: {v} differs from {first[0]}"
         ran.append(v)
     assert len(ran) >= 2, ran
+    if name in WS_CASES:  # the weight-streaming kernel is among them
+        assert any(v.startswith("ws_") for v in ran), ran
