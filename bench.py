@@ -144,6 +144,155 @@ def codec_io_kernels(reps: int) -> dict:
             "algorithmic_bytes": {"frame_to_model": to_model_b, "model_to_frame": to_frame_b}}
 
 
+# Standalone bandwidth kernels at the residual-block workload's shapes (C128
+# at 92x160, C256 at 46x80: depthwise 3x3, the 3x3 conv C->4C's pixel
+# shuffle, the pixel unshuffle before a 1x1 conv) and at the 1920x1088
+# graph's shuffle shapes: (name, op, (n, c, h, w) input).
+STANDALONE = [
+    ("dw3x3_c128_92x160", "depthwise", (1, 128, 92, 160)),
+    ("dw3x3_c256_46x80", "depthwise", (1, 256, 46, 80)),
+    ("d2s2_c512_92x160", "depth_to_space", (1, 512, 92, 160)),
+    ("d2s2_c1024_46x80", "depth_to_space", (1, 1024, 46, 80)),
+    ("s2d2_c128_92x160", "space_to_depth", (1, 128, 92, 160)),
+    ("s2d2_c256_46x80", "space_to_depth", (1, 256, 46, 80)),
+    ("dw3x3_c256_68x120", "depthwise", (1, 256, 68, 120)),
+    ("d2s2_c256_272x480", "depth_to_space", (1, 256, 272, 480)),
+    ("d2s2_c12_544x960", "depth_to_space", (1, 12, 544, 960)),
+    ("s2d2_c3_1088x1920", "space_to_depth", (1, 3, 1088, 1920)),
+]
+
+
+def standalone_kernels(reps: int, cold_reps: int) -> dict:
+    """Device-resident timing of the standalone depthwise / DEPTH_TO_SPACE /
+    SPACE_TO_DEPTH kernels through the device C ABI, at STANDALONE's shapes.
+    Warm: HIP events around `reps` back-to-back launches (operands stay in
+    L2 / MALL when they fit). Cold: per launch, a 512 MiB device copy evicts
+    L2 and the MALL outside the events, then events around the one launch
+    (median of `cold_reps`; includes the dispatch latency a lone launch
+    pays). Algorithmic bytes: input and output once (plus the depthwise
+    weights and bias). Beside each kernel, the same two timings of a device
+    copy of its input into its output (the runtime's copy kernel, the same
+    bytes less the depthwise taps): the floor a launch of that size sees."""
+    import ctypes as C
+
+    import numpy as np
+
+    import mlvc_hip
+
+    L = mlvc_hip.device_lib()
+    vp, ci = C.c_void_p, C.c_int
+    L.mlvc_hip_malloc.argtypes = [C.POINTER(vp), C.c_size_t]
+    L.mlvc_hip_free.argtypes = [vp]
+    L.mlvc_hip_memcpy_h2d.argtypes = [vp, vp, C.c_size_t, vp]
+    L.mlvc_hip_memcpy_d2d.argtypes = [vp, vp, C.c_size_t, vp]
+    L.mlvc_hip_stream_create.argtypes = [C.POINTER(vp)]
+    L.mlvc_hip_stream_destroy.argtypes = [vp]
+    L.mlvc_hip_stream_synchronize.argtypes = [vp]
+    L.mlvc_hip_event_create.argtypes = [C.POINTER(vp)]
+    L.mlvc_hip_event_destroy.argtypes = [vp]
+    L.mlvc_hip_event_record.argtypes = [vp, vp]
+    L.mlvc_hip_event_synchronize.argtypes = [vp]
+    L.mlvc_hip_event_elapsed_ms.argtypes = [vp, vp, C.POINTER(C.c_float)]
+    L.mlvc_hip_depthwise.argtypes = [vp, vp, vp, vp] + [ci] * 12 + [vp]
+    L.mlvc_hip_depth_to_space.argtypes = [vp, vp] + [ci] * 5 + [vp]
+    L.mlvc_hip_space_to_depth.argtypes = [vp, vp] + [ci] * 5 + [vp]
+
+    def ok(rc):
+        if rc != 0:
+            raise mlvc_hip.MlvcError(L.mlvc_hip_last_error().decode())
+
+    bufs = []
+
+    def alloc(nbytes):
+        p = vp()
+        ok(L.mlvc_hip_malloc(C.byref(p), max(nbytes, 16)))
+        bufs.append(p)
+        return p
+
+    def put(a):
+        p = alloc(a.nbytes)
+        ok(L.mlvc_hip_memcpy_h2d(p, a.ctypes.data, a.nbytes, None))
+        return p
+
+    rng = np.random.default_rng(3)
+    s, e0, e1 = vp(), vp(), vp()
+    ok(L.mlvc_hip_stream_create(C.byref(s)))
+    ok(L.mlvc_hip_event_create(C.byref(e0)))
+    ok(L.mlvc_hip_event_create(C.byref(e1)))
+    flush = alloc(COLD_FLUSH_BYTES)
+    half = COLD_FLUSH_BYTES // 2
+
+    def elapsed_us():
+        ok(L.mlvc_hip_event_synchronize(e1))
+        ms = C.c_float()
+        ok(L.mlvc_hip_event_elapsed_ms(e0, e1, C.byref(ms)))
+        return ms.value * 1e3
+
+    def timed_warm_cold(launch):
+        cold = []
+        for _ in range(cold_reps):
+            ok(L.mlvc_hip_memcpy_d2d(vp(flush.value + half), flush, half, s))
+            ok(L.mlvc_hip_event_record(e0, s))
+            launch()
+            ok(L.mlvc_hip_event_record(e1, s))
+            cold.append(elapsed_us())
+        for _ in range(3):
+            launch()
+        ok(L.mlvc_hip_event_record(e0, s))
+        for _ in range(reps):
+            launch()
+        ok(L.mlvc_hip_event_record(e1, s))
+        return elapsed_us() / reps, float(np.median(cold)) if cold else None
+
+    rows = []
+    try:
+        for name, op, (n, c, h, w) in STANDALONE:
+            elems = n * c * h * w
+            x = put(rng.uniform(-1, 1, elems).astype(np.float16).view(np.uint16))
+            y = alloc(elems * 2)
+            nbytes = 4 * elems
+            if op == "depthwise":
+                wt = put(rng.normal(0, 1 / 3, c * 9).astype(np.float16).view(np.uint16))
+                bias = put(rng.normal(0, 0.01, c).astype(np.float32))
+                nbytes += c * 9 * 2 + c * 4
+                launch = lambda: ok(L.mlvc_hip_depthwise(x, wt, bias, y, n, c, h, w, h, w, 3, 3, 1, 1, 1, 1, s))
+            elif op == "depth_to_space":
+                launch = lambda: ok(L.mlvc_hip_depth_to_space(x, y, n, c, h, w, 2, s))
+            else:
+                launch = lambda: ok(L.mlvc_hip_space_to_depth(x, y, n, c, h, w, 2, s))
+            copy = lambda: ok(L.mlvc_hip_memcpy_d2d(y, x, elems * 2, s))
+            ok(L.mlvc_hip_stream_synchronize(None))
+            warm_us, cold_us = timed_warm_cold(launch)
+            copy_warm_us, copy_cold_us = timed_warm_cold(copy)
+            rows.append({"name": name, "op": op, "shape": [n, c, h, w], "algorithmic_bytes": nbytes,
+                         "warm_us": warm_us, "warm_gbs": nbytes / warm_us / 1e3,
+                         "warm_hbm_frac": nbytes / warm_us / 1e3 / PEAK_HBM_GBS,
+                         "cold_us": cold_us, "cold_gbs": nbytes / cold_us / 1e3 if cold_us else None,
+                         "cold_hbm_frac": nbytes / cold_us / 1e3 / PEAK_HBM_GBS if cold_us else None,
+                         "copy_warm_us": copy_warm_us, "copy_cold_us": copy_cold_us})
+    finally:
+        ok(L.mlvc_hip_stream_synchronize(s))
+        for p in bufs:
+            L.mlvc_hip_free(p)
+        L.mlvc_hip_event_destroy(e0)
+        L.mlvc_hip_event_destroy(e1)
+        L.mlvc_hip_stream_destroy(s)
+    return {"kernels": rows, "cold_flush_bytes": COLD_FLUSH_BYTES,
+            "workload": "standalone depthwise 3x3 / block-2 DEPTH_TO_SPACE / SPACE_TO_DEPTH at the residual-block "
+                        "shapes (C128 @92x160, C256 @46x80 and their 4C shuffles) and the 1920x1088 graph's shuffle "
+                        "shapes; warm = back-to-back launches, cold = one launch after a cache-evicting copy"}
+
+
+def log_standalone(res: dict) -> None:
+    for k in res["kernels"]:
+        cold = (f"cold {k['cold_us']:7.1f} us {k['cold_gbs']:6.0f} GB/s {k['cold_hbm_frac']:.3f}"
+                if k["cold_us"] is not None else "")
+        copy = (f"  copy warm {k['copy_warm_us']:6.1f} cold {k['copy_cold_us']:6.1f} us"
+                if k["copy_cold_us"] is not None else f"  copy warm {k['copy_warm_us']:6.1f} us")
+        log(f"standalone {k['name']:20} {k['algorithmic_bytes'] / 1e6:8.2f} MB  warm {k['warm_us']:7.1f} us "
+            f"{k['warm_gbs']:6.0f} GB/s {k['warm_hbm_frac']:.3f}  {cold}{copy}")
+
+
 def codec_buffered(frames: int) -> dict:
     """End to end through BufferedCodecBackend at the 1080p frame shape: two
     slots in flight, each submit uploading a pinned frame (encoder) or latent
@@ -352,6 +501,11 @@ def main() -> int:
     ap.add_argument("--codec-frames", type=int, default=60)
     ap.add_argument("--no-realops", action="store_true", help="skip the real-model operator measurements")
     ap.add_argument("--realops-frames", type=int, default=50)
+    ap.add_argument("--no-standalone", action="store_true",
+                    help="skip the standalone depthwise / pixel-shuffle measurements")
+    ap.add_argument("--standalone-only", action="store_true",
+                    help="run only the standalone kernel measurements (for a kernel trace of them); no JSON line")
+    ap.add_argument("--standalone-cold", type=int, default=20, help="cold launches timed per standalone kernel")
     ap.add_argument("--cold-frames", type=int, default=50,
                     help="frames timed with L2 and MALL flushed before each (0: skip)")
     ap.add_argument("--api-frames", type=int, default=30,
@@ -379,6 +533,9 @@ def main() -> int:
 
     if args.pmc_pass is not None:
         return pmc_pass([int(i) for i in args.pmc_pass.split(",") if i])
+    if args.standalone_only:
+        log_standalone(standalone_kernels(args.kernel_reps, args.standalone_cold))
+        return 0
 
     with tempfile.TemporaryDirectory() as d:
         mlvc_hip.synth_write(CONFIG, d, 0)
@@ -449,6 +606,11 @@ def main() -> int:
             f"model->frame {codec['model_to_frame_us']:.1f} us ({codec['model_to_frame_gbs']:.0f} GB/s); buffered "
             f"encoder {codec['encoder_frames_per_s']:.0f} frames/s, decoder {codec['decoder_frames_per_s']:.0f} frames/s")
 
+    alone = None
+    if not args.no_standalone:
+        alone = standalone_kernels(args.kernel_reps, args.standalone_cold)
+        log_standalone(alone)
+
     ops = None
     if not args.no_realops:
         ops = realops(args.kernel_reps, args.realops_frames)
@@ -483,6 +645,7 @@ def main() -> int:
         "cpu_baseline": base,
         "codec_io": codec,
         "realops": ops,
+        "standalone": alone,
     }
     if rank == 0:
         print(json.dumps(line), flush=True)

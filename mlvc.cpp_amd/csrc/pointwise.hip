@@ -14,6 +14,15 @@ namespace {
 
 constexpr int kBlock = 256;
 
+// Opaque to the optimiser: keeps f2h(fmaf(a, b, c)) from becoming one
+// v_fma_mixlo_f16, which rounds once to FP16 where the reference rounds the
+// FP32 result of the multiply-add to FP16 (two roundings).
+__device__ __forceinline__ float keep(float x)
+{
+    asm("" : "+v"(x));
+    return x;
+}
+
 unsigned grid_for(size_t work)
 {
     return static_cast<unsigned>(std::max<size_t>(1, std::min<size_t>((work + kBlock - 1) / kBlock, 1u << 20)));
@@ -60,8 +69,98 @@ __global__ __launch_bounds__(kBlock) void depthwise_kernel(const std::uint16_t* 
         std::uint16_t* yp = y + (static_cast<size_t>(plane) * oh + oy) * ow + ox0;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            if (ox0 + j < ow) yp[j] = f2h(acc[j]);
+            if (ox0 + j < ow) yp[j] = f2h(keep(acc[j]));
     }
+}
+
+// 3x3, stride 1, pad 1 on rows of a multiple of 8 pixels (16-byte aligned):
+// one thread computes eight consecutive outputs in each of kDwRows rows, so
+// each input row segment it loads serves up to three of its output rows.
+// Every load is issued up front from clamped addresses (kDwRows + 2
+// 16-byte row segments, the pixels beside them, the nine taps) and a thread
+// waits for memory once; taps whose input lies outside the image are then
+// skipped by selects. The arithmetic is the kernel above's: bias-seeded,
+// taps in (ky, kx) order, one fused multiply-add each. grid.x: 8-pixel
+// segments x row groups of one plane; grid.y: planes.
+constexpr int kDwRows = 4;
+
+__global__ __launch_bounds__(kBlock) void depthwise3x3_row8_kernel(const std::uint16_t* __restrict__ x,
+                                                                   const std::uint16_t* __restrict__ w,
+                                                                   const float* __restrict__ bias,
+                                                                   std::uint16_t* __restrict__ y, int c, int h, int wd)
+{
+    constexpr int R = kDwRows, NR = R + 2;
+    const int segs = wd / 8, groups = (h + R - 1) / R;
+    const int i = blockIdx.x * kBlock + threadIdx.x;
+    if (i >= segs * groups) return;
+    const int plane = blockIdx.y, ch = plane % c;
+    const int g = i / segs, x0 = (i - g * segs) * 8, oy0 = g * R;
+    const std::uint16_t* xp = x + static_cast<size_t>(plane) * h * wd;
+    const std::uint16_t* wp = w + ch * 9;
+    const int xl = x0 > 0 ? x0 - 1 : 0, xr = x0 + 8 < wd ? x0 + 8 : wd - 1;
+    u32x4 v[NR];
+    std::uint32_t lft[NR], rgt[NR], tap[9];
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {  // input rows oy0 - 1 .. oy0 + R
+        const int iy = min(max(oy0 - 1 + r, 0), h - 1);
+        const std::uint16_t* row = xp + static_cast<size_t>(iy) * wd;
+        v[r] = *reinterpret_cast<const u32x4*>(row + x0);
+        lft[r] = row[xl];
+        rgt[r] = row[xr];
+    }
+#pragma unroll
+    for (int k = 0; k < 9; ++k) tap[k] = wp[k];
+    // Keeps the compiler from sinking the pixel loads into the selects below
+    // (a load per skipped-tap branch, each with its own wait).
+#pragma unroll
+    for (int r = 0; r < NR; ++r) asm volatile("" : "+v"(lft[r]), "+v"(rgt[r]));
+    const float b = bias[ch];
+    // All rows are computed before the first store: loads and stores share
+    // one in-order counter, so a store issued between two waits for loads
+    // would make the second wait also wait for the store's write.
+    u32x4 o[R];
+#pragma unroll
+    for (int orow = 0; orow < R; ++orow) {
+        const int oy = oy0 + orow;
+        float acc[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = b;
+#pragma unroll
+        for (int ky = 0; ky < 3; ++ky) {
+            const int r = orow + ky;
+            const bool row_in = oy - 1 + ky >= 0 && oy - 1 + ky < h;
+            // Converted once and kept opaque, so the taps are plain FP32
+            // multiply-adds rather than mixed-precision ones that convert
+            // the same pixel again for each of its three taps.
+            float px[10];  // input columns x0 - 1 .. x0 + 8
+            px[0] = keep(h2f(static_cast<std::uint16_t>(lft[r])));
+            px[9] = keep(h2f(static_cast<std::uint16_t>(rgt[r])));
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                px[1 + 2 * k] = keep(h2f(static_cast<std::uint16_t>(v[r][k] & 0xFFFFu)));
+                px[2 + 2 * k] = keep(h2f(static_cast<std::uint16_t>(v[r][k] >> 16)));
+            }
+#pragma unroll
+            for (int kx = 0; kx < 3; ++kx) {
+                const float wv = keep(h2f(static_cast<std::uint16_t>(tap[ky * 3 + kx])));
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const int ix = x0 + j - 1 + kx;
+                    const bool in = row_in && ix >= 0 && ix < wd;
+                    acc[j] = in ? fmaf(px[j + kx], wv, acc[j]) : acc[j];
+                }
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            o[orow][k] = static_cast<std::uint32_t>(f2h(keep(acc[2 * k]))) |
+                         (static_cast<std::uint32_t>(f2h(keep(acc[2 * k + 1]))) << 16);
+    }
+#pragma unroll
+    for (int orow = 0; orow < R; ++orow) asm volatile("" : "+v"(o[orow]));  // every row done before any store
+#pragma unroll
+    for (int orow = 0; orow < R; ++orow)
+        if (oy0 + orow < h) *reinterpret_cast<u32x4*>(y + (static_cast<size_t>(plane) * h + oy0 + orow) * wd + x0) = o[orow];
 }
 
 // DEPTH_TO_SPACE (CRD): out[b][c][y*s+dy][x*s+dx] = in[b][c*s*s + dy*s + dx][y][x].
@@ -96,6 +195,64 @@ __global__ __launch_bounds__(kBlock) void s2d_kernel(const std::uint16_t* __rest
         const int c = ocx / (s * s), r = ocx % (s * s), dy = r / s, dx = r % s;
         y[i] = x[((static_cast<size_t>(b) * ic + c) * h + oy * s + dy) * w + ox * s + dx];
     }
+}
+
+// Block 2 on input rows of a multiple of 8 pixels (16-byte aligned): one
+// thread takes eight input pixels of the two planes c*4 + dy*2 + {0, 1} at
+// input row y and writes the sixteen output pixels they interleave into, at
+// output row 2y + dy, as two 16-byte stores. grid.x: segments x input rows
+// x dy of one output plane; grid.y: output planes (b*oc + c).
+__global__ __launch_bounds__(kBlock) void d2s2_row8_kernel(const std::uint16_t* __restrict__ x, std::uint16_t* __restrict__ y,
+                                                          int h, int w)
+{
+    const int segs = w / 8;
+    const int i = blockIdx.x * kBlock + threadIdx.x;
+    if (i >= segs * 2 * h) return;
+    const int Y = i / segs, x0 = (i - Y * segs) * 8, iy = Y >> 1, dy = Y & 1;
+    const size_t plane = blockIdx.y, hw = static_cast<size_t>(h) * w;
+    const std::uint16_t* in = x + (plane * 4 + static_cast<size_t>(dy) * 2) * hw + static_cast<size_t>(iy) * w + x0;
+    const u32x4 a = *reinterpret_cast<const u32x4*>(in);       // dx = 0
+    const u32x4 b = *reinterpret_cast<const u32x4*>(in + hw);  // dx = 1
+    u32x4 lo, hi;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        lo[2 * k] = (a[k] & 0xFFFFu) | (b[k] << 16);
+        lo[2 * k + 1] = (a[k] >> 16) | (b[k] & 0xFFFF0000u);
+        hi[2 * k] = (a[k + 2] & 0xFFFFu) | (b[k + 2] << 16);
+        hi[2 * k + 1] = (a[k + 2] >> 16) | (b[k + 2] & 0xFFFF0000u);
+    }
+    std::uint16_t* out = y + (plane * 2 * h + Y) * (2 * static_cast<size_t>(w)) + 2 * x0;
+    *reinterpret_cast<u32x4*>(out) = lo;
+    *reinterpret_cast<u32x4*>(out + 8) = hi;
+}
+
+// Block 2 on input rows of a multiple of 16 pixels (16-byte aligned): one
+// thread reads sixteen pixels of input row 2*oy + dy and writes their even
+// (dx = 0) and odd (dx = 1) halves to planes c*4 + dy*2 + {0, 1} at row oy,
+// one 16-byte store each. grid.x: segments x output rows x dy of one input
+// plane; grid.y: input planes (b*ic + c).
+__global__ __launch_bounds__(kBlock) void s2d2_row8_kernel(const std::uint16_t* __restrict__ x, std::uint16_t* __restrict__ y,
+                                                          int h, int w)
+{
+    const int ow = w / 2, oh = h / 2, segs = ow / 8;
+    const int i = blockIdx.x * kBlock + threadIdx.x;
+    if (i >= segs * h) return;
+    const int Y = i / segs, ox0 = (i - Y * segs) * 8, oy = Y >> 1, dy = Y & 1;
+    const size_t plane = blockIdx.y, ohw = static_cast<size_t>(oh) * ow;
+    const std::uint16_t* in = x + (plane * h + Y) * static_cast<size_t>(w) + 2 * ox0;
+    const u32x4 a = *reinterpret_cast<const u32x4*>(in);
+    const u32x4 b = *reinterpret_cast<const u32x4*>(in + 8);
+    u32x4 ev, od;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        ev[k] = (a[2 * k] & 0xFFFFu) | (a[2 * k + 1] << 16);
+        od[k] = (a[2 * k] >> 16) | (a[2 * k + 1] & 0xFFFF0000u);
+        ev[k + 2] = (b[2 * k] & 0xFFFFu) | (b[2 * k + 1] << 16);
+        od[k + 2] = (b[2 * k] >> 16) | (b[2 * k + 1] & 0xFFFF0000u);
+    }
+    std::uint16_t* out = y + (plane * 4 + static_cast<size_t>(dy) * 2) * ohw + static_cast<size_t>(oy) * ow + ox0;
+    *reinterpret_cast<u32x4*>(out) = ev;
+    *reinterpret_cast<u32x4*>(out + ohw) = od;
 }
 
 template <int OP>  // 0: leaky relu, 1: add
@@ -169,6 +326,16 @@ int mlvc_hip_depthwise(const void* x, const uint16_t* w, const float* bias, void
             throw std::runtime_error("depthwise: invalid geometry");
         if (oh != (ih + 2 * pad_h - kh) / stride_h + 1 || ow != (iw + 2 * pad_w - kw) / stride_w + 1)
             throw std::runtime_error("depthwise: output shape does not match the geometry");
+        const size_t planes = static_cast<size_t>(n) * c;
+        if (kh == 3 && kw == 3 && stride_h == 1 && stride_w == 1 && pad_h == 1 && pad_w == 1 && iw % 8 == 0 &&
+            planes <= 65535 && static_cast<size_t>(ih) * (iw / 8) < (1u << 30) && aligned16(x) && aligned16(y)) {
+            const size_t threads = static_cast<size_t>((ih + kDwRows - 1) / kDwRows) * (iw / 8);
+            const unsigned gx = static_cast<unsigned>((threads + kBlock - 1) / kBlock);
+            hipLaunchKernelGGL(depthwise3x3_row8_kernel, dim3(gx, static_cast<unsigned>(planes)), dim3(kBlock), 0, to_stream(s),
+                               static_cast<const std::uint16_t*>(x), w, bias, static_cast<std::uint16_t*>(y), c, ih, iw);
+            check(hipGetLastError(), "depthwise launch");
+            return;
+        }
         const size_t work = static_cast<size_t>(n) * c * oh * ((ow + 3) / 4);
         hipLaunchKernelGGL(depthwise_kernel, dim3(grid_for(work)), dim3(kBlock), 0, to_stream(s),
                            static_cast<const std::uint16_t*>(x), w, bias, static_cast<std::uint16_t*>(y), n * c, c,
@@ -183,6 +350,15 @@ int mlvc_hip_depth_to_space(const void* x, void* y, int n, int in_c, int h, int 
         if (n <= 0 || h <= 0 || w <= 0 || block <= 0 || in_c <= 0 || in_c % (block * block) != 0)
             throw std::runtime_error("depth_to_space: invalid geometry");
         const int oc = in_c / (block * block);
+        const size_t planes = static_cast<size_t>(n) * oc;
+        if (block == 2 && w % 8 == 0 && planes <= 65535 && static_cast<size_t>(h) * (w / 4) < (1u << 30) && aligned16(x) &&
+            aligned16(y)) {
+            const unsigned gx = static_cast<unsigned>((static_cast<size_t>(h) * (w / 4) + kBlock - 1) / kBlock);
+            hipLaunchKernelGGL(d2s2_row8_kernel, dim3(gx, static_cast<unsigned>(planes)), dim3(kBlock), 0, to_stream(s),
+                               static_cast<const std::uint16_t*>(x), static_cast<std::uint16_t*>(y), h, w);
+            check(hipGetLastError(), "depth_to_space launch");
+            return;
+        }
         const size_t total = static_cast<size_t>(n) * in_c * h * w;
         hipLaunchKernelGGL(d2s_kernel, dim3(grid_for(total)), dim3(kBlock), 0, to_stream(s),
                            static_cast<const std::uint16_t*>(x), static_cast<std::uint16_t*>(y), n, oc, h, w, block);
@@ -195,6 +371,15 @@ int mlvc_hip_space_to_depth(const void* x, void* y, int n, int in_c, int h, int 
     return guard([&] {
         if (n <= 0 || in_c <= 0 || block <= 0 || h <= 0 || w <= 0 || h % block != 0 || w % block != 0)
             throw std::runtime_error("space_to_depth: invalid geometry");
+        const size_t planes = static_cast<size_t>(n) * in_c;
+        if (block == 2 && w % 16 == 0 && planes <= 65535 && static_cast<size_t>(h) * (w / 16) < (1u << 30) && aligned16(x) &&
+            aligned16(y)) {
+            const unsigned gx = static_cast<unsigned>((static_cast<size_t>(h) * (w / 16) + kBlock - 1) / kBlock);
+            hipLaunchKernelGGL(s2d2_row8_kernel, dim3(gx, static_cast<unsigned>(planes)), dim3(kBlock), 0, to_stream(s),
+                               static_cast<const std::uint16_t*>(x), static_cast<std::uint16_t*>(y), h, w);
+            check(hipGetLastError(), "space_to_depth launch");
+            return;
+        }
         const size_t total = static_cast<size_t>(n) * in_c * h * w;
         hipLaunchKernelGGL(s2d_kernel, dim3(grid_for(total)), dim3(kBlock), 0, to_stream(s),
                            static_cast<const std::uint16_t*>(x), static_cast<std::uint16_t*>(y), n, in_c, h, w, block);

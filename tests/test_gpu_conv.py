@@ -103,8 +103,12 @@ def test_fused_concat_load(tmp_path, k, pad):
     assert_parity(got[0], want[0], "concat-fused conv")
 
 
+# 3x3 s1 p1 with rows of a multiple of 8 pixels runs the 16-byte row kernel:
+# 256x46x80 and 128x92x160 (the residual-block shapes), 8x1x8 (one row, every
+# tap at a border), 24x7x16 (two segments a row).
 @pytest.mark.parametrize("c,h,w,k,s,p", [(16, 13, 17, 3, 1, 1), (256, 46, 80, 3, 1, 1), (12, 9, 10, 3, 1, 1),
-                                         (64, 15, 21, 3, 2, 1), (32, 11, 11, 5, 1, 2)])
+                                         (64, 15, 21, 3, 2, 1), (32, 11, 11, 5, 1, 2), (128, 92, 160, 3, 1, 1),
+                                         (8, 1, 8, 3, 1, 1), (24, 7, 16, 3, 1, 1)])
 def test_depthwise(tmp_path, c, h, w, k, s, p):
     shapes = graphs.single_conv_graph(tmp_path, "m", 1, c, h, w, c, k, s, p, groups=c, seed=c)
     got, want, launches = run_both(tmp_path, "m", shapes)
@@ -139,6 +143,28 @@ def test_standalone_layout_and_eltwise(tmp_path, rng):
     assert kinds == ["add", "leaky_relu", "space_to_depth", "depth_to_space", "concat"], kinds
     for i, (gg, ww) in enumerate(zip(got, want)):
         assert (gg == ww).all(), f"output {i} differs"  # one rounding per op on both sides
+
+
+# Block-2 shuffles on rows of 16-byte segments run the row kernels (D2S:
+# input width % 8 == 0; S2D: input width % 16 == 0), the others the
+# per-element kernels: the residual-block path's 512-channel shuffle, two
+# images, and widths on either side of each condition.
+@pytest.mark.parametrize("op,shape", [("DEPTH_TO_SPACE", (1, 512, 12, 16)), ("DEPTH_TO_SPACE", (2, 16, 5, 8)),
+                                      ("DEPTH_TO_SPACE", (1, 8, 3, 12)), ("SPACE_TO_DEPTH", (1, 128, 12, 32)),
+                                      ("SPACE_TO_DEPTH", (2, 4, 4, 16)), ("SPACE_TO_DEPTH", (1, 4, 6, 24))])
+def test_standalone_pixel_shuffle(tmp_path, rng, op, shape):
+    g = graphs.Graph()
+    x = g.input("x", list(shape))
+    g.output(g.pixel(op, "y", x, 2))
+    g.write(tmp_path, "m")
+    ins = [graphs.half(rng.uniform(-2, 2, shape))]
+    want = mlvc_oracle.OraclePlan(tmp_path, "m").run(ins)
+    gpu = mlvc_hip.Backend(tmp_path, "hip")
+    gpu.load("m")
+    got = gpu.run(ins)
+    assert [l["kind"] for l in gpu.launches()] == [op.lower()]
+    gpu.close()
+    assert got[0].shape == want[0].shape and (got[0] == want[0]).all()  # a permutation: bit for bit
 
 
 # ica <= 16 runs the streaming kernel (persistent grid of two workgroups per
