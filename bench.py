@@ -41,17 +41,31 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def kernel_table(gpu, reps: int):
+def kernel_table(gpu, reps: int, cold_reps: int = 0):
+    """Per launch: mean of `reps` back-to-back launches (warm: inputs and
+    weights stay in L2 / MALL between repeats) and, with cold_reps > 0, the
+    median of `cold_reps` single launches each after a cache-evicting copy
+    (cold: everything comes from HBM)."""
+    import numpy as np
+
     rows = []
     for l in gpu.launches():
         ms = gpu.time_launch(l["index"], reps)
         ai = l["flops"] / l["bytes"] if l["bytes"] else 0.0
         bound = "mfma" if ai >= RIDGE else "hbm"
-        t = ms * 1e-3
-        tflops = l["flops"] / t / 1e12 if l["flops"] else 0.0
-        gbs = l["bytes"] / t / 1e9
-        frac = tflops / PEAK_MFMA_TFLOPS if bound == "mfma" else gbs / PEAK_HBM_GBS
-        rows.append(dict(l, ms=ms, ai=ai, bound=bound, tflops=tflops, gbs=gbs, frac=frac))
+
+        def rates(ms):
+            t = ms * 1e-3
+            tflops = l["flops"] / t / 1e12 if l["flops"] else 0.0
+            gbs = l["bytes"] / t / 1e9
+            return tflops, gbs, tflops / PEAK_MFMA_TFLOPS if bound == "mfma" else gbs / PEAK_HBM_GBS
+
+        tflops, gbs, frac = rates(ms)
+        row = dict(l, ms=ms, ai=ai, bound=bound, tflops=tflops, gbs=gbs, frac=frac)
+        if cold_reps > 0:
+            cold = float(np.median(gpu.time_launch_cold(l["index"], cold_reps, COLD_FLUSH_BYTES)))
+            row.update(cold_ms=cold, cold_frac=rates(cold)[2])
+        rows.append(row)
     return rows
 
 
@@ -495,6 +509,8 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--kernel-reps", type=int, default=20)
+    ap.add_argument("--launch-cold-reps", type=int, default=5,
+                    help="single launches per kernel timed after a cache-evicting copy (0: skip)")
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-codec", action="store_true", help="skip the codec I/O measurements")
@@ -565,7 +581,7 @@ def main() -> int:
         log(f"per frame: median {frame_ms['median']:.3f} ms (p10 {frame_ms['p10']:.3f}, p90 {frame_ms['p90']:.3f})"
             + (f"; cold (L2 + MALL flushed) median {cold_ms['median']:.3f} ms (p10 {cold_ms['p10']:.3f}, "
                f"p90 {cold_ms['p90']:.3f})" if cold_ms else ""))
-        rows = kernel_table(gpu, args.kernel_reps)
+        rows = kernel_table(gpu, args.kernel_reps, args.launch_cold_reps)
         dom = max(rows, key=lambda r: r["ms"])
         dom_t = dom["ms"] * 1e-3
         if dom["bound"] == "mfma":
@@ -577,10 +593,15 @@ def main() -> int:
         roof["traffic"] = measured_traffic(args.traffic, dom["name"], dom["kind"])
         roof["kernel"] = f"{dom['name']} [{dom['kind']}]"
         roof["kernel_ms"] = dom["ms"]
-        log(f"{'#':>3} {'launch':28} {'kernel':48} {'us':>9} {'TFLOP/s':>8} {'GB/s':>8} {'AI':>7} bound frac")
+        if "cold_ms" in dom:
+            roof["kernel_cold_ms"] = dom["cold_ms"]
+            roof["frac_cold"] = dom["cold_frac"]
+        log(f"{'#':>3} {'launch':28} {'kernel':48} {'us':>9} {'TFLOP/s':>8} {'GB/s':>8} {'AI':>7} bound frac"
+            + ("  cold us  frac" if args.launch_cold_reps > 0 else ""))
         for r in rows:
             log(f"{r['index']:3d} {r['name'][:28]:28} {r['kind'][:48]:48} {r['ms']*1e3:9.1f} {r['tflops']:8.1f} "
-                f"{r['gbs']:8.0f} {r['ai']:7.1f} {r['bound']:5} {r['frac']:.3f}")
+                f"{r['gbs']:8.0f} {r['ai']:7.1f} {r['bound']:5} {r['frac']:.3f}"
+                + (f" {r['cold_ms']*1e3:8.1f} {r['cold_frac']:.3f}" if "cold_ms" in r else ""))
         sum_kernel_ms = sum(r["ms"] for r in rows)
         log(f"sum of isolated kernel times {sum_kernel_ms:.3f} ms/frame; graph replay {gpu_ms / args.steps:.3f} ms/frame "
             f"(events), {wall * 1e3 / args.steps:.3f} ms/frame (wall); {conv_flops / 1e9:.1f} GFLOP and "
@@ -642,6 +663,9 @@ def main() -> int:
         "cold_frame_ms": cold_ms,
         "run_api_frames_per_s": api_fps,
         "roofline": roof,
+        "launches": [{"name": r["name"], "kernel": r["kind"], "us": r["ms"] * 1e3, "bound": r["bound"], "frac": r["frac"],
+                      **({"cold_us": r["cold_ms"] * 1e3, "cold_frac": r["cold_frac"]} if "cold_ms" in r else {})}
+                     for r in rows],
         "cpu_baseline": base,
         "codec_io": codec,
         "realops": ops,

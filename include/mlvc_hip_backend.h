@@ -116,6 +116,12 @@ int mlvc_hip_backend_launch_info(mlvc_backend* backend, int index, char* name, s
 /* Launches kernel `index` `reps` times back to back on the backend's stream
  * between two events and reports the mean duration per launch. */
 int mlvc_hip_backend_time_launch(mlvc_backend* backend, int index, int reps, float* ms_per_launch);
+/* Launches kernel `index` `reps` times, one at a time, each after a
+ * device-to-device copy of flush_bytes / 2 bytes (outside its events) that
+ * evicts L2 and the MALL, and writes each launch's duration to ms_each[reps]
+ * (1 <= reps <= 4096). No counterpart in the reference: a measurement helper
+ * beside mlvc_hip_backend_time_frames_each. */
+int mlvc_hip_backend_time_launch_cold(mlvc_backend* backend, int index, int reps, size_t flush_bytes, float* ms_each);
 
 /* aot::load_aot_graph(model_dir, model_name) (runtime/src/aot_graph.cpp:
  * 291-317 with decode_graph's validation, :110-284) without any device

@@ -324,6 +324,14 @@ int mlvc_hip_backend_time_launch(mlvc_backend* backend, int index, int reps, flo
     return guard([&] { *ms_per_launch = hip(backend).time_launch(static_cast<std::size_t>(index), reps); });
 }
 
+int mlvc_hip_backend_time_launch_cold(mlvc_backend* backend, int index, int reps, size_t flush_bytes, float* ms_each)
+{
+    return guard([&] {
+        if (!ms_each) throw std::runtime_error("time_launch_cold: null output");
+        hip(backend).time_launch_cold(static_cast<std::size_t>(index), reps, flush_bytes, ms_each);
+    });
+}
+
 int mlvc_aot_inspect(const char* model_dir, const char* model_name, int* nodes, int* tensors, uint64_t* arena_bytes,
                      uint64_t* weights_bytes)
 {

@@ -479,13 +479,7 @@ public:
             hip_check(mlvc_hip_event_create(&e), "event creation");
             frame_evs_.push_back(e);
         }
-        if (flush_bytes > 0 && flush_bytes != flush_bytes_) {
-            if (flush_buf_) hip_check(mlvc_hip_free(flush_buf_), "flush buffer release");
-            flush_buf_ = nullptr;
-            flush_bytes_ = 0;
-            hip_check(mlvc_hip_malloc(&flush_buf_, flush_bytes), "flush buffer allocation");
-            flush_bytes_ = flush_bytes;
-        }
+        ensure_flush_buffer(flush_bytes);
         const std::size_t half = flush_bytes / 2;
         auto* fb = static_cast<std::uint8_t*>(flush_buf_);
         for (int f = 0; f < frames; ++f) {
@@ -518,6 +512,30 @@ public:
     {
         const Launch& l = *launches_.at(i);
         return {l.name, l.kind_name, l.flops, l.bytes};
+    }
+
+    // Per-launch GPU times of `reps` single launches of kernel i, each after a
+    // device-to-device copy of flush_bytes / 2 bytes (outside its events)
+    // that evicts L2 and the MALL: the launch reads its inputs and weights
+    // from HBM, as a launch whose producer ran long before would.
+    void time_launch_cold(std::size_t i, int reps, std::size_t flush_bytes, float* ms_each)
+    {
+        if (reps <= 0 || reps > 4096) fail("time_launch_cold: reps must be in 1..4096");
+        if (flush_bytes < 2) fail("time_launch_cold: flush_bytes must be at least 2");
+        select();
+        Launch& l = *launches_.at(i);
+        ensure_flush_buffer(flush_bytes);
+        const std::size_t half = flush_bytes / 2;
+        auto* fb = static_cast<std::uint8_t*>(flush_buf_);
+        enqueue_one(l, 0);
+        for (int r = 0; r < reps; ++r) {
+            hip_check(mlvc_hip_memcpy_d2d(fb + half, fb, half, stream_), "cache flush copy");
+            hip_check(mlvc_hip_event_record(ev0_, stream_), "event record");
+            enqueue_one(l, 0);
+            hip_check(mlvc_hip_event_record(ev1_, stream_), "event record");
+            hip_check(mlvc_hip_event_synchronize(ev1_), "event sync");
+            hip_check(mlvc_hip_event_elapsed_ms(ev0_, ev1_, &ms_each[r]), "event timing");
+        }
     }
 
     float time_launch(std::size_t i, int reps)
@@ -2194,6 +2212,16 @@ private:
     aot::LoadedGraph graph_;
     mlvc_hip_stream stream_ = nullptr;
     mlvc_hip_event ev0_ = nullptr, ev1_ = nullptr;
+    void ensure_flush_buffer(std::size_t flush_bytes)
+    {
+        if (flush_bytes == 0 || flush_bytes == flush_bytes_) return;
+        if (flush_buf_) hip_check(mlvc_hip_free(flush_buf_), "flush buffer release");
+        flush_buf_ = nullptr;
+        flush_bytes_ = 0;
+        hip_check(mlvc_hip_malloc(&flush_buf_, flush_bytes), "flush buffer allocation");
+        flush_bytes_ = flush_bytes;
+    }
+
     std::vector<mlvc_hip_event> frame_evs_;  // time_frames_each: start/stop per frame
     void* flush_buf_ = nullptr;              // time_frames_each: cache-flush copy buffer
     std::size_t flush_bytes_ = 0;
@@ -2266,6 +2294,11 @@ void HipBackend::download_outputs(const std::vector<std::uint16_t*>& outputs) { 
 std::size_t HipBackend::launch_count() const { return require_plan("launch_count()").launch_count(); }
 LaunchInfo HipBackend::launch_info(std::size_t index) const { return require_plan("launch_info()").launch_info(index); }
 float HipBackend::time_launch(std::size_t index, int reps) { return require_plan("time_launch()").time_launch(index, reps); }
+
+void HipBackend::time_launch_cold(std::size_t index, int reps, std::size_t flush_bytes, float* ms_each)
+{
+    require_plan("time_launch_cold()").time_launch_cold(index, reps, flush_bytes, ms_each);
+}
 
 void register_hip_backend(bool make_default)
 {

@@ -60,6 +60,9 @@ public:
     std::size_t launch_count() const;
     LaunchInfo launch_info(std::size_t index) const;
     float time_launch(std::size_t index, int reps);
+    // Per-launch times of `reps` single launches of kernel `index`, each after
+    // a cache-evicting device copy of flush_bytes / 2 bytes outside its events.
+    void time_launch_cold(std::size_t index, int reps, std::size_t flush_bytes, float* ms_each);
 
 private:
     Plan& require_plan(const char* caller) const;

@@ -1,6 +1,7 @@
-// 3x3 stride-2 tile variants of the MFMA conv kernel (conv_kernel.hpp).
+// 3x3 stride-2 tile variants of the MFMA conv kernel (conv_kernel.hpp) and of
+// the weight-streaming kernel (conv_ws.hpp).
 
-#include "conv_kernel.hpp"
+#include "conv_ws.hpp"
 
 namespace mlvc_hip {
 namespace conv {
@@ -22,6 +23,13 @@ const Variant kTable[] = {
     MLVC_VARIANT_WO(64, 2, 32, 3, 3, 2, 16, 1, 2, 4),
     MLVC_VARIANT_WO(64, 2, 32, 3, 3, 2, 16, 2, 1, 4),
     MLVC_VARIANT_OCC(32, 2, 64, 3, 3, 2, 16, 4),
+    MLVC_VARIANT_WS2(128, 4, 32, 32, 2, 4),
+    MLVC_VARIANT_WS2(128, 2, 64, 32, 2, 4),
+    MLVC_VARIANT_WS2(128, 2, 32, 64, 2, 4),
+    MLVC_VARIANT_WS2(128, 4, 32, 64, 1, 4),
+    MLVC_VARIANT_WS2(128, 2, 32, 32, 2, 4),
+    MLVC_VARIANT_WS2(192, 4, 32, 32, 2, 3),
+    MLVC_VARIANT_WS2(192, 2, 32, 64, 2, 3),
 };
 }  // namespace
 

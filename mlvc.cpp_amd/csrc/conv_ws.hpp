@@ -30,14 +30,18 @@
 namespace mlvc_hip {
 namespace conv {
 
-template <int BM_, int TH_, int TW_, int SC_, int OCC_ = 2>
+template <int BM_, int TH_, int TW_, int SC_, int OCC_ = 2, int S_ = 1, int WAVES_ = 4>
 struct WsCfg {
-    static constexpr int BM = BM_, TH = TH_, TW = TW_, SC = SC_, OCC = OCC_;
-    static constexpr int KH = 3, KW = 3, TAPS = 9, S = 1;
-    static constexpr int WAVES = 4, kThreads = 256;
+    static constexpr int BM = BM_, TH = TH_, TW = TW_, SC = SC_, OCC = OCC_, S = S_;
+    static constexpr int KH = 3, KW = 3, TAPS = 9;
+    static constexpr int WAVES = WAVES_, kThreads = 64 * WAVES;
     static constexpr int BN = TH * TW, MTT = BM / 32, MT = MTT / WAVES, NT = BN / 32;
-    static constexpr int IH_T = TH + 2, IW_T = TW + 2;
-    static constexpr int NSEG = (IW_T + 14) / 8, IW_S = NSEG * 8;
+    static constexpr int IH_T = (TH - 1) * S + 3, IW_T = (TW - 1) * S + 3;
+    // Staged columns: the halo plus up to 7 columns of 8-alignment on the left.
+    // With stride 2, even input columns fill the first HALF of a row and odd
+    // ones the second, so the 32 pixels of a B fragment read consecutive
+    // entries for every tap.
+    static constexpr int NSEG = (IW_T + 14) / 8, IW_S = NSEG * 8, HALF = IW_S / 2;
     static constexpr int PST = SC + 8;               // halves per staged pixel
     static constexpr int ROW = IW_S * PST + 8;       // rows start 4 banks apart
     static constexpr int IN_LDS = IH_T * ROW;
@@ -48,7 +52,8 @@ struct WsCfg {
     static constexpr int EPI_MAX = EPI_LDS > D2S_LDS ? EPI_LDS : D2S_LDS;
     static constexpr int LDS = IN_LDS > EPI_MAX ? IN_LDS : EPI_MAX;
     static constexpr int RING = 3;                   // A-fragment prefetch distance in k-steps
-    static_assert(BM % 128 == 0 && MT >= 1 && BN % 32 == 0 && TW % 8 == 0 && SC % 16 == 0, "tile shape");
+    static_assert(MTT % WAVES == 0 && MT >= 1 && BN % 32 == 0 && TW % 8 == 0 && SC % 16 == 0, "tile shape");
+    static_assert(S == 1 || S == 2, "stride");
     static_assert(TAPS % RING == 0, "ring slots are static per tap");
     static_assert(LDS * 2 * OCC <= 160 * 1024, "LDS budget");
     __device__ static constexpr int at(int row, int x) { return row * ROW + x * PST; }
@@ -63,7 +68,7 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
     const int item = xcd_order(blockIdx.x, a.nwg);
     const int ocb = item % a.ocbs, tile = (item / a.ocbs) % a.tiles, b = item / (a.ocbs * a.tiles);
     const int tx0 = (tile % a.tiles_x) * C::TW, ty0 = (tile / a.tiles_x) * C::TH;
-    const int iy0 = ty0 - a.ph, ix0 = tx0 - a.pw;
+    const int iy0 = ty0 * C::S - a.ph, ix0 = tx0 * C::S - a.pw;
     const int xa = ix0 - (((ix0 % 8) + 8) % 8);  // first staged column, 8-aligned
     const int col_off = ix0 - xa;
     const int mt0 = wave * C::MT, hsel = 4 * (lane >> 5);
@@ -107,7 +112,8 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
                     const int wd = j >> 1;
                     const u32x4 t = {pack_half(v[ii][0][wd], v[ii][1][wd], up), pack_half(v[ii][2][wd], v[ii][3][wd], up),
                                      pack_half(v[ii][4][wd], v[ii][5][wd], up), pack_half(v[ii][6][wd], v[ii][7][wd], up)};
-                    *reinterpret_cast<u32x4*>(&lds[C::at(yi, sg * 8 + j) + c8 * 8]) = t;
+                    const int col = C::S == 1 ? sg * 8 + j : (j & 1) * C::HALF + sg * 4 + (j >> 1);
+                    *reinterpret_cast<u32x4*>(&lds[C::at(yi, col) + c8 * 8]) = t;
                 }
             }
         }
@@ -137,11 +143,20 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
 #pragma unroll
                 for (int nt = 0; nt < C::NT; ++nt) acc[mt][nt][4 * j + i] = bv[i];
         }
+    // B fragment of pixel p at tap (ky, kx): staged row S*py + ky, staged
+    // column px + kx + col_off (stride 1) or, for input column
+    // c = 2*px + kx + col_off, entry c/2 of the half of c's parity (stride 2).
     int pbase[C::NT];
 #pragma unroll
     for (int nt = 0; nt < C::NT; ++nt) {
         const int p = nt * 32 + (lane & 31);
-        pbase[nt] = C::at(p / C::TW, p % C::TW + col_off) + (lane >> 5) * 8;
+        pbase[nt] = C::at(C::S * (p / C::TW), p % C::TW) + (lane >> 5) * 8;
+    }
+    int toff[C::KW];  // column part of the tap offset, per kx
+#pragma unroll
+    for (int kx = 0; kx < C::KW; ++kx) {
+        const int c = kx + col_off;
+        toff[kx] = (C::S == 1 ? c : (c & 1) * C::HALF + (c >> 1)) * C::PST;
     }
     __syncthreads();
 
@@ -163,7 +178,7 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
                 half8 bv[C::NT];
 #pragma unroll
                 for (int nt = 0; nt < C::NT; ++nt)
-                    bv[nt] = *reinterpret_cast<const half8*>(&lds[pbase[nt] + C::at(ky, kx) + coff]);
+                    bv[nt] = *reinterpret_cast<const half8*>(&lds[pbase[nt] + ky * C::ROW + toff[kx] + coff]);
                 half8 av[C::MT];
 #pragma unroll
                 for (int mt = 0; mt < C::MT; ++mt) {
@@ -284,6 +299,10 @@ void launch_ws(const ConvArgs& a, dim3 grid, hipStream_t s)
 #define MLVC_VARIANT_WS(BM, TH, TW, SC, OCC)                                                                   \
     Variant{"ws_bm" #BM "_" #TH "x" #TW "_k3x3_s1_sc" #SC "_occ" #OCC, BM, TH, TW, 3, 3, 1, 16, nullptr,          \
             &launch_ws<WsCfg<BM, TH, TW, SC, OCC>>, nullptr, SC}
+// Stride 2, WAVES waves splitting the BM output channels.
+#define MLVC_VARIANT_WS2(BM, TH, TW, SC, OCC, WAVES)                                                           \
+    Variant{"ws_bm" #BM "_" #TH "x" #TW "_k3x3_s2_sc" #SC "_occ" #OCC "_w" #WAVES, BM, TH, TW, 3, 3, 2, 16, nullptr, \
+            &launch_ws<WsCfg<BM, TH, TW, SC, OCC, 2, WAVES>>, nullptr, SC}
 
 }  // namespace conv
 }  // namespace mlvc_hip

@@ -78,6 +78,8 @@ def backend_lib() -> C.CDLL:
         lib.mlvc_hip_backend_launch_info.argtypes = [C.c_void_p, C.c_int, C.c_char_p, C.c_size_t, C.c_char_p,
                                                      C.c_size_t, C.POINTER(C.c_double), C.POINTER(C.c_double)]
         lib.mlvc_hip_backend_time_launch.argtypes = [C.c_void_p, C.c_int, C.c_int, C.POINTER(C.c_float)]
+        lib.mlvc_hip_backend_time_launch_cold.argtypes = [C.c_void_p, C.c_int, C.c_int, C.c_size_t,
+                                                          C.POINTER(C.c_float)]
         lib.mlvc_synth_configs.argtypes = [C.c_char_p, C.c_size_t]
         lib.mlvc_synth_write.argtypes = [C.c_char_p, C.c_char_p, C.c_uint64]
         lib.mlvc_synth_input.argtypes = [C.c_char_p, C.c_int, C.c_int, C.c_uint64, _u16p, C.c_size_t]
@@ -326,6 +328,14 @@ class Backend:
         ms = C.c_float()
         _check(self._lib.mlvc_hip_backend_time_launch(self._h, index, reps, C.byref(ms)))
         return ms.value
+
+    def time_launch_cold(self, index: int, reps: int, flush_bytes: int) -> np.ndarray:
+        """Per-launch GPU ms of `reps` single launches of kernel `index`, each
+        after a device copy of flush_bytes / 2 that evicts L2 and the MALL."""
+        ms = np.zeros(reps, dtype=np.float32)
+        _check(self._lib.mlvc_hip_backend_time_launch_cold(
+            self._h, index, reps, flush_bytes, ms.ctypes.data_as(C.POINTER(C.c_float))))
+        return ms
 
 
 # ---- seeded synthetic graphs ----------------------------------------------

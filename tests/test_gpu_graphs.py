@@ -174,6 +174,27 @@ def test_per_frame_timing_replays_the_same_frames(tmp_path):
     b.close()
 
 
+def test_cold_launch_timing(tmp_path):
+    """time_launch_cold times single launches after a cache-evicting copy:
+    one positive time per launch, and the argument checks of the C ABI."""
+    config = "mlvc_s_tiny"
+    bindings, _ = _write(tmp_path, config)
+    b = mlvc_hip.Backend(tmp_path, "hip")
+    b.load(config, bindings)
+    b.upload_inputs([mlvc_hip.synth_input(config, 0, 0, b.in_shapes[0])])
+    b.reset_state()
+    b.time_frames(1)
+    n = len(b.launches())
+    for i in (0, n - 1):
+        ms = b.time_launch_cold(i, 3, 8 << 20)
+        assert ms.shape == (3,) and (ms > 0).all()
+    with pytest.raises(mlvc_hip.MlvcError, match="reps"):
+        b.time_launch_cold(0, 0, 8 << 20)
+    with pytest.raises(mlvc_hip.MlvcError, match="flush_bytes"):
+        b.time_launch_cold(0, 1, 0)
+    b.close()
+
+
 @pytest.mark.parametrize("config", ["mlvc_s_tiny", "mlvc_tiny", "dwblock_92x160_c128", "dwblock_46x80_c256"])
 def test_fused_and_unfused_schedules_bit_identical(tmp_path, monkeypatch, config):
     """Every GPU fusion (S2D/CONCAT loads, epilogues, D2S stores, the fused

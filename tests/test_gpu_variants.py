@@ -41,11 +41,13 @@ CASES = [
     ("many_tiles_d2s", 1, 32, 384, 768, 128, 3, 1, 1, dict(epilogue="lrelu", d2s=2)),
     ("many_tiles_s2", 2, 24, 600, 1000, 64, 3, 2, 1, dict(epilogue="residual")),
     ("many_tiles_1x1", 1, 128, 512, 512, 64, 1, 1, 0, dict(concat_ic=64, epilogue="lrelu")),
+    ("many_tiles_s2_rows", 1, 64, 272, 960, 192, 3, 2, 1, dict(epilogue="lrelu")),
 ]
 
 # Geometries the weight-streaming 3x3 kernel (conv_ws.hpp) takes: NCHW inputs
 # with rows of a multiple of 8 pixels, no concat or SPACE_TO_DEPTH staging.
-WS_CASES = {"mid_4x8", "shuffle_8x16", "many_tiles_s1", "many_tiles_d2s", "residual_d2s"}
+WS_CASES = {"mid_4x8", "shuffle_8x16", "many_tiles_s1", "many_tiles_d2s", "residual_d2s", "down_s2", "down_s2_4x8",
+            "many_tiles_s2_rows"}
 
 
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
