@@ -132,7 +132,8 @@ int mlvc_aot_inspect(const char* model_dir, const char* model_name, int* nodes, 
 
 /* ---- bundle / asset path ----
  * Model directories or "embedded:<profile>" locations (reference
- * core/src/model_assets.cpp:36-252; this build links no embedded image).
+ * core/src/model_assets.cpp:36-252; the embedded image is described in
+ * mlvc_embedded_models.h).
  * mlvc_model_config_json: load_model_config (core/src/model.cpp:150-183:
  * metadata.pb checked against model_bundle.pb, ModelConfig::validate,
  * :50-91) as a JSON object of the ModelConfig members plus the derived
@@ -142,6 +143,17 @@ int mlvc_aot_inspect(const char* model_dir, const char* model_name, int* nodes, 
  * packager, tools/python/mlvc_tools/package.py:97-145, done in C++). */
 int mlvc_model_config_json(const char* model_dir, char* buf, size_t len);
 int mlvc_model_verify_bundle(const char* model_dir);
+/* model_bundle.pb of a location as JSON: profile, model_version, width,
+ * height and the artifacts (path, size) it lists. */
+int mlvc_model_bundle_json(const char* model_dir, char* buf, size_t len);
+/* Profiles of the linked embedded model image, newline-separated, in index
+ * order (list_embedded_model_profiles, model_assets.cpp:204-214); empty when
+ * none is linked. */
+int mlvc_model_embedded_profiles(char* buf, size_t len);
+/* "embedded:mlvc-psnr-v1" when that profile is embedded, else the first
+ * embedded profile, else "" (default_model_location, model_assets.cpp:
+ * 216-225). */
+int mlvc_model_default_location(char* buf, size_t len);
 
 /* ---- seeded synthetic graphs (graph.pb / weights.bin / metadata.pb) ---- */
 int mlvc_synth_configs(char* buf, size_t len);

@@ -6,7 +6,9 @@
 #include "mlvc/runtime/graph_builder.hpp"
 #include "mlvc_hip_backend.h"
 
+#include "mlvc/core/assets.hpp"
 #include "mlvc/core/model.hpp"
+#include "mlvc/runtime/wire.hpp"
 
 #include <cstring>
 #include <optional>
@@ -382,6 +384,51 @@ int mlvc_model_config_json(const char* model_dir, char* buf, size_t len)
 int mlvc_model_verify_bundle(const char* model_dir)
 {
     return guard([&] { mlvc::verify_model_bundle(*mlvc::make_model_asset_reader(std::filesystem::path(model_dir))); });
+}
+
+int mlvc_model_bundle_json(const char* model_dir, char* buf, size_t len)
+{
+    return guard([&] {
+        const auto assets = mlvc::make_model_asset_reader(std::filesystem::path(model_dir));
+        const auto b = mlvc::wire::parse_model_file(assets->read_binary("model_bundle.pb"), "model_bundle.pb",
+                                                    mlvc::wire::parse_bundle);
+        auto quoted = [](const std::string& v) {
+            std::string q = "\"";
+            for (char c : v) {
+                if (c == '"' || c == '\\') q += '\\';
+                if (static_cast<unsigned char>(c) < 0x20) throw std::runtime_error("model bundle string holds a control character");
+                q += c;
+            }
+            return q + "\"";
+        };
+        std::string j = "{\"profile\":" + quoted(b.profile) + ",\"model_version\":" + quoted(b.model_version) +
+                        ",\"width\":" + std::to_string(b.width) + ",\"height\":" + std::to_string(b.height) + ",\"artifacts\":[";
+        for (std::size_t i = 0; i < b.artifacts.size(); ++i)
+            j += (i ? "," : "") + std::string("{\"path\":") + quoted(b.artifacts[i].path) +
+                 ",\"size\":" + std::to_string(b.artifacts[i].size_bytes) + "}";
+        j += "]}";
+        if (j.size() + 1 > len) throw std::runtime_error("buffer too small for the model bundle description");
+        copy_str(j, buf, len);
+    });
+}
+
+int mlvc_model_embedded_profiles(char* buf, size_t len)
+{
+    return guard([&] {
+        std::string s;
+        for (const auto& p : mlvc::list_embedded_model_profiles()) s += (s.empty() ? "" : "\n") + p;
+        if (s.size() + 1 > len) throw std::runtime_error("buffer too small for the embedded profile list");
+        copy_str(s, buf, len);
+    });
+}
+
+int mlvc_model_default_location(char* buf, size_t len)
+{
+    return guard([&] {
+        const std::string s = mlvc::default_model_location().generic_string();
+        if (s.size() + 1 > len) throw std::runtime_error("buffer too small for the default model location");
+        copy_str(s, buf, len);
+    });
 }
 
 int mlvc_synth_configs(char* buf, size_t len)

@@ -2,7 +2,9 @@
 
 Outputs (git-ignored, shipped with the tree to the GPU host):
   mlvc.cpp_amd/lib/libmlvc_hip_device.so  gfx950 kernels + device C ABI (hipcc)
-  mlvc.cpp_amd/lib/libmlvc_hip.so         C++20 runtime + "hip" backend + backend C ABI (g++)
+  mlvc.cpp_amd/lib/libmlvc_hip.so         C++20 runtime + "hip" backend + backend C ABI (g++); with
+                                          MLVC_EMBED_MODEL_ROOT=<dir>, also the model bundles below <dir>
+                                          (<profile>/<WxH>/) as an embedded image (python/mlvc_embed.py)
   oracle/liboracle.so                     CPU oracle (test infrastructure, g++)
   oracle/_ref/libmlvc_ref_kernels.so      reference CPU kernels, when the reference checkout exists
 
@@ -72,8 +74,21 @@ def build_all(jobs: int | None = None, verbose: bool = True) -> None:
         orc.result()
     dev_lib = LIB / "libmlvc_hip_device.so"
     _run([HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", *dev_objs, "-o", str(dev_lib)])
-    _run(["g++", "-shared", *host_objs, f"-L{LIB}", "-lmlvc_hip_device", "-Wl,-rpath,$ORIGIN",
-          "-o", str(LIB / "libmlvc_hip.so"), "-lpthread"])
+    link_host = ["g++", "-shared", *host_objs, f"-L{LIB}", "-lmlvc_hip_device", "-Wl,-rpath,$ORIGIN",
+                 "-o", str(LIB / "libmlvc_hip.so"), "-lpthread"]
+    _run(link_host)
+    embed_root = os.environ.get("MLVC_EMBED_MODEL_ROOT")
+    if embed_root:
+        # Embedded model image: the packer checks every bundle through the
+        # library just linked, then the library is linked again with the
+        # image's objects (the payload is .incbin'd at assembly time).
+        out = OBJ / "embedded-models"
+        _run([sys.executable, str(PKG / "python" / "mlvc_embed.py"), "--model-root", embed_root, "--out-dir", str(out)])
+        image = []
+        for src in ("mlvc_embedded_models.S", "mlvc_embedded_models_index.c"):
+            image.append(str(out / (src + ".o")))
+            _run(["gcc", "-c", "-fPIC", f"-I{REPO / 'include'}", str(out / src), "-o", image[-1]])
+        _run(link_host[:-3] + image + link_host[-3:])
     ref_script = ORACLE / "build_ref.sh"
     if pathlib.Path("/root/reference/backends/cpu/src").is_dir():
         _run(["bash", str(ref_script)])

@@ -384,3 +384,30 @@ def model_config(model_dir) -> dict:
 def verify_bundle(model_dir) -> None:
     """Checks every artifact listed in model_bundle.pb for presence, size and SHA-256."""
     _check(backend_lib().mlvc_model_verify_bundle(str(model_dir).encode()))
+
+
+def bundle_info(model_dir) -> dict:
+    """model_bundle.pb of a location: profile, model_version, width, height, artifacts [{path, size}]."""
+    n = 1 << 16
+    while True:
+        buf = C.create_string_buffer(n)
+        rc = backend_lib().mlvc_model_bundle_json(str(model_dir).encode(), buf, len(buf))
+        if rc == 0:
+            return json.loads(buf.value.decode())
+        if "buffer too small" not in backend_lib().mlvc_backend_last_error().decode() or n >= 1 << 24:
+            _check(rc)
+        n *= 4
+
+
+def embedded_profiles() -> list[str]:
+    """Profiles of the linked embedded model image (empty when none is linked)."""
+    buf = C.create_string_buffer(1 << 16)
+    _check(backend_lib().mlvc_model_embedded_profiles(buf, len(buf)))
+    return [p for p in buf.value.decode().split("\n") if p]
+
+
+def default_model_location() -> str:
+    """'embedded:mlvc-psnr-v1' if embedded, else the first embedded profile's location, else ''."""
+    buf = C.create_string_buffer(4096)
+    _check(backend_lib().mlvc_model_default_location(buf, len(buf)))
+    return buf.value.decode()

@@ -4,8 +4,9 @@
 // Same interface as the reference's core/include/mlvc/core/assets.hpp:16-37
 // (ModelAssetReader with location_label/exists/read_binary, the directory and
 // embedded readers, "embedded:<profile>" locations and the default-location
-// rule of core/src/model_assets.cpp:36-252), plus an in-memory reader. This
-// build links no embedded model image, so it behaves like the reference built
+// rule of core/src/model_assets.cpp:36-252), plus an in-memory reader. The
+// embedded readers read the model image described in mlvc_embedded_models.h
+// when one is linked; without one, the build behaves like the reference built
 // without MLVC_HAS_EMBEDDED_MODELS: embedded readers hold no files and the
 // profile list is empty.
 

@@ -251,7 +251,7 @@ LoadedGraph load_aot_graph(const ModelAssetReader& assets, const std::string& mo
 
 LoadedGraph load_aot_graph(const std::filesystem::path& model_dir, const std::string& model_name)
 {
-    return load_aot_graph(*make_directory_asset_reader(model_dir), model_name);
+    return load_aot_graph(*make_model_asset_reader(model_dir), model_name);  // "embedded:<profile>" too (:319-324)
 }
 
 }  // namespace mlvc::aot

@@ -1,10 +1,24 @@
-// Directory and in-memory model asset readers.
+// Directory, embedded and in-memory model asset readers.
 
 #include "mlvc/core/assets.hpp"
 
+#include "mlvc_embedded_models.h"
+
 #include <algorithm>
+#include <cstdint>
 #include <fstream>
+#include <optional>
+#include <span>
 #include <stdexcept>
+
+// The embedded image is optional: an image object defines these symbols
+// (mlvc_embedded_models.h); without one they resolve to null.
+extern "C" {
+#pragma weak mlvc_embedded_models_start
+#pragma weak mlvc_embedded_models_end
+#pragma weak mlvc_embedded_models_index
+#pragma weak mlvc_embedded_models_count
+}
 
 namespace mlvc {
 namespace {
@@ -46,16 +60,58 @@ void check_profile(const std::string& profile)
         throw std::runtime_error("invalid embedded model profile: " + profile);
 }
 
-// No model image is linked into this build: every lookup misses.
+bool image_linked()
+{
+    return mlvc_embedded_models_start != nullptr && mlvc_embedded_models_end != nullptr &&
+           mlvc_embedded_models_index != nullptr && &mlvc_embedded_models_count != nullptr;
+}
+
+std::span<const mlvc_embedded_model_asset> image_index()
+{
+    if (!image_linked()) return {};
+    return {mlvc_embedded_models_index, static_cast<std::size_t>(mlvc_embedded_models_count)};
+}
+
+// The packed data, [start, end) (model_assets.cpp:50-61).
+std::span<const std::byte> image_data()
+{
+    const auto begin = reinterpret_cast<std::uintptr_t>(mlvc_embedded_models_start);
+    const auto end = reinterpret_cast<std::uintptr_t>(mlvc_embedded_models_end);
+    if (end < begin) throw std::runtime_error("embedded model section is corrupt");
+    return {reinterpret_cast<const std::byte*>(begin), static_cast<std::size_t>(end - begin)};
+}
+
+// First index entry of (profile, path), checked against the data
+// (model_assets.cpp:63-76).
+std::optional<std::span<const std::byte>> find_asset(std::string_view profile, std::string_view path)
+{
+    for (const auto& e : image_index()) {
+        if (!e.profile || !e.path || profile != e.profile || path != e.path) continue;
+        const auto data = image_data();
+        if (e.offset > data.size() || e.size > data.size() - e.offset)
+            throw std::runtime_error("embedded model index is corrupt");
+        return data.subspan(static_cast<std::size_t>(e.offset), static_cast<std::size_t>(e.size));
+    }
+    return std::nullopt;
+}
+
+// Files of one profile of the linked image; without an image, every lookup
+// misses and reads fail as in a build without embedded models.
 class EmbeddedAssetReader final : public ModelAssetReader {
 public:
     explicit EmbeddedAssetReader(std::string profile) : profile_(std::move(profile)) { check_profile(profile_); }
 
     std::string location_label() const override { return std::string(kEmbeddedPrefix) + profile_; }
-    bool exists(const std::filesystem::path&) const override { return false; }
-    std::vector<std::byte> read_binary(const std::filesystem::path&) const override
+    bool exists(const std::filesystem::path& rel) const override
     {
-        throw std::runtime_error("embedded models are disabled in this build (" + location_label() + ")");
+        return image_linked() && find_asset(profile_, rel.generic_string()).has_value();
+    }
+    std::vector<std::byte> read_binary(const std::filesystem::path& rel) const override
+    {
+        if (!image_linked())
+            throw std::runtime_error("embedded models are disabled in this build (" + location_label() + ")");
+        if (const auto a = find_asset(profile_, rel.generic_string())) return {a->begin(), a->end()};
+        throw std::runtime_error("embedded model asset not found: " + profile_ + "/" + rel.generic_string());
     }
 
 private:
@@ -116,7 +172,13 @@ std::shared_ptr<const ModelAssetReader> resolve_model_asset_reader(
     return make_model_asset_reader(embedded);
 }
 
-std::vector<std::string> list_embedded_model_profiles() { return {}; }
+std::vector<std::string> list_embedded_model_profiles()
+{
+    std::vector<std::string> out;
+    for (const auto& e : image_index())
+        if (e.profile && std::find(out.begin(), out.end(), e.profile) == out.end()) out.emplace_back(e.profile);
+    return out;
+}
 
 std::filesystem::path default_model_location()
 {

@@ -260,7 +260,7 @@ void build_codec(GraphBuilder& g, Rng& rng, SyntheticModel& info, int h, int w, 
         info.input_hi = {1.0, 0.0};
     }
     info.model_name = encoder ? "MLVCEncoder" : "MLVCDecoder";
-    info.profile = "synthetic/codec_" + std::to_string(w) + "x" + std::to_string(h);
+    info.profile = "synthetic-codec_" + std::to_string(w) + "x" + std::to_string(h);
     // The bundle's model description (metadata.pb), shared by both graphs:
     // 64-channel feature at 1/2, 256-channel latent at 1/16, hyperprior at
     // 1/64, QP table of 64 of 72 with a 4-frame shift cycle, no feature reset.
@@ -596,7 +596,7 @@ GraphBuilder build_synthetic(const std::string& config, std::uint64_t seed, Synt
     SyntheticModel local;
     find(config).make(g, rng, local);
     if (local.model_name.empty()) local.model_name = config;
-    if (local.profile.empty()) local.profile = "synthetic/" + config;
+    if (local.profile.empty()) local.profile = "synthetic-" + config;  // one path component, as embedded profiles are
     if (info) *info = local;
     return g;
 }
