@@ -44,6 +44,8 @@ const Variant kTable[] = {
     MLVC_VARIANT_WS(256, 4, 32, 64, 2),
     MLVC_VARIANT_WS(128, 4, 32, 64, 2),
     MLVC_VARIANT_WS(256, 2, 32, 128, 2),
+    MLVC_VARIANT_WSR(128, 4, 32, 64, 2, 9),
+    MLVC_VARIANT_WSR(256, 2, 32, 128, 2, 9),
 };
 }  // namespace
 

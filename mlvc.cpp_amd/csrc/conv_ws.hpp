@@ -30,7 +30,7 @@
 namespace mlvc_hip {
 namespace conv {
 
-template <int BM_, int TH_, int TW_, int SC_, int OCC_ = 2, int S_ = 1, int WAVES_ = 4>
+template <int BM_, int TH_, int TW_, int SC_, int OCC_ = 2, int S_ = 1, int WAVES_ = 4, int RING_ = 3>
 struct WsCfg {
     static constexpr int BM = BM_, TH = TH_, TW = TW_, SC = SC_, OCC = OCC_, S = S_;
     static constexpr int KH = 3, KW = 3, TAPS = 9;
@@ -51,7 +51,7 @@ struct WsCfg {
     static constexpr int D2S_LDS = BM * BN;  // [BM/4][2TH][2TW]
     static constexpr int EPI_MAX = EPI_LDS > D2S_LDS ? EPI_LDS : D2S_LDS;
     static constexpr int LDS = IN_LDS > EPI_MAX ? IN_LDS : EPI_MAX;
-    static constexpr int RING = 3;                   // A-fragment prefetch distance in k-steps
+    static constexpr int RING = RING_;               // A-fragment prefetch distance in k-steps
     static_assert(MTT % WAVES == 0 && MT >= 1 && BN % 32 == 0 && TW % 8 == 0 && SC % 16 == 0, "tile shape");
     static_assert(S == 1 || S == 2, "stride");
     static_assert(TAPS % RING == 0, "ring slots are static per tap");
@@ -299,6 +299,11 @@ void launch_ws(const ConvArgs& a, dim3 grid, hipStream_t s)
 #define MLVC_VARIANT_WS(BM, TH, TW, SC, OCC)                                                                   \
     Variant{"ws_bm" #BM "_" #TH "x" #TW "_k3x3_s1_sc" #SC "_occ" #OCC, BM, TH, TW, 3, 3, 1, 16, nullptr,          \
             &launch_ws<WsCfg<BM, TH, TW, SC, OCC>>, nullptr, SC}
+// A ring RING k-steps deep (3 or 9): with one m-tile per wave, 9 steps of
+// fragments cover the L2 latency that 3 do not.
+#define MLVC_VARIANT_WSR(BM, TH, TW, SC, OCC, RING)                                                            \
+    Variant{"ws_bm" #BM "_" #TH "x" #TW "_k3x3_s1_sc" #SC "_occ" #OCC "_r" #RING, BM, TH, TW, 3, 3, 1, 16, nullptr, \
+            &launch_ws<WsCfg<BM, TH, TW, SC, OCC, 1, 4, RING>>, nullptr, SC}
 // Stride 2, WAVES waves splitting the BM output channels.
 #define MLVC_VARIANT_WS2(BM, TH, TW, SC, OCC, WAVES)                                                           \
     Variant{"ws_bm" #BM "_" #TH "x" #TW "_k3x3_s2_sc" #SC "_occ" #OCC "_w" #WAVES, BM, TH, TW, 3, 3, 2, 16, nullptr, \
