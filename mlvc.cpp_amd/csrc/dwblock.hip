@@ -17,18 +17,24 @@
 //     per lane, pre-packed in A-fragment order) through both GEMMs, so W1 and
 //     then W2 are in flight from the first instruction to the last MFMA,
 //     across the depthwise stage and the barriers (LDS-only fences);
-//   * the depthwise input never touches LDS: two threads per channel load
-//     their 4 halo rows with range-checked buffer loads (one dword left, 16
-//     bytes, one dword right per row) and run the taps from registers; taps
-//     outside the image are skipped, so what those loads return is unused;
+//   * the input tile (6 rows x 24 columns of every channel: the 4x8 tile,
+//     its halo and 8-column alignment) is staged into LDS by coalesced
+//     16-byte loads, consecutive lanes reading consecutive 16-byte pieces of
+//     one channel row. Loading it per channel instead (lane = channel) made
+//     every load instruction touch 64 cache lines, and issuing them took a
+//     quarter of the kernel. Two threads per channel then run the depthwise
+//     taps from the staged rows; taps outside the image are skipped, so what
+//     the range-checked loads return there is unused. The residual is read
+//     from the same staged tile;
 //   * accumulators are seeded with the bias (float4 loads issued at start);
 //   * LeakyReLU for 0 <= alpha <= 1 is max(fp16(v), fp16(v * alpha)) on
 //     packed halves (rounding is monotonic, so this equals the reference's
 //     select), with the product rounded to FP32 first;
 //   * the project result is rounded into LDS as [channel][pixel] and leaves
-//     as 16-byte rows with the residual added from 16-byte loads of x.
-// LDS: d[pixel][C + 8] (later reused as y[channel][pixel]) and
-// e[pixel][E + 8]. Requires W % 8 == 0 (16-byte rows).
+//     as 16-byte rows with the residual added from the staged tile.
+// LDS: x[channel][6 rows][24 columns] (+8 halves per channel),
+// d[pixel][C + 8] (later reused as y[channel][pixel]) and e[pixel][E + 8].
+// Requires W % 8 == 0 (16-byte rows).
 
 #include "common.hpp"
 #include "mlvc_hip_device.h"
@@ -44,6 +50,10 @@ constexpr int kYS = kP + 8;                       // y staging row stride (halve
 #define MLVC_DW_RING 16
 #endif
 constexpr int kRing = MLVC_DW_RING;               // weight fragments in flight per wave
+constexpr int kXR = kTH + 2, kXW = kTW + 16;      // staged input rows and columns (x0 - 8 .. x0 + kTW + 7)
+// Halves per staged channel: 304 bytes, 76 dwords, so 16 lanes reading 16
+// bytes at the same offset of 16 consecutive channels hit distinct banks.
+constexpr int kXCS = kXR * kXW + 8;
 constexpr int kRawBufferFlags = 0x00020000;       // raw buffer resource word 3 (gfx950)
 constexpr int kOutOfRange = 0x40000000;           // byte offset past every staged tensor (< 2^30 bytes)
 
@@ -59,6 +69,8 @@ struct BlockCfg {
     static constexpr int RV = C * kTH / T;                            // output rows (16 B) per thread
     static constexpr int DST = C + 8, EST = E + 8;
     static constexpr int DS_HALVES = kP * DST > C * kYS ? kP * DST : C * kYS;
+    static constexpr int XUNITS = C * kXR * (kXW / 8);                // 16-byte pieces of the staged tile
+    static constexpr int XU = (XUNITS + T - 1) / T;                   // per thread
     static_assert(C % 128 == 0 && E % 128 == 0 && MT1 >= 1 && MT2 >= 1, "channel counts");
     static_assert(TPC * ORT == kTH && C * kTH % T == 0, "thread mapping");
 };
@@ -96,6 +108,7 @@ __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArg
     constexpr int NF1 = B::NF1, NF = B::NF, ORT = B::ORT, RV = B::RV, T = B::T;
     __shared__ __attribute__((aligned(16))) std::uint16_t es[kP * EST];
     __shared__ __attribute__((aligned(16))) std::uint16_t dys[B::DS_HALVES];
+    __shared__ __attribute__((aligned(16))) std::uint16_t xs[C * kXCS];  // x[channel][row][column]
     std::uint16_t* const ds = dys;  // d[pixel][C + 8]
     std::uint16_t* const ys = dys;  // y[channel][kYS], after the expand stage
 
@@ -116,28 +129,23 @@ __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArg
         f -= NF1;
         return w2[((wave * MT2 + f % MT2) * KS2 + f / MT2) * 64 + lane];
     };
-    // ---- 1. depthwise halo rows of channel c straight into registers ------
-    // Thread (c, g): output rows g*ORT .. g*ORT + ORT - 1 of the tile, input
-    // rows y0 + g*ORT - 1 .. + ORT. Per row: the dword holding columns
-    // x0-2, x0-1, the 16 bytes x0 .. x0+7 and the dword x0+8, x0+9. The
-    // whole byte offset goes in the VGPR operand: the range check applies to
-    // that operand alone, not to the SGPR offset. Rows outside the image get
-    // an offset past the end (zeros); the left/right dwords at the image edge
-    // read a neighbouring row or zeros. All of those taps are skipped.
-    const int c = tid % C, g = tid / C;
+    // ---- 1. input tile into LDS, coalesced --------------------------------
+    // Piece u: 8 columns (x0 - 8 + 8k .. + 7) of staged row r (image row
+    // y0 - 1 + r) of channel c; k fastest, then r, then c. The whole byte
+    // offset goes in the VGPR operand: the range check applies to that
+    // operand alone, not to the SGPR offset. Pieces outside the image get an
+    // offset past the end (zeros); the taps that would read them are skipped.
     const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<std::uint16_t*>(xb), 0, static_cast<int>(C * plane * 2), kRawBufferFlags);
-    const int row0 = y0 + g * ORT - 1;
-    std::uint32_t xl[ORT + 2], xr[ORT + 2];
-    u32x4 xm[ORT + 2];
+    u32x4 xp[B::XU];
 #pragma unroll
-    for (int r = 0; r < ORT + 2; ++r) {
-        const int iy = row0 + r;
-        const int off = iy >= 0 && iy < a.h ? ((c * a.h + iy) * a.w + x0) * 2 : kOutOfRange;
-        xl[r] = __builtin_amdgcn_raw_buffer_load_b32(rx, off - 4, 0, 0);
-        xm[r] = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
-        xr[r] = __builtin_amdgcn_raw_buffer_load_b32(rx, off + 16, 0, 0);
+    for (int i = 0; i < B::XU; ++i) {
+        const int u = tid + i * T, k = u % (kXW / 8), r = (u / (kXW / 8)) % kXR, ch = u / ((kXW / 8) * kXR);
+        const int iy = y0 - 1 + r, ix = x0 - 8 + 8 * k;
+        const bool ok = u < B::XUNITS && iy >= 0 && iy < a.h && ix >= 0 && ix < a.w;
+        xp[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? ((ch * a.h + iy) * a.w + ix) * 2 : kOutOfRange, 0, 0);
     }
+    const int c = tid % C, g = tid / C;
     // Taps as separate 16-bit loads (one register each, nothing to unpack
     // before the depthwise stage, so issuing them waits for nothing).
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<std::uint16_t*>(a.dw_w), 0, C * 9 * 2,
@@ -147,11 +155,11 @@ __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArg
     for (int t = 0; t < 9; ++t) wdw[t] = __builtin_amdgcn_raw_buffer_load_b16(rw, (c * 9 + t) * 2, 0, 0);
     const float bdw = a.dw_b[c];
     // The depthwise operands are requested first: loads complete in issue
-    // order for the wait counter, so the depthwise stage then waits for
-    // them only, and runs while the weight ring below is still in flight.
+    // order for the wait counter, so the staging below waits for them only,
+    // and the depthwise stage runs while the weight ring is still in flight.
     __builtin_amdgcn_sched_barrier(0);
 
-    // The weight ring, then the expand bias and the residual rows.
+    // The weight ring, then the expand bias.
     u32x4 ring[kRing];
 #pragma unroll
     for (int f = 0; f < kRing; ++f) ring[f] = f < NF ? frag(f) : u32x4{0u, 0u, 0u, 0u};
@@ -167,16 +175,28 @@ __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArg
             for (int i = 0; i < 4; ++i) acc1[m][4 * j + i] = bv[i];
         }
 
-    // Residual rows for the output stage, loaded ahead of use.
-    u32x4 res[RV];
-#pragma unroll
-    for (int i = 0; i < RV; ++i) {
-        const int q = tid + T * i, ch = q / kTH, gy = min(y0 + q % kTH, a.h - 1);  // rows past h are not stored
-        res[i] = *reinterpret_cast<const u32x4*>(xb + ch * plane + static_cast<size_t>(gy) * a.w + x0);
-    }
     // The scheduler would otherwise sink the ring loads down to their MFMAs
     // (minimising live registers) and serialise the stream on L2 latency.
     __builtin_amdgcn_sched_barrier(0);
+
+#pragma unroll
+    for (int i = 0; i < B::XU; ++i) {
+        const int u = tid + i * T, k = u % (kXW / 8), r = (u / (kXW / 8)) % kXR, ch = u / ((kXW / 8) * kXR);
+        if (u < B::XUNITS) *reinterpret_cast<u32x4*>(&xs[ch * kXCS + r * kXW + 8 * k]) = xp[i];
+    }
+    lds_barrier();
+    // This thread's halo rows from the staged tile: per row the dword of
+    // columns x0-2, x0-1, the 16 bytes x0 .. x0+7 and the dword x0+8, x0+9.
+    const int row0 = g * ORT;  // staged row of image row y0 + g*ORT - 1
+    std::uint32_t xl[ORT + 2], xr[ORT + 2];
+    u32x4 xm[ORT + 2];
+#pragma unroll
+    for (int r = 0; r < ORT + 2; ++r) {
+        const std::uint16_t* rowp = &xs[c * kXCS + (row0 + r) * kXW];
+        xl[r] = *reinterpret_cast<const std::uint32_t*>(rowp + 6);
+        xm[r] = *reinterpret_cast<const u32x4*>(rowp + 8);
+        xr[r] = *reinterpret_cast<const std::uint32_t*>(rowp + 16);
+    }
 
     {
         const bool left = x0 > 0, right = x0 + kTW < a.w;
@@ -286,11 +306,12 @@ __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArg
         const int q = tid + T * i, ch = q / kTH, row = q % kTH, gy = y0 + row;
         if (gy >= a.h) continue;
         const u32x4 pv = *reinterpret_cast<const u32x4*>(&ys[ch * kYS + row * kTW]);
+        const u32x4 rv = *reinterpret_cast<const u32x4*>(&xs[ch * kXCS + (row + 1) * kXW + 8]);  // residual x
         u32x4 o;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
-            const std::uint32_t lo = f2h(lo_h(pv[k]) + lo_h(res[i][k]));
-            const std::uint32_t hi = f2h(hi_h(pv[k]) + hi_h(res[i][k]));
+            const std::uint32_t lo = f2h(lo_h(pv[k]) + lo_h(rv[k]));
+            const std::uint32_t hi = f2h(hi_h(pv[k]) + hi_h(rv[k]));
             o[k] = lo | (hi << 16);
         }
         *reinterpret_cast<u32x4*>(yb + ch * plane + static_cast<size_t>(gy) * a.w + x0) = o;
