@@ -142,7 +142,8 @@ int mlvc_hip_depthwise(const void* x, const uint16_t* w, const float* bias, void
  * epilogue (pointwise_conv.cu / cutlass.cu EVT epilogues) that the
  * reference runs as three launches; rounding points are unchanged.
  * x, y: [n, c, h, w]; dw_w: [c, 1, 3, 3] fp16 (stride 1, pad 1);
- * w1: W1 [e, c] packed by mlvc_hip_dwblock_pack; w2: W2 [c, e] packed. */
+ * w1: W1 [e, c] packed by mlvc_hip_dwblock_pack; w2: W2 [c, e] packed.
+ * x, y and dw_w must be 16-byte aligned. */
 typedef struct mlvc_hip_dwblock_desc {
     int n, c, e, h, w;
     const void* x;

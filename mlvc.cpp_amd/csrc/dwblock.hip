@@ -71,6 +71,8 @@ struct BlockCfg {
     static constexpr int DS_HALVES = kP * DST > C * kYS ? kP * DST : C * kYS;
     static constexpr int XUNITS = C * kXR * (kXW / 8);                // 16-byte pieces of the staged tile
     static constexpr int XU = (XUNITS + T - 1) / T;                   // per thread
+    static constexpr int TAP_PIECES = C * 9 * 2 / 16;                 // 16-byte pieces of the depthwise taps
+    static_assert(C * 9 * 2 % 16 == 0 && TAP_PIECES <= T, "tap staging");
     static_assert(C % 128 == 0 && E % 128 == 0 && MT1 >= 1 && MT2 >= 1, "channel counts");
     static_assert(TPC * ORT == kTH && C * kTH % T == 0, "thread mapping");
 };
@@ -109,6 +111,7 @@ __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArg
     __shared__ __attribute__((aligned(16))) std::uint16_t es[kP * EST];
     __shared__ __attribute__((aligned(16))) std::uint16_t dys[B::DS_HALVES];
     __shared__ __attribute__((aligned(16))) std::uint16_t xs[C * kXCS];  // x[channel][row][column]
+    __shared__ __attribute__((aligned(16))) std::uint16_t taps[C * 9];  // depthwise taps [channel][ky][kx]
     std::uint16_t* const ds = dys;  // d[pixel][C + 8]
     std::uint16_t* const ys = dys;  // y[channel][kYS], after the expand stage
 
@@ -146,13 +149,11 @@ __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArg
         xp[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? ((ch * a.h + iy) * a.w + ix) * 2 : kOutOfRange, 0, 0);
     }
     const int c = tid % C, g = tid / C;
-    // Taps as separate 16-bit loads (one register each, nothing to unpack
-    // before the depthwise stage, so issuing them waits for nothing).
-    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<std::uint16_t*>(a.dw_w), 0, C * 9 * 2,
-                                                                        kRawBufferFlags);
-    std::uint16_t wdw[9];
-#pragma unroll
-    for (int t = 0; t < 9; ++t) wdw[t] = __builtin_amdgcn_raw_buffer_load_b16(rw, (c * 9 + t) * 2, 0, 0);
+    // The taps of all channels as 16-byte pieces, staged with the tile (a
+    // thread's own nine taps per channel would be nine loads, each touching
+    // as many cache lines as the wave has channels).
+    u32x4 tp = {0u, 0u, 0u, 0u};
+    if (tid < B::TAP_PIECES) tp = reinterpret_cast<const u32x4*>(a.dw_w)[tid];
     const float bdw = a.dw_b[c];
     // The depthwise operands are requested first: loads complete in issue
     // order for the wait counter, so the staging below waits for them only,
@@ -184,7 +185,11 @@ __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArg
         const int u = tid + i * T, k = u % (kXW / 8), r = (u / (kXW / 8)) % kXR, ch = u / ((kXW / 8) * kXR);
         if (u < B::XUNITS) *reinterpret_cast<u32x4*>(&xs[ch * kXCS + r * kXW + 8 * k]) = xp[i];
     }
+    if (tid < B::TAP_PIECES) *reinterpret_cast<u32x4*>(&taps[tid * 8]) = tp;
     lds_barrier();
+    std::uint16_t wdw[9];
+#pragma unroll
+    for (int t = 0; t < 9; ++t) wdw[t] = taps[c * 9 + t];
     // This thread's halo rows from the staged tile: per row the dword of
     // columns x0-2, x0-1, the 16 bytes x0 .. x0+7 and the dword x0+8, x0+9.
     const int row0 = g * ORT;  // staged row of image row y0 + g*ORT - 1
@@ -364,6 +369,9 @@ int mlvc_hip_dwblock_launch(const mlvc_hip_dwblock_desc* d, mlvc_hip_stream s)
             throw std::runtime_error("dwblock: unsupported geometry");
         if (!d->x || !d->y || !d->dw_w || !d->dw_b || !d->w1 || !d->b1 || !d->w2 || !d->b2)
             throw std::runtime_error("dwblock: null tensor");
+        if ((reinterpret_cast<std::uintptr_t>(d->dw_w) | reinterpret_cast<std::uintptr_t>(d->x) |
+             reinterpret_cast<std::uintptr_t>(d->y)) & 15u)
+            throw std::runtime_error("dwblock: x, y and the depthwise taps must be 16-byte aligned");
         if (static_cast<std::uint64_t>(d->c) * d->h * d->w * 2 + 64 >= static_cast<std::uint64_t>(kOutOfRange))
             throw std::runtime_error("dwblock: image too large for 32-bit buffer offsets");
         DwBlockArgs a{static_cast<const std::uint16_t*>(d->x), static_cast<std::uint16_t*>(d->y),
