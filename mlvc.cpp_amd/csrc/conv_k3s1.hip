@@ -46,6 +46,12 @@ const Variant kTable[] = {
     MLVC_VARIANT_WS(256, 2, 32, 128, 2),
     MLVC_VARIANT_WSR(128, 4, 32, 64, 2, 9),
     MLVC_VARIANT_WSR(256, 2, 32, 128, 2, 9),
+    // Widths that divide 120 and 240 (24, 40) or 240 and 480 (48), so the
+    // 68x120 and 136x240 decoder convs run without padded columns.
+    MLVC_VARIANT_WSR(128, 4, 24, 64, 2, 9),
+    MLVC_VARIANT_WSR(128, 8, 24, 64, 2, 9),
+    MLVC_VARIANT_WSR(128, 4, 40, 64, 2, 9),
+    MLVC_VARIANT_WSR(128, 4, 48, 64, 2, 9),
 };
 }  // namespace
 
