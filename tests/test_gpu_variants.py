@@ -42,6 +42,11 @@ CASES = [
     ("many_tiles_s2", 2, 24, 600, 1000, 64, 3, 2, 1, dict(epilogue="residual")),
     ("many_tiles_1x1", 1, 128, 512, 512, 64, 1, 1, 0, dict(concat_ic=64, epilogue="lrelu")),
     ("many_tiles_s2_rows", 1, 64, 272, 960, 192, 3, 2, 1, dict(epilogue="lrelu")),
+    # At most 16 output channels: plain and DEPTH_TO_SPACE(2) outputs, ragged
+    # right edge, and more tiles than the device holds workgroups at once.
+    ("small_oc_plain", 1, 32, 24, 64, 8, 3, 1, 1, dict(epilogue="lrelu")),
+    ("small_oc_residual", 1, 64, 20, 40, 16, 3, 1, 1, dict(epilogue="residual")),
+    ("recon_many_tiles", 2, 64, 136, 512, 12, 3, 1, 1, dict(d2s=2)),
 ]
 
 # Geometries the weight-streaming 3x3 kernel (conv_ws.hpp) takes: NCHW inputs
