@@ -52,6 +52,7 @@ const Variant kTable[] = {
     MLVC_VARIANT_WSR(128, 8, 24, 64, 2, 9),
     MLVC_VARIANT_WSR(128, 4, 40, 64, 2, 9),
     MLVC_VARIANT_WSR(128, 4, 48, 64, 2, 9),
+    MLVC_VARIANT_WS(128, 8, 32, 64, 2),
 };
 }  // namespace
 

@@ -52,6 +52,9 @@ struct WsCfg {
     static constexpr int EPI_MAX = EPI_LDS > D2S_LDS ? EPI_LDS : D2S_LDS;
     static constexpr int LDS = IN_LDS > EPI_MAX ? IN_LDS : EPI_MAX;
     static constexpr int RING = RING_;               // A-fragment prefetch distance in k-steps
+    // Staging units in flight per thread: 2, or 1 where the accumulators and
+    // the ring leave no room for a second unit's 32 registers.
+    static constexpr int STAGE_BATCH = MT * NT * 16 + RING * MT * 4 > 160 ? 1 : 2;
     static_assert(MTT % WAVES == 0 && MT >= 1 && BN % 32 == 0 && TW % 8 == 0 && SC % 16 == 0, "tile shape");
     static_assert(S == 1 || S == 2, "stride");
     static_assert(TAPS % RING == 0, "ring slots are static per tap");
@@ -85,7 +88,7 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
     const __amdgpu_buffer_rsrc_t rx =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<std::uint16_t*>(x_img), 0, static_cast<int>(a.ic * hw2), kRawBufferFlags);
     auto stage = [&](int cb) {
-        constexpr int BATCH = 2;  // units in flight per thread (bounds the staging registers)
+        constexpr int BATCH = C::STAGE_BATCH;  // units in flight per thread (bounds the staging registers)
 #pragma unroll
         for (int i0 = 0; i0 < C::UNITS_PER_T; i0 += BATCH) {
             u32x4 v[BATCH][8];
