@@ -186,8 +186,15 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
 #pragma unroll
                 for (int mt = 0; mt < C::MT; ++mt) {
                     av[mt] = __builtin_bit_cast(half8, ring[tap % C::RING][mt]);
-                    if (s + C::RING < total) ring[tap % C::RING][mt] = frag(s + C::RING, mt);
+                    ring[tap % C::RING][mt] = frag(min(s + C::RING, total - 1), mt);
                 }
+                // The refill is issued here, before this tap's MFMAs, and
+                // unconditionally (past the last step it re-reads that step):
+                // the wait counter then stays at the ring depth. A conditional
+                // refill made the compiler wait for every load where its
+                // branch joined, and left alone it sinks the loads to their
+                // use, either way exposing the L2 latency every few taps.
+                __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
                 for (int mt = 0; mt < C::MT; ++mt)
 #pragma unroll
