@@ -48,9 +48,7 @@ struct WsCfg {
     static constexpr int UNITS = (SC / 8) * IH_T * NSEG;  // 8 channels x 8 columns each
     static constexpr int UNITS_PER_T = (UNITS + kThreads - 1) / kThreads;
     static constexpr int EPI_ROW = BN + 8, EPI_LDS = BM * EPI_ROW;
-    static constexpr int D2S_LDS = BM * BN;  // [BM/4][2TH][2TW]
-    static constexpr int EPI_MAX = EPI_LDS > D2S_LDS ? EPI_LDS : D2S_LDS;
-    static constexpr int LDS = IN_LDS > EPI_MAX ? IN_LDS : EPI_MAX;
+    static constexpr int LDS = IN_LDS > EPI_LDS ? IN_LDS : EPI_LDS;  // the plain epilogue's tile aliases the halo
     static constexpr int RING = RING_;               // A-fragment prefetch distance in k-steps
     // Staging units in flight per thread: 2, or 1 where the accumulators and
     // the ring leave no room for a second unit's 32 registers.
@@ -207,14 +205,15 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
     // ---- epilogue (as conv_mfma_kernel): round, then the epilogue on the
     // rounded value. Lane l of accumulator (mt, nt) holds channels oc0 + i,
     // oc0 = ocb*BM + (mt0+mt)*32 + 8j + 4*(l/32), of tile pixel nt*32 + l%32.
-    // The result goes through LDS and leaves as 16-byte rows: plain outputs
-    // as [channel][pixel]; with DEPTH_TO_SPACE(2) the 4 channels of a lane
-    // are the (dy, dx) block of output channel oc0/4, staged as
-    // [channel][2*TH rows][2*TW columns].
+    // Plain outputs go through an LDS [channel][pixel] tile and leave as
+    // 16-byte rows; with DEPTH_TO_SPACE(2) the 4 channels of a lane are the
+    // (dy, dx) block of output channel oc0/4, stored as two 4-byte pairs.
     const bool max_form = a.alpha >= 0.0f && a.alpha <= 1.0f;
-    __syncthreads();  // every wave is done reading the halo
     if (a.d2s == 2) {
-        constexpr int W2 = 2 * C::TW, ROWS = 2 * C::TH;
+        // Straight from the accumulators, no LDS and no barrier: each wave
+        // writes as soon as its own K loop ends. Lanes 0-31 and 32-63 each
+        // write 32 consecutive pixel pairs, 128 contiguous bytes per row.
+        const int OW2 = a.ow * 2, OH2 = a.oh * 2, occ = a.oc / 4;
 #pragma unroll
         for (int mt = 0; mt < C::MT; ++mt)
 #pragma unroll
@@ -246,24 +245,18 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
                             h23 = f2h(lo_f16(h23) + h2f(r[2])) | (static_cast<std::uint32_t>(f2h(hi_f16(h23) + h2f(r[3]))) << 16);
                         }
                     }
-                    std::uint16_t* st = &lds[((ocl / 4) * ROWS + 2 * py) * W2 + 2 * px];
-                    *reinterpret_cast<std::uint32_t*>(st) = h01;
-                    *reinterpret_cast<std::uint32_t*>(st + W2) = h23;
+                    // Rows oc0 .. oc0+3 are the (dy, dx) block of output channel oc0 / 4.
+                    const int c = oc0 / 4;
+                    if (inside && c < occ) {
+                        std::uint16_t* dst = a.y + (static_cast<size_t>(b * occ + c) * OH2 + 2 * oy) * OW2 + 2 * ox;
+                        *reinterpret_cast<std::uint32_t*>(dst) = h01;
+                        *reinterpret_cast<std::uint32_t*>(dst + OW2) = h23;
+                    }
                 }
             }
-        __syncthreads();
-        // 16-byte row pieces: W2/8 per staged row, rows of every channel.
-        constexpr int PIECES = W2 / 8, UNITS = (C::BM / 4) * ROWS * PIECES;
-        const int OW2 = a.ow * 2, OH2 = a.oh * 2, occ = a.oc / 4;
-        for (int u = tid; u < UNITS; u += C::kThreads) {
-            const int pc = u % PIECES, r = (u / PIECES) % ROWS, cl = u / (PIECES * ROWS);
-            const int c = ocb * (C::BM / 4) + cl, gy = 2 * ty0 + r, gx = 2 * tx0 + pc * 8;
-            if (c >= occ || gy >= OH2 || gx >= OW2) continue;
-            *reinterpret_cast<u32x4*>(a.y + (static_cast<size_t>(b * occ + c) * OH2 + gy) * OW2 + gx) =
-                *reinterpret_cast<const u32x4*>(&lds[(cl * ROWS + r) * W2 + pc * 8]);
-        }
         return;
     }
+    __syncthreads();  // every wave is done reading the halo
 #pragma unroll
     for (int mt = 0; mt < C::MT; ++mt)
 #pragma unroll
