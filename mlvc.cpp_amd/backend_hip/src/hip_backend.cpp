@@ -2045,6 +2045,9 @@ private:
         const char* tune_file = std::getenv("MLVC_HIP_TUNE_FILE");
         const char* tune_write = std::getenv("MLVC_HIP_TUNE_WRITE");
         const bool write_back = tune_file && tune_write && std::string(tune_write) == "1";
+        // MLVC_HIP_TUNE_VERBOSE=1 prints every candidate's time per launch.
+        const char* verbose_env = std::getenv("MLVC_HIP_TUNE_VERBOSE");
+        const bool tune_verbose = verbose_env && std::string(verbose_env) == "1";
         std::map<std::string, std::string> chosen;
         if (tune_file) {
             std::ifstream in(tune_file);
@@ -2093,6 +2096,9 @@ private:
                 hip_check(mlvc_hip_event_elapsed_ms(ev0_, ev1_, &ms), "event timing");
                 std::swap(L.packed, w);
                 std::swap(L.bias, b);
+                if (tune_verbose)
+                    std::fprintf(stderr, "hip tune %s %s %.2f us\n", key.c_str(), mlvc_hip_conv_variant_name(v),
+                                 1e3 * ms / kReps);
                 if (best_ms < 0.0F || ms < best_ms) {
                     best_ms = ms;
                     best = v;
