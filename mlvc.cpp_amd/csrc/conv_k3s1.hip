@@ -53,6 +53,15 @@ const Variant kTable[] = {
     MLVC_VARIANT_WSR(128, 4, 40, 64, 2, 9),
     MLVC_VARIANT_WSR(128, 4, 48, 64, 2, 9),
     MLVC_VARIANT_WS(128, 8, 32, 64, 2),
+    // Two m-tiles per wave with a 9-step ring.
+    MLVC_VARIANT_WSR(256, 4, 24, 64, 2, 9),
+    MLVC_VARIANT_WSR(256, 2, 48, 64, 2, 9),
+    // Pipelined passes of 32 channels.
+    MLVC_VARIANT_WSP(256, 4, 32, 32, 2, 3),
+    MLVC_VARIANT_WSP(128, 8, 32, 32, 2, 3),
+    MLVC_VARIANT_WSP(128, 4, 32, 32, 2, 9),
+    MLVC_VARIANT_WSP(128, 4, 48, 32, 2, 9),
+    MLVC_VARIANT_WSP(128, 4, 24, 32, 2, 9),
 };
 }  // namespace
 

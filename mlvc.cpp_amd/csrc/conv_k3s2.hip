@@ -30,6 +30,11 @@ const Variant kTable[] = {
     MLVC_VARIANT_WS2(128, 2, 32, 32, 2, 4),
     MLVC_VARIANT_WS2(192, 4, 32, 32, 2, 3),
     MLVC_VARIANT_WS2(192, 2, 32, 64, 2, 3),
+    // Deeper A rings, six waves over 192 output channels (one m-tile
+    // each), and widths dividing 240 (24, 48).
+    MLVC_VARIANT_WS2R(256, 2, 32, 64, 2, 8, 9),
+    MLVC_VARIANT_WS2R(192, 2, 32, 64, 2, 6, 9),
+    MLVC_VARIANT_WS2R(128, 4, 24, 32, 2, 4, 9),
 };
 }  // namespace
 

@@ -30,7 +30,7 @@
 namespace mlvc_hip {
 namespace conv {
 
-template <int BM_, int TH_, int TW_, int SC_, int OCC_ = 2, int S_ = 1, int WAVES_ = 4, int RING_ = 3>
+template <int BM_, int TH_, int TW_, int SC_, int OCC_ = 2, int S_ = 1, int WAVES_ = 4, int RING_ = 3, bool PIPE_ = false>
 struct WsCfg {
     static constexpr int BM = BM_, TH = TH_, TW = TW_, SC = SC_, OCC = OCC_, S = S_;
     static constexpr int KH = 3, KW = 3, TAPS = 9;
@@ -48,7 +48,13 @@ struct WsCfg {
     static constexpr int UNITS = (SC / 8) * IH_T * NSEG;  // 8 channels x 8 columns each
     static constexpr int UNITS_PER_T = (UNITS + kThreads - 1) / kThreads;
     static constexpr int EPI_ROW = BN + 8, EPI_LDS = BM * EPI_ROW;
-    static constexpr int LDS = IN_LDS > EPI_LDS ? IN_LDS : EPI_LDS;  // the plain epilogue's tile aliases the halo
+    // Pipelined passes: two halo buffers; pass p+1 is loaded into registers
+    // at the start of pass p and written to the other buffer after its first
+    // 16-channel step, so one barrier per pass and no exposed staging after
+    // the first pass.
+    static constexpr bool PIPE = PIPE_;
+    static constexpr int NBUF = PIPE ? 2 : 1;
+    static constexpr int LDS = NBUF * IN_LDS > EPI_LDS ? NBUF * IN_LDS : EPI_LDS;  // the plain epilogue's tile aliases the halo
     static constexpr int RING = RING_;               // A-fragment prefetch distance in k-steps
     // Staging units in flight per thread: 2, or 1 where the accumulators and
     // the ring leave no room for a second unit's 32 registers.
@@ -85,38 +91,43 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
     const std::uint16_t* x_img = a.x + static_cast<size_t>(b) * a.ic * hw;
     const __amdgpu_buffer_rsrc_t rx =
         __builtin_amdgcn_make_buffer_rsrc(const_cast<std::uint16_t*>(x_img), 0, static_cast<int>(a.ic * hw2), kRawBufferFlags);
+    // Unit i of this thread (units i0 .. i0 + N - 1 in v[0 .. N-1]): issue
+    // its eight row loads, then write it transposed into the halo buffer at
+    // LDS offset boff.
+    auto issue = [&](int cb, int i, u32x4 (&v)[8]) {
+        const int u = tid + i * C::kThreads;
+        const int sg = u % C::NSEG, yi = (u / C::NSEG) % C::IH_T, c8 = u / (C::NSEG * C::IH_T);
+        const int iy = iy0 + yi, ix = xa + sg * 8;
+        const bool ok = i < C::UNITS_PER_T && u < C::UNITS && iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw;
+        const std::uint32_t off =
+            ok ? static_cast<std::uint32_t>(iy * a.iw + ix) * 2u + static_cast<std::uint32_t>(cb + c8 * 8) * hw2 : kOutOfRange;
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            v[k] = __builtin_amdgcn_raw_buffer_load_b128(rx, static_cast<int>(off == kOutOfRange ? off : off + k * hw2), 0, 0);
+    };
+    auto put = [&](int i, const u32x4 (&v)[8], int boff) {
+        const int u = tid + i * C::kThreads;
+        if (i >= C::UNITS_PER_T || u >= C::UNITS) return;
+        const int sg = u % C::NSEG, yi = (u / C::NSEG) % C::IH_T, c8 = u / (C::NSEG * C::IH_T);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const bool up = j & 1;
+            const int wd = j >> 1;
+            const u32x4 t = {pack_half(v[0][wd], v[1][wd], up), pack_half(v[2][wd], v[3][wd], up),
+                             pack_half(v[4][wd], v[5][wd], up), pack_half(v[6][wd], v[7][wd], up)};
+            const int col = C::S == 1 ? sg * 8 + j : (j & 1) * C::HALF + sg * 4 + (j >> 1);
+            *reinterpret_cast<u32x4*>(&lds[boff + C::at(yi, col) + c8 * 8]) = t;
+        }
+    };
     auto stage = [&](int cb) {
         constexpr int BATCH = C::STAGE_BATCH;  // units in flight per thread (bounds the staging registers)
 #pragma unroll
         for (int i0 = 0; i0 < C::UNITS_PER_T; i0 += BATCH) {
             u32x4 v[BATCH][8];
 #pragma unroll
-            for (int ii = 0; ii < BATCH; ++ii) {
-                const int u = tid + (i0 + ii) * C::kThreads;
-                const int sg = u % C::NSEG, yi = (u / C::NSEG) % C::IH_T, c8 = u / (C::NSEG * C::IH_T);
-                const int iy = iy0 + yi, ix = xa + sg * 8;
-                const bool ok = i0 + ii < C::UNITS_PER_T && u < C::UNITS && iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw;
-                const std::uint32_t off =
-                    ok ? static_cast<std::uint32_t>(iy * a.iw + ix) * 2u + static_cast<std::uint32_t>(cb + c8 * 8) * hw2 : kOutOfRange;
+            for (int ii = 0; ii < BATCH; ++ii) issue(cb, i0 + ii, v[ii]);
 #pragma unroll
-                for (int k = 0; k < 8; ++k)
-                    v[ii][k] = __builtin_amdgcn_raw_buffer_load_b128(rx, static_cast<int>(off == kOutOfRange ? off : off + k * hw2), 0, 0);
-            }
-#pragma unroll
-            for (int ii = 0; ii < BATCH; ++ii) {
-                const int u = tid + (i0 + ii) * C::kThreads;
-                if (i0 + ii >= C::UNITS_PER_T || u >= C::UNITS) continue;
-                const int sg = u % C::NSEG, yi = (u / C::NSEG) % C::IH_T, c8 = u / (C::NSEG * C::IH_T);
-#pragma unroll
-                for (int j = 0; j < 8; ++j) {
-                    const bool up = j & 1;
-                    const int wd = j >> 1;
-                    const u32x4 t = {pack_half(v[ii][0][wd], v[ii][1][wd], up), pack_half(v[ii][2][wd], v[ii][3][wd], up),
-                                     pack_half(v[ii][4][wd], v[ii][5][wd], up), pack_half(v[ii][6][wd], v[ii][7][wd], up)};
-                    const int col = C::S == 1 ? sg * 8 + j : (j & 1) * C::HALF + sg * 4 + (j >> 1);
-                    *reinterpret_cast<u32x4*>(&lds[C::at(yi, col) + c8 * 8]) = t;
-                }
-            }
+            for (int ii = 0; ii < BATCH; ++ii) put(i0 + ii, v[ii], 0);
         }
     };
 
@@ -161,43 +172,74 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
     }
     __syncthreads();
 
+    // One (16-channel step, tap) step of the K loop on the halo buffer at
+    // LDS offset boff.
+    auto kstep = [&](int c16, int tap, int coff, int boff) {
+        const int s = c16 * C::TAPS + tap;
+        const int ky = tap / C::KW, kx = tap % C::KW;
+        half8 bv[C::NT];
+#pragma unroll
+        for (int nt = 0; nt < C::NT; ++nt)
+            bv[nt] = *reinterpret_cast<const half8*>(&lds[boff + pbase[nt] + ky * C::ROW + toff[kx] + coff]);
+        half8 av[C::MT];
+#pragma unroll
+        for (int mt = 0; mt < C::MT; ++mt) {
+            av[mt] = __builtin_bit_cast(half8, ring[tap % C::RING][mt]);
+            ring[tap % C::RING][mt] = frag(min(s + C::RING, total - 1), mt);
+        }
+        // The refill is issued here, before this tap's MFMAs, and
+        // unconditionally (past the last step it re-reads that step):
+        // the wait counter then stays at the ring depth. A conditional
+        // refill made the compiler wait for every load where its
+        // branch joined, and left alone it sinks the loads to their
+        // use, either way exposing the L2 latency every few taps.
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < C::NT; ++nt)
+                acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[mt], bv[nt], acc[mt][nt], 0, 0, 0);
+    };
+
     // ---- K loop: 16-channel step outer, tap inner, in passes of SC channels;
     // no barrier inside a pass.
-    for (int cb = 0; cb < nsteps16 * 16; cb += C::SC) {
-        if (cb > 0) {
-            __syncthreads();  // every wave is done with the previous pass's halo
-            stage(cb);
-            __syncthreads();
-        }
-        const int c16_end = min(nsteps16, (cb + C::SC) / 16);
-        for (int c16 = cb / 16; c16 < c16_end; ++c16) {
-            const int coff = c16 * 16 - cb;
+    if constexpr (C::PIPE) {
+        u32x4 pv[C::UNITS_PER_T][8];
+        int buf = 0;
+        for (int cb = 0; cb < nsteps16 * 16; cb += C::SC) {
+            const bool next = cb + C::SC < nsteps16 * 16;
+            if (next) {
 #pragma unroll
-            for (int tap = 0; tap < C::TAPS; ++tap) {
-                const int s = c16 * C::TAPS + tap;
-                const int ky = tap / C::KW, kx = tap % C::KW;
-                half8 bv[C::NT];
+                for (int i = 0; i < C::UNITS_PER_T; ++i) issue(cb + C::SC, i, pv[i]);
+            }
 #pragma unroll
-                for (int nt = 0; nt < C::NT; ++nt)
-                    bv[nt] = *reinterpret_cast<const half8*>(&lds[pbase[nt] + ky * C::ROW + toff[kx] + coff]);
-                half8 av[C::MT];
+            for (int j = 0; j < C::SC / 16; ++j) {
+                const int c16 = cb / 16 + j;
+                if (c16 < nsteps16) {
 #pragma unroll
-                for (int mt = 0; mt < C::MT; ++mt) {
-                    av[mt] = __builtin_bit_cast(half8, ring[tap % C::RING][mt]);
-                    ring[tap % C::RING][mt] = frag(min(s + C::RING, total - 1), mt);
+                    for (int tap = 0; tap < C::TAPS; ++tap) kstep(c16, tap, j * 16, buf * C::IN_LDS);
                 }
-                // The refill is issued here, before this tap's MFMAs, and
-                // unconditionally (past the last step it re-reads that step):
-                // the wait counter then stays at the ring depth. A conditional
-                // refill made the compiler wait for every load where its
-                // branch joined, and left alone it sinks the loads to their
-                // use, either way exposing the L2 latency every few taps.
-                __builtin_amdgcn_sched_barrier(0);
+                // The next pass's halo goes into the other buffer, which no
+                // wave has read since the previous pass's closing barrier.
+                if (j == 0 && next) {
 #pragma unroll
-                for (int mt = 0; mt < C::MT; ++mt)
+                    for (int i = 0; i < C::UNITS_PER_T; ++i) put(i, pv[i], (buf ^ 1) * C::IN_LDS);
+                }
+            }
+            __syncthreads();
+            buf ^= 1;
+        }
+    } else {
+        for (int cb = 0; cb < nsteps16 * 16; cb += C::SC) {
+            if (cb > 0) {
+                __syncthreads();  // every wave is done with the previous pass's halo
+                stage(cb);
+                __syncthreads();
+            }
+            const int c16_end = min(nsteps16, (cb + C::SC) / 16);
+            for (int c16 = cb / 16; c16 < c16_end; ++c16) {
 #pragma unroll
-                    for (int nt = 0; nt < C::NT; ++nt)
-                        acc[mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av[mt], bv[nt], acc[mt][nt], 0, 0, 0);
+                for (int tap = 0; tap < C::TAPS; ++tap) kstep(c16, tap, c16 * 16 - cb, 0);
             }
         }
     }
@@ -311,6 +353,14 @@ void launch_ws(const ConvArgs& a, dim3 grid, hipStream_t s)
 #define MLVC_VARIANT_WS2(BM, TH, TW, SC, OCC, WAVES)                                                           \
     Variant{"ws_bm" #BM "_" #TH "x" #TW "_k3x3_s2_sc" #SC "_occ" #OCC "_w" #WAVES, BM, TH, TW, 3, 3, 2, 16, nullptr, \
             &launch_ws<WsCfg<BM, TH, TW, SC, OCC, 2, WAVES>>, nullptr, SC}
+// Pipelined passes (two halo buffers, next pass staged under the current one).
+#define MLVC_VARIANT_WSP(BM, TH, TW, SC, OCC, RING)                                                            \
+    Variant{"ws_bm" #BM "_" #TH "x" #TW "_k3x3_s1_sc" #SC "_occ" #OCC "_r" #RING "_pipe", BM, TH, TW, 3, 3, 1, 16,     \
+            nullptr, &launch_ws<WsCfg<BM, TH, TW, SC, OCC, 1, 4, RING, true>>, nullptr, SC}
+// Stride 2 with a ring RING k-steps deep.
+#define MLVC_VARIANT_WS2R(BM, TH, TW, SC, OCC, WAVES, RING)                                                    \
+    Variant{"ws_bm" #BM "_" #TH "x" #TW "_k3x3_s2_sc" #SC "_occ" #OCC "_w" #WAVES "_r" #RING, BM, TH, TW, 3, 3, 2, 16, \
+            nullptr, &launch_ws<WsCfg<BM, TH, TW, SC, OCC, 2, WAVES, RING>>, nullptr, SC}
 
 }  // namespace conv
 }  // namespace mlvc_hip

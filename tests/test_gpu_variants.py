@@ -47,12 +47,16 @@ CASES = [
     ("small_oc_plain", 1, 32, 24, 64, 8, 3, 1, 1, dict(epilogue="lrelu")),
     ("small_oc_residual", 1, 64, 20, 40, 16, 3, 1, 1, dict(epilogue="residual")),
     ("recon_many_tiles", 2, 64, 136, 512, 12, 3, 1, 1, dict(d2s=2)),
+    # Input channels not a multiple of the weight-streaming kernel's pass
+    # width (32 or 64): the last pass is partial.
+    ("ragged_ic_ws", 1, 80, 12, 32, 128, 3, 1, 1, dict(epilogue="lrelu")),
+    ("ragged_ic_ws_d2s", 2, 48, 8, 16, 256, 3, 1, 1, dict(epilogue="lrelu", d2s=2)),
 ]
 
 # Geometries the weight-streaming 3x3 kernel (conv_ws.hpp) takes: NCHW inputs
 # with rows of a multiple of 8 pixels, no concat or SPACE_TO_DEPTH staging.
 WS_CASES = {"mid_4x8", "shuffle_8x16", "many_tiles_s1", "many_tiles_d2s", "residual_d2s", "down_s2", "down_s2_4x8",
-            "many_tiles_s2_rows"}
+            "many_tiles_s2_rows", "ragged_ic_ws", "ragged_ic_ws_d2s"}
 
 
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
