@@ -47,9 +47,19 @@ namespace {
 constexpr int kTH = 4, kTW = 8, kP = kTH * kTW;  // 32 pixels per workgroup
 constexpr int kYS = kP + 8;                       // y staging row stride (halves)
 #ifndef MLVC_DW_RING
-#define MLVC_DW_RING 16
+#define MLVC_DW_RING 24
 #endif
 constexpr int kRing = MLVC_DW_RING;               // weight fragments in flight per wave
+#ifndef MLVC_DW_EARLY
+#define MLVC_DW_EARLY 0
+#endif
+// Ring slots filled before the depthwise stage; the rest are requested
+// between its rows. A wave stalls at a load while the memory request queue
+// is full, so fragments requested up front delay the start of its
+// depthwise work; requested between the depthwise rows, they keep the weight
+// stream going while the VALU works (24 slots, none up front: 12.3-14.1 to
+// 11.8-13.0 us per block).
+constexpr int kEarly = MLVC_DW_EARLY;
 constexpr int kXR = kTH + 2, kXW = kTW + 16;      // staged input rows and columns (x0 - 8 .. x0 + kTW + 7)
 // Halves per staged channel: 304 bytes, 76 dwords, so 16 lanes reading 16
 // bytes at the same offset of 16 consecutive channels hit distinct banks.
@@ -163,7 +173,7 @@ __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArg
     // The weight ring, then the expand bias.
     u32x4 ring[kRing];
 #pragma unroll
-    for (int f = 0; f < kRing; ++f) ring[f] = f < NF ? frag(f) : u32x4{0u, 0u, 0u, 0u};
+    for (int f = 0; f < kEarly; ++f) ring[f] = f < NF ? frag(f) : u32x4{0u, 0u, 0u, 0u};
 
     // Expand accumulators seeded with b1: lane holds rows 8j + hsel + (0..3).
     floatx16 acc1[MT1];
@@ -215,6 +225,16 @@ __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArg
             const int gy = y0 + g * ORT + r;
 #pragma unroll
             for (int ky = 0; ky < 3; ++ky) {
+                if constexpr (kRing > kEarly) {
+                    constexpr int kLate = kRing - kEarly, kPer = (kLate + 3 * ORT - 1) / (3 * ORT);
+                    const int it = r * 3 + ky;
+#pragma unroll
+                    for (int q = 0; q < kPer; ++q) {
+                        const int f = kEarly + it * kPer + q;
+                        if (f < kRing) ring[f] = f < NF ? frag(f) : u32x4{0u, 0u, 0u, 0u};
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
                 const int iy = gy + ky - 1;
                 if (iy < 0 || iy >= a.h) continue;
                 const int rr = r + ky;
