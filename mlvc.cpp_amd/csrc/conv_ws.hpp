@@ -94,16 +94,20 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
     // Unit i of this thread (units i0 .. i0 + N - 1 in v[0 .. N-1]): issue
     // its eight row loads, then write it transposed into the halo buffer at
     // LDS offset boff.
-    auto issue = [&](int cb, int i, u32x4 (&v)[8]) {
+    auto unit_off = [&](int cb, int i) -> std::uint32_t {
         const int u = tid + i * C::kThreads;
         const int sg = u % C::NSEG, yi = (u / C::NSEG) % C::IH_T, c8 = u / (C::NSEG * C::IH_T);
         const int iy = iy0 + yi, ix = xa + sg * 8;
         const bool ok = i < C::UNITS_PER_T && u < C::UNITS && iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw;
-        const std::uint32_t off =
-            ok ? static_cast<std::uint32_t>(iy * a.iw + ix) * 2u + static_cast<std::uint32_t>(cb + c8 * 8) * hw2 : kOutOfRange;
+        return ok ? static_cast<std::uint32_t>(iy * a.iw + ix) * 2u + static_cast<std::uint32_t>(cb + c8 * 8) * hw2 : kOutOfRange;
+    };
+    auto load_row = [&](std::uint32_t off, int k) {  // channel k of a unit
+        return __builtin_amdgcn_raw_buffer_load_b128(rx, static_cast<int>(off == kOutOfRange ? off : off + k * hw2), 0, 0);
+    };
+    auto issue = [&](int cb, int i, u32x4 (&v)[8]) {
+        const std::uint32_t off = unit_off(cb, i);
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
-            v[k] = __builtin_amdgcn_raw_buffer_load_b128(rx, static_cast<int>(off == kOutOfRange ? off : off + k * hw2), 0, 0);
+        for (int k = 0; k < 8; ++k) v[k] = load_row(off, k);
     };
     auto put = [&](int i, const u32x4 (&v)[8], int boff) {
         const int u = tid + i * C::kThreads;
@@ -174,7 +178,12 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
 
     // One (16-channel step, tap) step of the K loop on the halo buffer at
     // LDS offset boff.
-    auto kstep = [&](int c16, int tap, int coff, int boff) {
+    // Pipelined passes: row loads of the next pass, NL per thread, issued
+    // inside the K loop (see below).
+    constexpr int NL = C::UNITS_PER_T * 8;
+    u32x4 pv[C::UNITS_PER_T][8];
+    std::uint32_t poff[C::UNITS_PER_T];
+    auto kstep = [&](int c16, int tap, int coff, int boff, bool pipe_issue) {
         const int s = c16 * C::TAPS + tap;
         const int ky = tap / C::KW, kx = tap % C::KW;
         half8 bv[C::NT];
@@ -186,6 +195,11 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
         for (int mt = 0; mt < C::MT; ++mt) {
             av[mt] = __builtin_bit_cast(half8, ring[tap % C::RING][mt]);
             ring[tap % C::RING][mt] = frag(min(s + C::RING, total - 1), mt);
+        }
+        if (C::PIPE && pipe_issue) {
+#pragma unroll
+            for (int q = 0; q < NL; ++q)
+                if (q * C::TAPS / NL == tap) pv[q / 8][q % 8] = load_row(poff[q / 8], q % 8);
         }
         // The refill is issued here, before this tap's MFMAs, and
         // unconditionally (past the last step it re-reads that step):
@@ -204,24 +218,27 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
     // ---- K loop: 16-channel step outer, tap inner, in passes of SC channels;
     // no barrier inside a pass.
     if constexpr (C::PIPE) {
-        u32x4 pv[C::UNITS_PER_T][8];
+        // The next pass's row loads are spread over the taps of this pass's
+        // first 16-channel step, after each tap's ring refill: a wave stalls
+        // at a load while the memory request queue is full, and issued in one
+        // burst they would hold back the MFMAs behind them. They are written
+        // to the other buffer after the pass's last step (no wave has read
+        // that buffer since the previous pass's closing barrier).
         int buf = 0;
         for (int cb = 0; cb < nsteps16 * 16; cb += C::SC) {
-            const bool next = cb + C::SC < nsteps16 * 16;
+            const bool next = cb + C::SC < nsteps16 * 16;  // only the last pass can be partial
             if (next) {
 #pragma unroll
-                for (int i = 0; i < C::UNITS_PER_T; ++i) issue(cb + C::SC, i, pv[i]);
+                for (int i = 0; i < C::UNITS_PER_T; ++i) poff[i] = unit_off(cb + C::SC, i);
             }
 #pragma unroll
             for (int j = 0; j < C::SC / 16; ++j) {
                 const int c16 = cb / 16 + j;
                 if (c16 < nsteps16) {
 #pragma unroll
-                    for (int tap = 0; tap < C::TAPS; ++tap) kstep(c16, tap, j * 16, buf * C::IN_LDS);
+                    for (int tap = 0; tap < C::TAPS; ++tap) kstep(c16, tap, j * 16, buf * C::IN_LDS, j == 0 && next);
                 }
-                // The next pass's halo goes into the other buffer, which no
-                // wave has read since the previous pass's closing barrier.
-                if (j == 0 && next) {
+                if (j == C::SC / 16 - 1 && next) {
 #pragma unroll
                     for (int i = 0; i < C::UNITS_PER_T; ++i) put(i, pv[i], (buf ^ 1) * C::IN_LDS);
                 }
@@ -239,7 +256,7 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
             const int c16_end = min(nsteps16, (cb + C::SC) / 16);
             for (int c16 = cb / 16; c16 < c16_end; ++c16) {
 #pragma unroll
-                for (int tap = 0; tap < C::TAPS; ++tap) kstep(c16, tap, c16 * 16 - cb, 0);
+                for (int tap = 0; tap < C::TAPS; ++tap) kstep(c16, tap, c16 * 16 - cb, 0, false);
             }
         }
     }
