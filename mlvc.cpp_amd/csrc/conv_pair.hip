@@ -406,38 +406,30 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void c
     // r unit of this lane (lane < 32): 8 channels x 8 pixels of this wave's row.
     const int rc8 = lane % 8, rpx = (lane / 8) * 8;
     u32x4 vin[8], rv[8];
-    auto fetch = [&](const Tile& t) {
+    // Load k (0..7) of this thread's input unit and r unit of tile t; with
+    // valid false every offset is out of range (nothing is read).
+    auto fetch_k = [&](const Tile& t, bool valid, int k) {
         if (tid < XUNITS) {
             const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
                 const_cast<std::uint16_t*>(a.x + static_cast<size_t>(t.b) * csrc * (plane_src / 2)), 0,
                 static_cast<int>(csrc * plane_src), kRawBufferFlags);
             const int ix0 = t.tx0 - 1, xa = ix0 - (((ix0 % 8) + 8) % 8);
             const int iy = t.ty0 - 1 + uyi, ix = xa + usg * 8;
-            const bool ok = iy >= 0 && iy < a.h && ix >= 0 && ix < a.w;
+            const bool ok = valid && iy >= 0 && iy < a.h && ix >= 0 && ix < a.w;
             if constexpr (C::STG == 2) {
                 const std::uint32_t base = static_cast<std::uint32_t>(2 * iy * sw + 2 * ix) * 2u;
-#pragma unroll
-                for (int ql = 0; ql < 2; ++ql) {
-                    // Source channels past the input (the zero padding of the
-                    // last chunk) are not fetched at all.
-                    const bool real = 2 * ug + ql < csrc;
-#pragma unroll
-                    for (int dy = 0; dy < 2; ++dy)
-#pragma unroll
-                        for (int hh = 0; hh < 2; ++hh) {
-                            const std::uint32_t off = ok ? base + static_cast<std::uint32_t>(2 * ug + ql) * plane_src +
-                                                               static_cast<std::uint32_t>(dy * sw * 2 + hh * 16)
-                                                         : kOutOfRange;
-                            vin[(ql * 2 + dy) * 2 + hh] =
-                                real ? __builtin_amdgcn_raw_buffer_load_b128(rx, static_cast<int>(off), 0, 0) : u32x4{0u, 0u, 0u, 0u};
-                        }
-                }
+                const int ql = k >> 2, dy = (k >> 1) & 1, hh = k & 1;
+                // Source channels past the input (the zero padding of the
+                // last chunk) are not fetched at all.
+                const bool real = 2 * ug + ql < csrc;
+                const std::uint32_t off = ok ? base + static_cast<std::uint32_t>(2 * ug + ql) * plane_src +
+                                                   static_cast<std::uint32_t>(dy * sw * 2 + hh * 16)
+                                             : kOutOfRange;
+                vin[k] = real ? __builtin_amdgcn_raw_buffer_load_b128(rx, static_cast<int>(off), 0, 0) : u32x4{0u, 0u, 0u, 0u};
             } else {
                 const std::uint32_t base =
                     ok ? static_cast<std::uint32_t>(iy * a.w + ix) * 2u + static_cast<std::uint32_t>(ug * 8) * hw2 : kOutOfRange;
-#pragma unroll
-                for (int k = 0; k < 8; ++k)
-                    vin[k] = __builtin_amdgcn_raw_buffer_load_b128(rx, static_cast<int>(ok ? base + k * hw2 : kOutOfRange), 0, 0);
+                vin[k] = __builtin_amdgcn_raw_buffer_load_b128(rx, static_cast<int>(ok ? base + k * hw2 : kOutOfRange), 0, 0);
             }
         }
         if (lane < 32) {
@@ -445,16 +437,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void c
                 const_cast<std::uint16_t*>(a.r + static_cast<size_t>(t.b) * C::CR * hw), 0, static_cast<int>(C::CR * hw2),
                 kRawBufferFlags);
             const int oy = t.ty0 + wave, ox = t.tx0 + rpx;
-            const bool ok = oy < a.h && ox < a.w;
+            const bool ok = valid && oy < a.h && ox < a.w;
             const std::uint32_t base = (static_cast<std::uint32_t>(rc8 * 8) * hw + static_cast<std::uint32_t>(oy * a.w + ox)) * 2u;
-#pragma unroll
-            for (int k = 0; k < 8; ++k)
-                rv[k] = __builtin_amdgcn_raw_buffer_load_b128(rr, static_cast<int>(ok ? base + k * hw2 : kOutOfRange), 0, 0);
+            rv[k] = __builtin_amdgcn_raw_buffer_load_b128(rr, static_cast<int>(ok ? base + k * hw2 : kOutOfRange), 0, 0);
         }
     };
 
     int v = static_cast<int>(blockIdx.x);
-    if (v < a.nwg) fetch(tile_of(v));
+    if (v < a.nwg) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) fetch_k(tile_of(v), true, k);
+    }
     for (; v < a.nwg; v += G) {
         const Tile t = tile_of(v);
         // The previous tile's phase A has finished reading the halo tile
@@ -489,7 +482,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void c
             }
         }
         __syncthreads();
-        if (v + G < a.nwg) fetch(tile_of(v + G));
+        // The next tile's loads go out one pair per tap of phase A rather than
+        // in one burst here: a wave stalls at a load while the memory request
+        // queue is full, which would hold back the MFMAs behind the burst.
+        // After the last tile they are issued out of range (nothing is read),
+        // so no branch decides whether they happen.
+        const bool more = v + G < a.nwg;
+        const Tile tn = tile_of(more ? v + G : v);
 
         // ---- phase A: 3x3 conv, BM = 64 ----
         floatx16 acc[C::MTA];
@@ -506,6 +505,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void c
 #pragma unroll
         for (int tap = 0; tap < 9; ++tap) {
             const int ky = tap / 3, kx = tap % 3;
+            if (tap < 8) {
+                fetch_k(tn, more, tap);
+                __builtin_amdgcn_sched_barrier(0);
+            }
             const half8 bv = *reinterpret_cast<const half8*>(&in_s[C::at(wave + ky, pxi + kx) + koff]);
 #pragma unroll
             for (int mt = 0; mt < C::MTA; ++mt) {
