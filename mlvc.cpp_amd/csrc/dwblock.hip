@@ -264,9 +264,14 @@ __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArg
     lds_barrier();
 
     // ---- 2. expand 1x1 C -> E, round, LeakyReLU, round -> es --------------
+    // The B fragment of step ks + 1 is read from LDS during step ks (the
+    // scheduling barrier that keeps the ring refills in place would otherwise
+    // leave each read's latency in front of its MFMAs).
+    half8 bnext = *reinterpret_cast<const half8*>(&ds[pl * DST + koff]);
 #pragma unroll
     for (int ks = 0; ks < KS1; ++ks) {
-        const half8 bv = *reinterpret_cast<const half8*>(&ds[pl * DST + ks * 16 + koff]);
+        const half8 bv = bnext;
+        if (ks + 1 < KS1) bnext = *reinterpret_cast<const half8*>(&ds[pl * DST + (ks + 1) * 16 + koff]);
 #pragma unroll
         for (int m = 0; m < MT1; ++m) {
             const int f = ks * MT1 + m;
@@ -302,9 +307,11 @@ __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArg
     lds_barrier();
 
     // ---- 3. project 1x1 E -> C, round -> ys[channel][pixel] ---------------
+    bnext = *reinterpret_cast<const half8*>(&es[pl * EST + koff]);
 #pragma unroll
     for (int ks = 0; ks < KS2; ++ks) {
-        const half8 bv = *reinterpret_cast<const half8*>(&es[pl * EST + ks * 16 + koff]);
+        const half8 bv = bnext;
+        if (ks + 1 < KS2) bnext = *reinterpret_cast<const half8*>(&es[pl * EST + (ks + 1) * 16 + koff]);
 #pragma unroll
         for (int m = 0; m < MT2; ++m) {
             const int f = NF1 + ks * MT2 + m;
