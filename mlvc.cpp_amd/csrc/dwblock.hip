@@ -14,9 +14,9 @@
 //   * 8 waves (2 per SIMD) for C = 256, so one wave's VALU work and waits
 //     overlap the other's MFMAs;
 //   * every wave runs ONE register ring of kRing weight fragments (16 bytes
-//     per lane, pre-packed in A-fragment order) through both GEMMs, so W1 and
-//     then W2 are in flight from the first instruction to the last MFMA,
-//     across the depthwise stage and the barriers (LDS-only fences);
+//     per lane, pre-packed in A-fragment order) through both GEMMs, filled
+//     between the depthwise rows, so W1 and then W2 are in flight from the
+//     depthwise stage to the last MFMA, across the barriers (LDS-only fences);
 //   * the input tile (6 rows x 24 columns of every channel: the 4x8 tile,
 //     its halo and 8-column alignment) is staged into LDS by coalesced
 //     16-byte loads, consecutive lanes reading consecutive 16-byte pieces of
