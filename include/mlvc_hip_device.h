@@ -229,6 +229,10 @@ int mlvc_hip_concat_channels(const void* a, int ca, const void* b, int cb, void*
                              mlvc_hip_stream s);
 /* Zero fill by kernel (safe inside captured graphs). */
 int mlvc_hip_zero(void* y, size_t bytes, mlvc_hip_stream s);
+/* Fills bytes / 2 FP16 values in [-1, 1), |v| >= 0.5, from a hash of the
+ * element index and seed (deterministic); for timing kernels on data that
+ * loads the matrix cores like real activations. */
+int mlvc_hip_fill_pattern(void* y, size_t bytes, unsigned seed, mlvc_hip_stream s);
 
 /* ---- operators of the real MLVC graphs (NCHW FP16) ----
  * Same values as the reference CPU kernels (backends/cpu/src/

@@ -2024,16 +2024,32 @@ private:
         }
     }
 
+    // Fills every activation buffer (arena, graph inputs, state) with FP16
+    // values in [-1, 1) (pattern = true: matrix cores fed zeros run cooler and
+    // faster than on real data, which can rank tile variants differently) or
+    // zeros.
+    void fill_buffers(bool pattern)
+    {
+        unsigned seed = 1;
+        auto fill = [&](void* p, std::size_t bytes, const char* what) {
+            bytes &= ~std::size_t{1};
+            if (!p || bytes == 0) return;
+            hip_check(pattern ? mlvc_hip_fill_pattern(p, bytes, seed++, stream_) : mlvc_hip_zero(p, bytes, stream_), what);
+        };
+        fill(arena_.ptr, arena_bytes_, "arena fill");
+        for (auto& [id, buf] : input_buf_) fill(buf.ptr, desc_bytes(desc(id)), "input fill");
+        for (auto& b : bindings_)
+            for (auto& buf : b.buf) fill(buf.ptr, b.bytes, "state fill");
+    }
+
     // Measures every eligible tile variant of each conv launch on the real
-    // buffers (zeroed first) and keeps the fastest. All variants of one kernel
-    // size share the K order, so the choice changes timing, never results.
+    // buffers (filled with an FP16 pattern first, zeroed again afterwards) and
+    // keeps the fastest. All variants of one kernel size share the K order, so
+    // the choice changes timing, never results.
     void tune()
     {
         select();
-        hip_check(mlvc_hip_zero(arena_.ptr, arena_bytes_, stream_), "arena clear");
-        for (auto& [id, buf] : input_buf_) hip_check(mlvc_hip_zero(buf.ptr, desc_bytes(desc(id)), stream_), "input clear");
-        for (auto& b : bindings_)
-            for (auto& buf : b.buf) hip_check(mlvc_hip_zero(buf.ptr, b.bytes, stream_), "state clear");
+        fill_buffers(true);
         constexpr int kWarm = 2, kReps = 5;
         // MLVC_HIP_TUNE_FILE=<path>: choices listed there ("<model>:<launch>
         // <variant>" per line) are taken without timing, so separate
@@ -2114,6 +2130,7 @@ private:
             }
             chosen[key] = mlvc_hip_conv_variant_name(best);
         }
+        fill_buffers(false);
         hip_check(mlvc_hip_stream_synchronize(stream_), "stream sync");
         if (write_back) {
             const std::string tmp = std::string(tune_file) + ".tmp" + std::to_string(static_cast<long>(::getpid()));

@@ -307,6 +307,23 @@ __global__ __launch_bounds__(kBlock) void zero_kernel(std::uint8_t* __restrict__
         y[i] = 0;
 }
 
+// FP16 values in [-1, 1) from a hash of (element index, seed): a stand-in
+// for real activations where only the timing of the kernels reading them
+// matters (load-time tuning), since matrix cores fed zeros draw less power
+// and run faster than on real data.
+__global__ __launch_bounds__(kBlock) void pattern_kernel(std::uint16_t* __restrict__ y, size_t count, std::uint32_t seed)
+{
+    for (size_t i = blockIdx.x * static_cast<size_t>(kBlock) + threadIdx.x; i < count;
+         i += static_cast<size_t>(gridDim.x) * kBlock) {
+        std::uint32_t h = static_cast<std::uint32_t>(i) * 0x9E3779B1u ^ (static_cast<std::uint32_t>(i >> 32) + seed) * 0x85EBCA77u;
+        h ^= h >> 15;
+        h *= 0x2C1B3C6Du;
+        h ^= h >> 13;
+        // sign | exponent 14 (0x3800 = 0.5) | 10 random mantissa bits: |v| in [0.5, 1)
+        y[i] = static_cast<std::uint16_t>((h & 0x8000u) | 0x3800u | ((h >> 4) & 0x03FFu));
+    }
+}
+
 bool aligned16(const void* p) { return (reinterpret_cast<std::uintptr_t>(p) & 15u) == 0; }
 
 }  // namespace
@@ -417,6 +434,17 @@ int mlvc_hip_concat_channels(const void* a, int ca, const void* b, int cb, void*
                            static_cast<const std::uint16_t*>(a), sa, static_cast<const std::uint16_t*>(b), sb,
                            static_cast<std::uint16_t*>(y), n);
         check(hipGetLastError(), "concat launch");
+    });
+}
+
+int mlvc_hip_fill_pattern(void* y, size_t bytes, unsigned seed, mlvc_hip_stream s)
+{
+    return guard([&] {
+        if (!y || bytes % 2 != 0) throw std::runtime_error("fill_pattern: null buffer or odd byte count");
+        const size_t count = bytes / 2;
+        hipLaunchKernelGGL(pattern_kernel, dim3(grid_for(count)), dim3(kBlock), 0, to_stream(s), static_cast<std::uint16_t*>(y),
+                           count, static_cast<std::uint32_t>(seed));
+        check(hipGetLastError(), "fill_pattern launch");
     });
 }
 
