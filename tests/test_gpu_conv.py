@@ -286,3 +286,31 @@ def test_conv_clip_epilogue(tmp_path, monkeypatch, k, lo, hi):
     plain.close()
     assert (got == ref).all()
 
+
+
+def test_fill_pattern():
+    """The load-time tuner's operand pattern: FP16 values with |v| in [0.5, 1),
+    both signs, deterministic in the seed, different across seeds, zeros
+    nowhere (the tuner times kernels on it instead of zeroed buffers)."""
+    import ctypes as C
+
+    from devmem import Dev
+
+    dev = Dev()
+    try:
+        L = dev.lib
+        L.mlvc_hip_fill_pattern.argtypes = [C.c_void_p, C.c_size_t, C.c_uint, C.c_void_p]
+        n = (1 << 20) + 3
+        bufs = [dev.alloc(2 * n) for _ in range(3)]
+        for p, seed in zip(bufs, (7, 7, 8)):
+            dev.check(L.mlvc_hip_fill_pattern(p, 2 * n, seed, None))
+        a, b, c = (dev.get(p, (n,), np.uint16) for p in bufs)
+        v = a.view(np.float16).astype(np.float32)
+        assert np.isfinite(v).all() and (np.abs(v) >= 0.5).all() and (np.abs(v) < 1.0).all()
+        assert 0.45 < (v < 0).mean() < 0.55
+        assert (a == b).all() and (a != c).mean() > 0.9
+        assert len(np.unique(a)) > 1500  # sign x 1024 mantissas, spread over them
+        dev.check(L.mlvc_hip_fill_pattern(bufs[0], 0, 1, None))  # empty fill is allowed
+        assert L.mlvc_hip_fill_pattern(bufs[0], 3, 1, None) != 0  # odd byte count rejected
+    finally:
+        dev.close()
