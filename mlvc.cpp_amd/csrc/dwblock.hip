@@ -329,13 +329,19 @@ __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArg
         for (int r = 0; r < 16; ++r)
             ys[(mt * 32 + 8 * (r >> 2) + hsel + (r & 3)) * kYS + pl] = f2h(acc2[m][r]);
     }
-    lds_barrier();
+    // Each wave writes out the channels it computed, so it waits for its own
+    // LDS writes only, not for the other waves (LDS runs a wave's
+    // instructions in order).
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
 
     // ---- 4. residual add, 16-byte rows out ------------------------------
+    static_assert(MT2 * 32 * kTH == 64 * RV, "output rows per lane");
     std::uint16_t* yb = a.y + static_cast<size_t>(b) * C * plane;
 #pragma unroll
     for (int i = 0; i < RV; ++i) {
-        const int q = tid + T * i, ch = q / kTH, row = q % kTH, gy = y0 + row;
+        const int q = lane + 64 * i, ch = wave * MT2 * 32 + q / kTH, row = q % kTH, gy = y0 + row;
         if (gy >= a.h) continue;
         const u32x4 pv = *reinterpret_cast<const u32x4*>(&ys[ch * kYS + row * kTW]);
         const u32x4 rv = *reinterpret_cast<const u32x4*>(&xs[ch * kXCS + (row + 1) * kXW + 8]);  // residual x
