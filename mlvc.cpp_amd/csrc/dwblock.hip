@@ -82,7 +82,10 @@ struct BlockCfg {
     static constexpr int XUNITS = C * kXR * (kXW / 8);                // 16-byte pieces of the staged tile
     static constexpr int XU = (XUNITS + T - 1) / T;                   // per thread
     static constexpr int TAP_PIECES = C * 9 * 2 / 16;                 // 16-byte pieces of the depthwise taps
-    static_assert(C * 9 * 2 % 16 == 0 && TAP_PIECES <= T, "tap staging");
+    static constexpr int WTAP = TAP_PIECES / WAVES;                   // per wave (32 channels)
+    static_assert(C * 9 * 2 % 16 == 0 && TAP_PIECES <= T && WTAP <= 64, "tap staging");
+    // Wave w stages and runs the depthwise taps of channels 32w .. 32w + 31.
+    static_assert(C == 32 * WAVES && TPC == 2 && XUNITS == XU * T, "per-wave channel slices");
     static_assert(C % 128 == 0 && E % 128 == 0 && MT1 >= 1 && MT2 >= 1, "channel counts");
     static_assert(TPC * ORT == kTH && C * kTH % T == 0, "thread mapping");
 };
@@ -150,20 +153,26 @@ __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArg
     // offset past the end (zeros); the taps that would read them are skipped.
     const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<std::uint16_t*>(xb), 0, static_cast<int>(C * plane * 2), kRawBufferFlags);
+    // Wave w loads the pieces of channels 32w .. 32w + 31 (64 consecutive
+    // pieces per instruction, as above) and its depthwise threads use only
+    // those channels: thread (c, g), c = 32w + lane % 32, row group
+    // g = lane / 32. So the staged tile needs no workgroup barrier before the
+    // depthwise stage.
     u32x4 xp[B::XU];
 #pragma unroll
     for (int i = 0; i < B::XU; ++i) {
-        const int u = tid + i * T, k = u % (kXW / 8), r = (u / (kXW / 8)) % kXR, ch = u / ((kXW / 8) * kXR);
+        const int u = wave * 64 * B::XU + lane + 64 * i, k = u % (kXW / 8), r = (u / (kXW / 8)) % kXR,
+                  ch = u / ((kXW / 8) * kXR);
         const int iy = y0 - 1 + r, ix = x0 - 8 + 8 * k;
-        const bool ok = u < B::XUNITS && iy >= 0 && iy < a.h && ix >= 0 && ix < a.w;
+        const bool ok = iy >= 0 && iy < a.h && ix >= 0 && ix < a.w;
         xp[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? ((ch * a.h + iy) * a.w + ix) * 2 : kOutOfRange, 0, 0);
     }
-    const int c = tid % C, g = tid / C;
-    // The taps of all channels as 16-byte pieces, staged with the tile (a
-    // thread's own nine taps per channel would be nine loads, each touching
-    // as many cache lines as the wave has channels).
+    const int c = 32 * wave + (lane & 31), g = lane >> 5;
+    // The taps of this wave's channels as 16-byte pieces, staged with the
+    // tile (a thread's own nine taps per channel would be nine loads, each
+    // touching as many cache lines as the wave has channels).
     u32x4 tp = {0u, 0u, 0u, 0u};
-    if (tid < B::TAP_PIECES) tp = reinterpret_cast<const u32x4*>(a.dw_w)[tid];
+    if (lane < B::WTAP) tp = reinterpret_cast<const u32x4*>(a.dw_w)[wave * B::WTAP + lane];
     const float bdw = a.dw_b[c];
     // The depthwise operands are requested first: loads complete in issue
     // order for the wait counter, so the staging below waits for them only,
@@ -192,11 +201,16 @@ __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArg
 
 #pragma unroll
     for (int i = 0; i < B::XU; ++i) {
-        const int u = tid + i * T, k = u % (kXW / 8), r = (u / (kXW / 8)) % kXR, ch = u / ((kXW / 8) * kXR);
-        if (u < B::XUNITS) *reinterpret_cast<u32x4*>(&xs[ch * kXCS + r * kXW + 8 * k]) = xp[i];
+        const int u = wave * 64 * B::XU + lane + 64 * i, k = u % (kXW / 8), r = (u / (kXW / 8)) % kXR,
+                  ch = u / ((kXW / 8) * kXR);
+        *reinterpret_cast<u32x4*>(&xs[ch * kXCS + r * kXW + 8 * k]) = xp[i];
     }
-    if (tid < B::TAP_PIECES) *reinterpret_cast<u32x4*>(&taps[tid * 8]) = tp;
-    lds_barrier();
+    if (lane < B::WTAP) *reinterpret_cast<u32x4*>(&taps[(wave * B::WTAP + lane) * 8]) = tp;
+    // Lanes read what other lanes of this wave wrote (LDS runs a wave's
+    // instructions in order).
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
     std::uint16_t wdw[9];
 #pragma unroll
     for (int t = 0; t < 9; ++t) wdw[t] = taps[c * 9 + t];
