@@ -184,16 +184,9 @@ __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArg
 #pragma unroll
     for (int f = 0; f < kEarly; ++f) ring[f] = f < NF ? frag(f) : u32x4{0u, 0u, 0u, 0u};
 
-    // Expand accumulators seeded with b1: lane holds rows 8j + hsel + (0..3).
-    floatx16 acc1[MT1];
-#pragma unroll
-    for (int m = 0; m < MT1; ++m)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const floatx4 bv = *reinterpret_cast<const floatx4*>(a.b1 + (wave * MT1 + m) * 32 + 8 * j + hsel);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc1[m][4 * j + i] = bv[i];
-        }
+    // Expand bias (lane rows 8j + hsel + (0..3)), requested with the first
+    // depthwise row's ring fragments rather than up front.
+    floatx4 b1v[MT1][4];
 
     // The scheduler would otherwise sink the ring loads down to their MFMAs
     // (minimising live registers) and serialise the stream on L2 latency.
@@ -249,6 +242,14 @@ __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArg
                     }
                     __builtin_amdgcn_sched_barrier(0);
                 }
+                if (r == 0 && ky == 0) {
+#pragma unroll
+                    for (int m = 0; m < MT1; ++m)
+#pragma unroll
+                        for (int j = 0; j < 4; ++j)
+                            b1v[m][j] = *reinterpret_cast<const floatx4*>(a.b1 + (wave * MT1 + m) * 32 + 8 * j + hsel);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
                 const int iy = gy + ky - 1;
                 if (iy < 0 || iy >= a.h) continue;
                 const int rr = r + ky;
@@ -278,6 +279,13 @@ __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArg
     lds_barrier();
 
     // ---- 2. expand 1x1 C -> E, round, LeakyReLU, round -> es --------------
+    floatx16 acc1[MT1];
+#pragma unroll
+    for (int m = 0; m < MT1; ++m)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc1[m][4 * j + i] = b1v[m][j][i];
     // The B fragment of step ks + 1 is read from LDS during step ks (the
     // scheduling barrier that keeps the ring refills in place would otherwise
     // leave each read's latency in front of its MFMAs).
