@@ -197,33 +197,31 @@ __global__ __launch_bounds__(kBlock) void s2d_kernel(const std::uint16_t* __rest
     }
 }
 
-// Block 2 on input rows of a multiple of 8 pixels (16-byte aligned): one
-// thread takes eight input pixels of the two planes c*4 + dy*2 + {0, 1} at
-// input row y and writes the sixteen output pixels they interleave into, at
-// output row 2y + dy, as two 16-byte stores. grid.x: segments x input rows
-// x dy of one output plane; grid.y: output planes (b*oc + c).
-__global__ __launch_bounds__(kBlock) void d2s2_row8_kernel(const std::uint16_t* __restrict__ x, std::uint16_t* __restrict__ y,
+// Block 2 on input rows of a multiple of 4 pixels (8-byte aligned): one
+// thread takes four input pixels of each of the two planes c*4 + dy*2 +
+// {0, 1} at input row y (8-byte loads) and writes the eight output pixels
+// they interleave into as one 16-byte store, so consecutive lanes load and
+// store consecutive bytes. grid.x: 16-byte output chunks x output rows of
+// one output plane; grid.y: output planes (b*oc + c).
+__global__ __launch_bounds__(kBlock) void d2s2_row4_kernel(const std::uint16_t* __restrict__ x, std::uint16_t* __restrict__ y,
                                                           int h, int w)
 {
-    const int segs = w / 8;
+    typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+    const int cw = w / 4;  // 16-byte chunks per output row
     const int i = blockIdx.x * kBlock + threadIdx.x;
-    if (i >= segs * 2 * h) return;
-    const int Y = i / segs, x0 = (i - Y * segs) * 8, iy = Y >> 1, dy = Y & 1;
+    if (i >= cw * 2 * h) return;
+    const int Y = i / cw, k = i - Y * cw, iy = Y >> 1, dy = Y & 1;
     const size_t plane = blockIdx.y, hw = static_cast<size_t>(h) * w;
-    const std::uint16_t* in = x + (plane * 4 + static_cast<size_t>(dy) * 2) * hw + static_cast<size_t>(iy) * w + x0;
-    const u32x4 a = *reinterpret_cast<const u32x4*>(in);       // dx = 0
-    const u32x4 b = *reinterpret_cast<const u32x4*>(in + hw);  // dx = 1
-    u32x4 lo, hi;
+    const std::uint16_t* in = x + (plane * 4 + static_cast<size_t>(dy) * 2) * hw + static_cast<size_t>(iy) * w + 4 * k;
+    const u32x2 a = *reinterpret_cast<const u32x2*>(in);       // dx = 0
+    const u32x2 b = *reinterpret_cast<const u32x2*>(in + hw);  // dx = 1
+    u32x4 o;
 #pragma unroll
-    for (int k = 0; k < 2; ++k) {
-        lo[2 * k] = (a[k] & 0xFFFFu) | (b[k] << 16);
-        lo[2 * k + 1] = (a[k] >> 16) | (b[k] & 0xFFFF0000u);
-        hi[2 * k] = (a[k + 2] & 0xFFFFu) | (b[k + 2] << 16);
-        hi[2 * k + 1] = (a[k + 2] >> 16) | (b[k + 2] & 0xFFFF0000u);
+    for (int q = 0; q < 2; ++q) {
+        o[2 * q] = (a[q] & 0xFFFFu) | (b[q] << 16);
+        o[2 * q + 1] = (a[q] >> 16) | (b[q] & 0xFFFF0000u);
     }
-    std::uint16_t* out = y + (plane * 2 * h + Y) * (2 * static_cast<size_t>(w)) + 2 * x0;
-    *reinterpret_cast<u32x4*>(out) = lo;
-    *reinterpret_cast<u32x4*>(out + 8) = hi;
+    *reinterpret_cast<u32x4*>(y + (plane * 2 * h + Y) * (2 * static_cast<size_t>(w)) + 8 * k) = o;
 }
 
 // Block 2 on input rows of a multiple of 16 pixels (16-byte aligned): one
@@ -368,10 +366,10 @@ int mlvc_hip_depth_to_space(const void* x, void* y, int n, int in_c, int h, int 
             throw std::runtime_error("depth_to_space: invalid geometry");
         const int oc = in_c / (block * block);
         const size_t planes = static_cast<size_t>(n) * oc;
-        if (block == 2 && w % 8 == 0 && planes <= 65535 && static_cast<size_t>(h) * (w / 4) < (1u << 30) && aligned16(x) &&
+        if (block == 2 && w % 4 == 0 && planes <= 65535 && static_cast<size_t>(h) * (w / 2) < (1u << 30) && aligned16(x) &&
             aligned16(y)) {
-            const unsigned gx = static_cast<unsigned>((static_cast<size_t>(h) * (w / 4) + kBlock - 1) / kBlock);
-            hipLaunchKernelGGL(d2s2_row8_kernel, dim3(gx, static_cast<unsigned>(planes)), dim3(kBlock), 0, to_stream(s),
+            const unsigned gx = static_cast<unsigned>((static_cast<size_t>(h) * (w / 2) + kBlock - 1) / kBlock);
+            hipLaunchKernelGGL(d2s2_row4_kernel, dim3(gx, static_cast<unsigned>(planes)), dim3(kBlock), 0, to_stream(s),
                                static_cast<const std::uint16_t*>(x), static_cast<std::uint16_t*>(y), h, w);
             check(hipGetLastError(), "depth_to_space launch");
             return;

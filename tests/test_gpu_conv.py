@@ -145,12 +145,13 @@ def test_standalone_layout_and_eltwise(tmp_path, rng):
         assert (gg == ww).all(), f"output {i} differs"  # one rounding per op on both sides
 
 
-# Block-2 shuffles on rows of 16-byte segments run the row kernels (D2S:
-# input width % 8 == 0; S2D: input width % 16 == 0), the others the
-# per-element kernels: the residual-block path's 512-channel shuffle, two
-# images, and widths on either side of each condition.
+# Block-2 shuffles on aligned rows run the row kernels (D2S: input width
+# % 4 == 0; S2D: input width % 16 == 0), the others the per-element kernels:
+# the residual-block path's 512-channel shuffle, two images, and widths on
+# either side of each condition.
 @pytest.mark.parametrize("op,shape", [("DEPTH_TO_SPACE", (1, 512, 12, 16)), ("DEPTH_TO_SPACE", (2, 16, 5, 8)),
-                                      ("DEPTH_TO_SPACE", (1, 8, 3, 12)), ("SPACE_TO_DEPTH", (1, 128, 12, 32)),
+                                      ("DEPTH_TO_SPACE", (1, 8, 3, 12)), ("DEPTH_TO_SPACE", (1, 64, 7, 4)),
+                                      ("DEPTH_TO_SPACE", (2, 8, 4, 6)), ("SPACE_TO_DEPTH", (1, 128, 12, 32)),
                                       ("SPACE_TO_DEPTH", (2, 4, 4, 16)), ("SPACE_TO_DEPTH", (1, 4, 6, 24))])
 def test_standalone_pixel_shuffle(tmp_path, rng, op, shape):
     g = graphs.Graph()
