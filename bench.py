@@ -15,7 +15,9 @@ the CPU oracle's frames/s on a bounded sample of the same workload, and the
 codec I/O measurements around the encoder / decoder graphs (conversion
 kernels at 1080p, buffered end-to-end frames/s) and the real-model operator
 kernels (fused ReGLU, feature update, quantisation tails, GATHER, ...)
-against the HBM roofline. A per-kernel table goes to stderr.
+against the HBM roofline, and launch by launch the single 3x3 conv, the
+conv sweep and the two residual-block workloads against their summed
+per-kernel roofline. A per-kernel table goes to stderr.
 """
 
 from __future__ import annotations
@@ -395,6 +397,60 @@ def realops(reps: int, frames: int) -> dict:
             "frames_per_s": frames / (ms * 1e-3), "kernels_per_frame": n_launch, "kernels": kernels}
 
 
+# The smaller workloads, each timed launch by launch beside its summed
+# per-kernel roofline time (min over MFMA and HBM peaks of each launch's
+# algorithmic FLOPs and bytes): (label, synthetic graph, what it is).
+SMALL_CONFIGS = [
+    ("single_conv", "conv3x3_184x320", "3x3 conv 64->64 @184x320 + bias + LeakyReLU(0.01)"),
+    ("conv_sweep", "conv_sweep_640x368", "1x1 and 3x3 convs at 184x320/C64, 92x160/C128, 46x80/C256 and the "
+                                         "stride-2 3x3 convs between the levels"),
+    ("dwblock_92x160_c128", "dwblock_92x160_c128", "depthwise-separable residual block, unshuffle(2)->1x1 4C->C and "
+                                                    "3x3 C->4C->shuffle(2) at 92x160, C=128"),
+    ("dwblock_46x80_c256", "dwblock_46x80_c256", "the same at 46x80, C=256"),
+]
+
+
+def small_configs(reps: int, cold_reps: int, frames: int) -> dict:
+    """Per launch of each SMALL_CONFIGS graph: warm (mean of `reps`
+    back-to-back launches) and cold (median of `cold_reps` single launches
+    after a cache-evicting copy) time, TFLOP/s, GB/s, roofline bound and
+    fraction; per graph: the hipGraph replay time per pass (events around
+    `frames` replays) against the summed per-launch roofline time."""
+    import mlvc_hip
+
+    out = {}
+    for label, config, what in SMALL_CONFIGS:
+        with tempfile.TemporaryDirectory() as d:
+            mlvc_hip.synth_write(config, d, 0)
+            bindings, _ = mlvc_hip.synth_bindings(config)
+            gpu = mlvc_hip.Backend(d, "hip", device_id=0)
+            gpu.load(config, bindings)
+            gpu.upload_inputs([mlvc_hip.synth_input(config, i, 0, s) for i, s in enumerate(gpu.in_shapes)])
+            if bindings:
+                gpu.reset_state()
+            gpu.time_frames(10)
+            replay_us = gpu.time_frames(frames) / frames * 1e3
+            rows = kernel_table(gpu, reps, cold_reps)
+            gpu.close()
+        launches, roof_us = [], 0.0
+        for r in rows:
+            r_us = max(r["flops"] / (PEAK_MFMA_TFLOPS * 1e12), r["bytes"] / (PEAK_HBM_GBS * 1e9)) * 1e6
+            roof_us += r_us
+            launches.append({"name": r["name"], "kernel": r["kind"], "gflop": r["flops"] / 1e9,
+                             "algorithmic_mb": r["bytes"] / 1e6, "us": r["ms"] * 1e3, "tflops": r["tflops"],
+                             "gbs": r["gbs"], "bound": r["bound"], "frac": r["frac"], "roofline_us": r_us,
+                             **({"cold_us": r["cold_ms"] * 1e3, "cold_frac": r["cold_frac"]} if "cold_ms" in r else {})})
+            log(f"{label:20} {r['name'][:22]:22} {r['kind'][:46]:46} {r['ms'] * 1e3:7.1f} us {r['tflops']:7.1f} TFLOP/s "
+                f"{r['gbs']:6.0f} GB/s {r['bound']} {r['frac']:.3f}"
+                + (f"  cold {r['cold_ms'] * 1e3:6.1f} us {r['cold_frac']:.3f}" if "cold_ms" in r else ""))
+        sum_us = sum(l["us"] for l in launches)
+        log(f"{label:20} replay {replay_us:.1f} us per pass, sum of launches {sum_us:.1f} us, summed roofline "
+            f"{roof_us:.2f} us ({roof_us / sum_us:.3f} of the launches' time)")
+        out[label] = {"graph": config, "workload": what, "replay_us": replay_us, "sum_launch_us": sum_us,
+                      "roofline_us": roof_us, "roofline_frac": roof_us / sum_us, "launches": launches}
+    return out
+
+
 def cpu_baseline(model_dir, bindings, shape, budget_s: float):
     import mlvc_hip
     import mlvc_oracle
@@ -445,11 +501,10 @@ PMC_REPS = 10
 CALIB_BYTES = 128 << 20  # calibration stream kernel: reads and writes this many bytes
 
 
-def pmc_pass(indices) -> int:
-    """Dispatches for rocprofv3 --pmc: the calibration stream kernel (FP16
-    LeakyReLU over CALIB_BYTES, so FETCH_SIZE and WRITE_SIZE each have a
-    known algorithmic value) and then the chosen launches of the graph. Their
-    per-dispatch counters, scaled by calibration, give HBM bytes per launch."""
+def calibration_stream() -> None:
+    """PMC_REPS dispatches of the calibration stream kernel: FP16 LeakyReLU
+    over CALIB_BYTES, so FETCH_SIZE and WRITE_SIZE each have a known
+    algorithmic value that scales the counters of the kernels after it."""
     import ctypes as C
 
     import mlvc_hip
@@ -472,6 +527,16 @@ def pmc_pass(indices) -> int:
     dev.mlvc_hip_stream_synchronize(None)
     for b in bufs:
         dev.mlvc_hip_free(b)
+    log(f"pmc calibration: {PMC_REPS} x leaky_relu over {CALIB_BYTES} bytes")
+
+
+def pmc_pass(indices) -> int:
+    """Dispatches for rocprofv3 --pmc: the calibration stream kernel and then
+    the chosen launches of the graph. Their per-dispatch counters, scaled by
+    calibration, give HBM bytes per launch."""
+    import mlvc_hip
+
+    calibration_stream()
     with tempfile.TemporaryDirectory() as d:
         mlvc_hip.synth_write(CONFIG, d, 0)
         bindings, _ = mlvc_hip.synth_bindings(CONFIG)
@@ -485,22 +550,71 @@ def pmc_pass(indices) -> int:
             log(f"pmc launch {i}: {launches[i]['name']} [{launches[i]['kind']}] x{PMC_REPS + 1}")
             gpu.time_launch(i, PMC_REPS)
         gpu.close()
-    log(f"pmc calibration: {PMC_REPS} x leaky_relu over {CALIB_BYTES} bytes")
     return 0
 
 
-def measured_traffic(path, launch_name, kind):
-    """HBM bytes per launch (FETCH_SIZE + WRITE_SIZE, calibrated) for the
-    launch `launch_name` run by kernel variant `kind`, from a committed
-    rocprofv3 --pmc summary; None when no entry was measured on that variant."""
+def measured_traffic(path, launch_names, kind):
+    """HBM bytes per launch (FETCH_SIZE + WRITE_SIZE, calibrated) for a launch
+    among `launch_names` (launches of one variant on one shape) run by kernel
+    variant `kind`, from a committed rocprofv3 --pmc summary; None when no
+    entry was measured on that variant."""
     try:
         for line in pathlib.Path(path).read_text().splitlines():
             f = line.split()
-            if len(f) == 5 and f[0] == "traffic:" and f[1] == launch_name and f[2] == kind:
+            if len(f) == 5 and f[0] == "traffic:" and f[1] in launch_names and f[2] == kind:
                 return float(f[3]) + float(f[4])
     except OSError:
         pass
     return None
+
+
+def group_launches(rows):
+    """Launches of one kernel variant on one shape (same kind, FLOPs and
+    bytes) merged: mean time per launch, number of launches and their summed
+    time, largest summed time first."""
+    groups = {}
+    for r in rows:
+        g = groups.setdefault((r["kind"], r["flops"], r["bytes"]), dict(r, launches=0, total_ms=0.0, names=[]))
+        g["launches"] += 1
+        g["total_ms"] += r["ms"]
+        g["names"].append(r["name"])
+        if "cold_ms" in r:
+            g.setdefault("_cold", []).append(r["cold_ms"])
+    out = []
+    for g in groups.values():
+        g["ms"] = g["total_ms"] / g["launches"]
+        if "_cold" in g:
+            g["cold_ms"] = sum(g["_cold"]) / len(g["_cold"])
+            del g["_cold"]
+        out.append(g)
+    return sorted(out, key=lambda g: -g["total_ms"])
+
+
+def roofline_of(groups, traffic_path) -> dict:
+    """Roofline object of the first group: achieved algorithmic TFLOP/s
+    (MFMA-bound) or GB/s (HBM-bound) of one launch over its mean duration."""
+    dom = groups[0]
+    t = dom["ms"] * 1e-3
+    if dom["bound"] == "mfma":
+        roof = {"bound": "mfma", "achieved": dom["flops"] / t / 1e12, "peak": PEAK_MFMA_TFLOPS, "unit": "TFLOP/s"}
+    else:
+        roof = {"bound": "hbm", "achieved": dom["bytes"] / t / 1e9, "peak": PEAK_HBM_GBS, "unit": "GB/s"}
+    roof["frac"] = roof["achieved"] / roof["peak"]
+    names = dom["names"] or [dom["name"]]
+    roof["traffic"] = measured_traffic(traffic_path, names, dom["kind"])
+    roof["kernel"] = f"{names[0]} [{dom['kind']}]" if len(names) == 1 else \
+        f"{names[0]}..{names[-1]} ({len(names)} launches) [{dom['kind']}]"
+    roof["kernel_ms"] = dom["ms"]
+    roof["launches_per_frame"] = dom["launches"]
+    if "total_ms" in dom:
+        roof["frame_share"] = dom["total_ms"] / sum(g["total_ms"] for g in groups)
+    if "cold_ms" in dom:
+        roof["kernel_cold_ms"] = dom["cold_ms"]
+        cold_t = dom["cold_ms"] * 1e-3
+        roof["frac_cold"] = (dom["flops"] / cold_t / 1e12 / PEAK_MFMA_TFLOPS if dom["bound"] == "mfma"
+                             else dom["bytes"] / cold_t / 1e9 / PEAK_HBM_GBS)
+    roof["algorithmic_per_launch"] = {"flops": dom["flops"], "bytes": dom["bytes"]}
+    return roof
 
 
 def main() -> int:
@@ -522,6 +636,14 @@ def main() -> int:
     ap.add_argument("--standalone-only", action="store_true",
                     help="run only the standalone kernel measurements (for a kernel trace of them); no JSON line")
     ap.add_argument("--standalone-cold", type=int, default=20, help="cold launches timed per standalone kernel")
+    ap.add_argument("--no-small-configs", action="store_true",
+                    help="skip the single-conv, conv-sweep and residual-block workloads")
+    ap.add_argument("--small-configs-only", action="store_true",
+                    help="run only the single-conv, conv-sweep and residual-block workloads; no JSON line")
+    ap.add_argument("--small-frames", type=int, default=100, help="graph replays timed per small workload")
+    ap.add_argument("--codec-only", action="store_true",
+                    help="run only the codec I/O conversion kernels (after the calibration stream kernel, for "
+                         "rocprofv3 kernel traces and counter passes); no JSON line")
     ap.add_argument("--cold-frames", type=int, default=50,
                     help="frames timed with L2 and MALL flushed before each (0: skip)")
     ap.add_argument("--api-frames", type=int, default=30,
@@ -551,6 +673,16 @@ def main() -> int:
         return pmc_pass([int(i) for i in args.pmc_pass.split(",") if i])
     if args.standalone_only:
         log_standalone(standalone_kernels(args.kernel_reps, args.standalone_cold))
+        return 0
+    if args.small_configs_only:
+        small_configs(args.kernel_reps, args.launch_cold_reps, args.small_frames)
+        return 0
+    if args.codec_only:
+        calibration_stream()
+        c = codec_io_kernels(args.kernel_reps)
+        log(f"codec I/O: frame->model {c['frame_to_model_us']:.2f} us ({c['frame_to_model_gbs']:.0f} GB/s), "
+            f"model->frame {c['model_to_frame_us']:.2f} us ({c['model_to_frame_gbs']:.0f} GB/s), "
+            f"{args.kernel_reps + 3} launches each")
         return 0
 
     with tempfile.TemporaryDirectory() as d:
@@ -582,20 +714,13 @@ def main() -> int:
             + (f"; cold (L2 + MALL flushed) median {cold_ms['median']:.3f} ms (p10 {cold_ms['p10']:.3f}, "
                f"p90 {cold_ms['p90']:.3f})" if cold_ms else ""))
         rows = kernel_table(gpu, args.kernel_reps, args.launch_cold_reps)
-        dom = max(rows, key=lambda r: r["ms"])
-        dom_t = dom["ms"] * 1e-3
-        if dom["bound"] == "mfma":
-            roof = {"bound": "mfma", "achieved": dom["flops"] / dom_t / 1e12, "peak": PEAK_MFMA_TFLOPS,
-                    "unit": "TFLOP/s"}
-        else:
-            roof = {"bound": "hbm", "achieved": dom["bytes"] / dom_t / 1e9, "peak": PEAK_HBM_GBS, "unit": "GB/s"}
-        roof["frac"] = roof["achieved"] / roof["peak"]
-        roof["traffic"] = measured_traffic(args.traffic, dom["name"], dom["kind"])
-        roof["kernel"] = f"{dom['name']} [{dom['kind']}]"
-        roof["kernel_ms"] = dom["ms"]
-        if "cold_ms" in dom:
-            roof["kernel_cold_ms"] = dom["cold_ms"]
-            roof["frac_cold"] = dom["cold_frac"]
+        # The dominant kernel is the one with the largest share of the frame:
+        # launches of one kernel variant on one shape (the 12 fused residual
+        # blocks) count together. The longest single launch goes beside it.
+        roof = roofline_of(group_launches(rows), args.traffic)
+        longest = roofline_of([dict(max(rows, key=lambda r: r["ms"]), launches=1, names=None)], args.traffic)
+        roof["longest_launch"] = {k: longest[k] for k in ("kernel", "kernel_ms", "bound", "achieved", "unit", "frac",
+                                                          "traffic", "kernel_cold_ms", "frac_cold") if k in longest}
         log(f"{'#':>3} {'launch':28} {'kernel':48} {'us':>9} {'TFLOP/s':>8} {'GB/s':>8} {'AI':>7} bound frac"
             + ("  cold us  frac" if args.launch_cold_reps > 0 else ""))
         for r in rows:
@@ -637,6 +762,10 @@ def main() -> int:
         ops = realops(args.kernel_reps, args.realops_frames)
         log(f"realops: {ops['frames_per_s']:.0f} frames/s, {ops['kernels_per_frame']} kernels/frame")
 
+    small = None
+    if not args.no_small_configs:
+        small = small_configs(args.kernel_reps, args.launch_cold_reps, args.small_frames)
+
     conv_tflops = conv_flops * fps / 1e12
     line = {
         "metric": "conv-graph frames/s @1920x1088 + FP16 conv TFLOP/s (% MFMA peak), 1 GPU",
@@ -670,6 +799,7 @@ def main() -> int:
         "codec_io": codec,
         "realops": ops,
         "standalone": alone,
+        "small_configs": small,
     }
     if rank == 0:
         print(json.dumps(line), flush=True)

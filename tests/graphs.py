@@ -205,9 +205,12 @@ def to_float(h) -> np.ndarray:
 
 
 def single_conv_graph(directory, model, n, ic, h, w, oc, k, stride, pad, groups=1, epilogue=None, s2d=0, d2s=0,
-                      concat_ic=0, seed=0, wstd=None):
+                      concat_ic=0, seed=0, wstd=None, zero_sum=False):
     """One conv (optionally fed by SPACE_TO_DEPTH or CONCAT, followed by
-    LeakyReLU / residual ADD and DEPTH_TO_SPACE). Returns the input shapes."""
+    LeakyReLU / residual ADD and DEPTH_TO_SPACE). Returns the input shapes.
+    zero_sum: each output channel's weights sum to zero (before FP16
+    rounding) and the bias is small, so an input with a large constant part
+    gives partial sums far larger than the result."""
     rng = np.random.default_rng(seed)
     g = Graph()
     inputs = []
@@ -225,8 +228,11 @@ def single_conv_graph(directory, model, n, ic, h, w, oc, k, stride, pad, groups=
         inputs.append(g.shape(x))
     icg = ic // groups
     std = wstd if wstd is not None else 1.0 / np.sqrt(icg * k * k)
-    wt = g.weight_fp16("w", rng.normal(0, std, (oc, icg, k, k)))
-    bt = g.weight_fp16("b", rng.normal(0, 0.1, (oc,)))
+    wv = rng.normal(0, std, (oc, icg, k, k))
+    if zero_sum:
+        wv -= wv.mean(axis=(1, 2, 3), keepdims=True)
+    wt = g.weight_fp16("w", wv)
+    bt = g.weight_fp16("b", rng.normal(0, 0.001 if zero_sum else 0.1, (oc,)))
     y = g.conv("y", x, wt, bt, (stride, stride), (pad, pad, pad, pad), groups)
     if epilogue == "lrelu":
         y = g.leaky_relu("y_act", y, 0.01)
