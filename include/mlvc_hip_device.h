@@ -106,14 +106,37 @@ typedef struct mlvc_hip_conv_desc {
     int out_d2s_block;
     int variant;                       /* tile configuration; set by mlvc_hip_conv_plan */
     int vector_io;                     /* 16-byte row staging eligible; set by mlvc_hip_conv_plan */
+    int ksplit, split_c;               /* split K; set by mlvc_hip_conv_plan (below) */
+    void* workspace;                   /* FP32 partials of a split conv, mlvc_hip_conv_workspace_bytes */
+    size_t workspace_bytes;
 } mlvc_hip_conv_desc;
 
 /* Chooses the kernel variant for the geometry by a cost model (sets
  * desc->variant and desc->vector_io). Every 3x3 variant accumulates in the
  * same K order, and so does every 1x1 variant, so the choice never changes
  * results. Role of the reference's per-shape tile choice by fixed thresholds
- * (backends/driver_cubin/src/execution_plan.cpp:151-181, 374-432). */
+ * (backends/driver_cubin/src/execution_plan.cpp:151-181, 374-432).
+ *
+ * Also sets the split K of the geometry (a fixed rule of the conv geometry
+ * alone, independent of the variant, the epilogue and the fusions, so it
+ * never depends on tuning and fused and unfused schedules agree): a 1x1
+ * conv with K = ic >= 576 (above the 512-channel projections of the fused
+ * residual block, which are not split) and fewer than 512 work items of 128
+ * output channels x 128 pixels (items = n * ceil(oc/128) * ceil(oh*ow/128))
+ * is split into ksplit =
+ * ceil(ic / split_c) ranges of input channels, split_c = 64 * ceil(ic /
+ * (64 * s)), s = min(8, 512 / items, ic / 64) (integer division; no split
+ * when s <= 1). Split s sums its channels in the usual K order into an FP32
+ * partial (split 0 seeded with the bias, the others with zero); a second
+ * kernel adds the partials in split order, rounds to FP16 and applies the
+ * epilogue (ReGLU included) and the DEPTH_TO_SPACE store. Split convs run on
+ * the conv_mfma variants only and need desc->workspace (FP32 partials,
+ * mlvc_hip_conv_workspace_bytes; 16-byte aligned). The reference's role for
+ * this: its small-tile choice where a large-tile grid would be under two
+ * waves of SMs (driver_cubin/src/execution_plan.cpp:379-391). */
 int mlvc_hip_conv_plan(mlvc_hip_conv_desc* desc);
+/* Bytes of FP32 partials a launch of desc needs (0 when not split). */
+size_t mlvc_hip_conv_workspace_bytes(const mlvc_hip_conv_desc* desc);
 /* Lists every variant that can run the geometry (for measuring them on the
  * device and keeping the fastest); *count receives the total. */
 int mlvc_hip_conv_candidates(const mlvc_hip_conv_desc* desc, int* variants, int capacity, int* count);

@@ -1543,6 +1543,7 @@ private:
         }
         L.y = out;
         hip_check(mlvc_hip_conv_plan(&d), "conv planning");
+        if (d.ksplit > 1) tags = "+split" + std::to_string(d.ksplit) + tags;
         if (const std::string want = forced_conv_variant(); !want.empty()) {
             int count = 0;
             hip_check(mlvc_hip_conv_candidates(&d, nullptr, 0, &count), "conv candidates");
@@ -1858,6 +1859,10 @@ private:
         }
         arena_bytes_ = peak;
         arena_ = DeviceMem(peak);
+        for (const auto& lp : launches_)
+            if (lp->kind == Launch::kConv)
+                workspace_bytes_ = std::max(workspace_bytes_, mlvc_hip_conv_workspace_bytes(&lp->conv));
+        if (workspace_bytes_) workspace_ = DeviceMem(workspace_bytes_);
     }
 
     void allocate_io()
@@ -1898,6 +1903,8 @@ private:
             d.y = ptr(l.y, parity);
             d.packed_w = l.packed.ptr;
             d.bias = static_cast<const float*>(l.bias.ptr);
+            d.workspace = workspace_.ptr;
+            d.workspace_bytes = workspace_bytes_;
             hip_check(mlvc_hip_conv_launch(&d, stream_), "conv launch");
             break;
         }
@@ -2256,6 +2263,10 @@ private:
     std::map<TensorId, std::size_t> offset_;
     std::size_t arena_bytes_ = 0;
     DeviceMem arena_;
+    // FP32 partials of the split-K convs: one buffer for all of them (they
+    // run one after another on the stream), sized for the largest.
+    std::size_t workspace_bytes_ = 0;
+    DeviceMem workspace_;
     std::map<TensorId, DeviceMem> input_buf_;
     std::map<TensorId, DeviceMem> const_buf_;  // initializers read by elementwise / layout operators
     std::map<TensorId, int> consumers_;

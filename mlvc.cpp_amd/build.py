@@ -4,7 +4,8 @@ Outputs (git-ignored, shipped with the tree to the GPU host):
   mlvc.cpp_amd/lib/libmlvc_hip_device.so  gfx950 kernels + device C ABI (hipcc)
   mlvc.cpp_amd/lib/libmlvc_hip.so         C++20 runtime + "hip" backend + backend C ABI (g++); with
                                           MLVC_EMBED_MODEL_ROOT=<dir>, also the model bundles below <dir>
-                                          (<profile>/<WxH>/) as an embedded image (python/mlvc_embed.py)
+                                          (<profile>/<WxH>/) as an embedded image (python/mlvc_embed.py;
+                                          MLVC_EMBED_PROFILES=<profiles.json> selects and orders them)
   oracle/liboracle.so                     CPU oracle (test infrastructure, g++)
   oracle/_ref/libmlvc_ref_kernels.so      reference CPU kernels, when the reference checkout exists
 
@@ -83,7 +84,9 @@ def build_all(jobs: int | None = None, verbose: bool = True) -> None:
         # library just linked, then the library is linked again with the
         # image's objects (the payload is .incbin'd at assembly time).
         out = OBJ / "embedded-models"
-        _run([sys.executable, str(PKG / "python" / "mlvc_embed.py"), "--model-root", embed_root, "--out-dir", str(out)])
+        registry = os.environ.get("MLVC_EMBED_PROFILES")
+        _run([sys.executable, str(PKG / "python" / "mlvc_embed.py"), "--model-root", embed_root, "--out-dir", str(out)]
+             + (["--profiles", registry] if registry else []))
         image = []
         for src in ("mlvc_embedded_models.S", "mlvc_embedded_models_index.c"):
             image.append(str(out / (src + ".o")))

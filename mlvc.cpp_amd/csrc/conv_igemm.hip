@@ -40,6 +40,68 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(ConvArgs a, int n)
     }
 }
 
+// Split K, second kernel: out = epilogue(fp16(part[0] + part[1] + ...)) for
+// every output of the conv geometry, the partials added in split order
+// (FP32, nearest even), stored plainly or through DEPTH_TO_SPACE. Four
+// consecutive outputs per thread when the plane is a multiple of 4.
+__device__ __forceinline__ float splitk_sum(const ConvArgs& a, size_t stride, size_t e)
+{
+    float v = a.part[e];
+    for (int sp = 1; sp < a.ksplit; ++sp) v = v + a.part[sp * stride + e];
+    return v;
+}
+
+__global__ __launch_bounds__(256) void conv_splitk_reduce_kernel(ConvArgs a, int n)
+{
+    if (a.epi == MLVC_EPI_REGLU) {
+        // Output channel g of the G-channel ReGLU output pairs the rounded
+        // sums of rows 64 (g / 32) + g % 32 (gate) and that + 32 (linear).
+        const size_t ohw = static_cast<size_t>(a.oh) * a.ow, stride = static_cast<size_t>(n) * a.oc * ohw;
+        const int half = a.oc / 2;
+        const size_t total = static_cast<size_t>(n) * half * ohw;
+        for (size_t e = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; e < total;
+             e += static_cast<size_t>(gridDim.x) * blockDim.x) {
+            const size_t p = e % ohw;
+            const int g = static_cast<int>((e / ohw) % half), b = static_cast<int>(e / (ohw * half));
+            const int rg = (g / 32) * 64 + g % 32;
+            const size_t base = static_cast<size_t>(b) * a.oc * ohw + p;
+            const float vg = splitk_sum(a, stride, base + static_cast<size_t>(rg) * ohw);
+            const float vl = splitk_sum(a, stride, base + static_cast<size_t>(rg + 32) * ohw);
+            a.y[e] = reglu_h(f2h(vg), f2h(vl), a.lo, a.hi);
+        }
+        return;
+    }
+    const size_t ohw = static_cast<size_t>(a.oh) * a.ow;
+    const size_t total = static_cast<size_t>(n) * a.oc * ohw, stride = total;
+    const bool quad = ohw % 4 == 0;
+    const size_t units = quad ? total / 4 : total;
+    for (size_t u = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; u < units;
+         u += static_cast<size_t>(gridDim.x) * blockDim.x) {
+        const size_t e0 = quad ? 4 * u : u;
+        float v[4];
+        if (quad) {
+            const floatx4 p0 = *reinterpret_cast<const floatx4*>(a.part + e0);
+            v[0] = p0[0]; v[1] = p0[1]; v[2] = p0[2]; v[3] = p0[3];
+            for (int sp = 1; sp < a.ksplit; ++sp) {
+                const floatx4 p = *reinterpret_cast<const floatx4*>(a.part + sp * stride + e0);
+                v[0] = v[0] + p[0];
+                v[1] = v[1] + p[1];
+                v[2] = v[2] + p[2];
+                v[3] = v[3] + p[3];
+            }
+        } else {
+            v[0] = a.part[e0];
+            for (int sp = 1; sp < a.ksplit; ++sp) v[0] = v[0] + a.part[sp * stride + e0];
+        }
+        for (int i = 0; i < (quad ? 4 : 1); ++i) {
+            const size_t e = e0 + i;
+            const int ox = static_cast<int>(e % a.ow), oy = static_cast<int>((e / a.ow) % a.oh);
+            const int oc = static_cast<int>((e / ohw) % a.oc), b = static_cast<int>(e / (ohw * a.oc));
+            store_output(a, finish(a, v[i], b, oc, oy, ox), b, oc, oy, ox);
+        }
+    }
+}
+
 // ---------------------------------------------------------------- variants
 
 int cu_count()
@@ -127,9 +189,31 @@ void kernel_geometry(const mlvc_hip_conv_desc& d, int& ih, int& iw, int& oh, int
     }
 }
 
+// Split K of a geometry (see mlvc_hip_conv_plan in the header): a fixed
+// function of the geometry, so the summation order never depends on the
+// tile variant or on tuning.
+void split_rule(const mlvc_hip_conv_desc& d, int& ksplit, int& split_c)
+{
+    ksplit = 1;
+    split_c = d.ic;
+    if (d.kh != 1 || d.kw != 1 || d.ic < 576) return;
+    const long long items =
+        static_cast<long long>(d.n) * ((d.oc + 127) / 128) * ((static_cast<long long>(d.oh) * d.ow + 127) / 128);
+    const long long s = std::min<long long>({8, 512 / items, d.ic / 64});
+    if (s <= 1) return;
+    const int c = static_cast<int>(64 * ((d.ic + 64 * s - 1) / (64 * s)));
+    const int k = (d.ic + c - 1) / c;
+    if (k > 1) {
+        ksplit = k;
+        split_c = c;
+    }
+}
+
 bool eligible(const mlvc_hip_conv_desc& d, const Variant& k)
 {
     if (k.bm == 0 || k.kh != d.kh || k.kw != d.kw || k.s != d.stride_h || k.s != d.stride_w) return false;
+    // Split K: conv_mfma variants whose chunk divides the split.
+    if (d.ksplit > 1 && (k.ws_ic || d.split_c % k.kc != 0)) return false;
     // ReGLU pairs gate and linear rows inside 64-row blocks of one tile.
     if (d.epilogue == MLVC_EPI_REGLU && k.bm % 64 != 0) return false;
     if (d.kh == 1 && (d.pad_h || d.pad_w)) return false;
@@ -140,6 +224,10 @@ bool eligible(const mlvc_hip_conv_desc& d, const Variant& k)
         return false;
     int ih, iw, oh, ow;
     kernel_geometry(d, ih, iw, oh, ow);
+    // ...and its 16-byte row staging keeps buffer offsets (up to KC channel
+    // planes past the last one) below 2^31, as the launch requires.
+    if (k.ws_ic && (static_cast<std::uint64_t>(d.ic) + k.kc) * static_cast<std::uint64_t>(ih) * iw * 2 >= (1ull << 31))
+        return false;
     const bool flat = ih == 1 && oh == 1 && d.kh == 1 && d.kw == 1;
     return !(d.kh == 1 && flat != (k.th == 1));
 }
@@ -155,6 +243,7 @@ int mlvc_hip_conv_plan(mlvc_hip_conv_desc* desc)
 {
     return guard([&] {
         validate(*desc, false);
+        split_rule(*desc, desc->ksplit, desc->split_c);
         const mlvc_hip_conv_desc& d = *desc;
         int ih, iw, oh, ow;
         kernel_geometry(d, ih, iw, oh, ow);
@@ -175,10 +264,20 @@ int mlvc_hip_conv_plan(mlvc_hip_conv_desc* desc)
             }
         }
         desc->variant = best;
+        if (best == 0) {  // the direct fallback sums every channel itself
+            desc->ksplit = 1;
+            desc->split_c = d.ic;
+        }
         // 16-byte row-segment staging: plain or channel-concat input whose
         // split falls on 8 channels, rows of 8-aligned width.
         desc->vector_io = best != 0 && d.in_s2d_block <= 1 && (!d.x2 || d.ic_split % 8 == 0) && iw % 8 == 0;
     });
+}
+
+size_t mlvc_hip_conv_workspace_bytes(const mlvc_hip_conv_desc* desc)
+{
+    if (!desc || desc->ksplit <= 1) return 0;
+    return static_cast<size_t>(desc->ksplit) * desc->n * desc->oc * desc->oh * desc->ow * sizeof(float);
 }
 
 int mlvc_hip_conv_candidates(const mlvc_hip_conv_desc* desc, int* out, int capacity, int* count)
@@ -249,10 +348,15 @@ int mlvc_hip_conv_pack(const mlvc_hip_conv_desc* desc, const uint16_t* w, void* 
     });
 }
 
-int mlvc_hip_conv_launch(const mlvc_hip_conv_desc* desc, mlvc_hip_stream s)
+}  // extern "C"
+
+namespace mlvc_hip {
+namespace {
+
+// The launch behind mlvc_hip_conv_launch and mlvc_hip_conv_launch_noalloc.
+void launch_conv(const mlvc_hip_conv_desc& d, void* s)
 {
-    return guard([&] {
-        const mlvc_hip_conv_desc& d = *desc;
+    {
         validate(d, true);
         const Variant& k = variant_of(d);
         ConvArgs a{};
@@ -277,6 +381,19 @@ int mlvc_hip_conv_launch(const mlvc_hip_conv_desc* desc, mlvc_hip_stream s)
         a.alpha = d.alpha;
         a.lo = d.clip_lo;
         a.hi = d.clip_hi;
+        a.ksplit = 1;
+        a.split_c = d.ic;
+        if (d.ksplit > 1) {
+            if (k.bm == 0 || k.ws_ic || d.split_c <= 0 || d.split_c % k.kc != 0 ||
+                static_cast<long long>(d.split_c) * (d.ksplit - 1) >= d.ic || static_cast<long long>(d.split_c) * d.ksplit < d.ic)
+                throw std::runtime_error("conv: split K needs a conv_mfma variant whose chunk divides the split");
+            if (!d.workspace || d.workspace_bytes < mlvc_hip_conv_workspace_bytes(&d) ||
+                (reinterpret_cast<std::uintptr_t>(d.workspace) & 15u))
+                throw std::runtime_error("conv: split K needs a 16-byte aligned workspace of mlvc_hip_conv_workspace_bytes");
+            a.ksplit = d.ksplit;
+            a.split_c = d.split_c;
+            a.part = static_cast<float*>(d.workspace);
+        }
         if (k.bm == 0) {
             if (d.epilogue == MLVC_EPI_REGLU) throw std::runtime_error("conv: no tile variant runs this ReGLU conv");
             a.ih = d.ih; a.iw = d.iw; a.oh = d.oh; a.ow = d.ow;
@@ -300,9 +417,9 @@ int mlvc_hip_conv_launch(const mlvc_hip_conv_desc* desc, mlvc_hip_stream s)
             a.tiles = a.tiles_x * ((a.oh + k.th - 1) / k.th);
             a.ocbs = (d.oc + k.bm - 1) / k.bm;
             const long long nwg = static_cast<long long>(a.tiles) * a.ocbs * d.n;
-            if (nwg > 0x7FFFFFFF) throw std::runtime_error("conv: grid too large");
+            if (nwg * a.ksplit > 0x7FFFFFFF) throw std::runtime_error("conv: grid too large");
             a.nwg = static_cast<int>(nwg);
-            const dim3 grid(static_cast<unsigned>(a.nwg));
+            const dim3 grid(static_cast<unsigned>(a.nwg * a.ksplit));
             // SPACE_TO_DEPTH(2) vector staging: 32-byte aligned source rows
             // and offsets (up to KC/4 channel planes past the end) < 2^31.
             const std::uint64_t src_plane = static_cast<std::uint64_t>(a.ih) * a.iw * 4 * 2;
@@ -310,8 +427,33 @@ int mlvc_hip_conv_launch(const mlvc_hip_conv_desc* desc, mlvc_hip_stream s)
                                  a.iw % 8 == 0 && (static_cast<std::uint64_t>(d.ic / 4) + k.kc / 4 + 1) * src_plane < (1ull << 31);
             if (k.ws_ic && !vec) throw std::runtime_error("conv: variant needs 16-byte row staging");
             (s2d_vec ? k.launch_s2d : vec ? k.launch_vec : k.launch_scalar)(a, grid, to_stream(s));
+            if (a.ksplit > 1) {
+                ConvArgs r = a;  // the reduce works in the real output geometry
+                r.ih = d.ih;
+                r.iw = d.iw;
+                r.oh = d.oh;
+                r.ow = d.ow;
+                const size_t ohw = static_cast<size_t>(d.oh) * d.ow;
+                const size_t units = d.epilogue == MLVC_EPI_REGLU ? static_cast<size_t>(d.n) * (d.oc / 2) * ohw
+                                                                  : static_cast<size_t>(d.n) * d.oc * (ohw % 4 == 0 ? ohw / 4 : ohw);
+                const unsigned blocks = static_cast<unsigned>(std::min<size_t>((units + 255) / 256, 8192));
+                hipLaunchKernelGGL(conv_splitk_reduce_kernel, dim3(blocks), dim3(256), 0, to_stream(s), r, d.n);
+            }
         }
         check(hipGetLastError(), "conv kernel launch");
+    }
+}
+
+}  // namespace
+}  // namespace mlvc_hip
+
+extern "C" {
+
+int mlvc_hip_conv_launch(const mlvc_hip_conv_desc* desc, mlvc_hip_stream s)
+{
+    return guard([&] {
+        if (!desc) throw std::runtime_error("conv: null descriptor");
+        launch_conv(*desc, s);
     });
 }
 

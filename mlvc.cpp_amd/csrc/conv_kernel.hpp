@@ -58,6 +58,12 @@ struct ConvArgs {
     float lo, hi;  // MLVC_EPI_CLAMP / MLVC_EPI_REGLU clip bounds
     int tiles_x, nchunks;
     int tiles, ocbs, nwg;  // pixel tiles per image, output-channel blocks, workgroups (tiles*ocbs*n)
+    // Split K: ksplit > 1 workgroups per (tile, output-channel block), split
+    // s summing input channels [s * split_c, (s + 1) * split_c) (split_c a
+    // multiple of KC) into an FP32 partial part[s][n][oc][oh][ow]; split 0
+    // seeds its accumulators with the bias, the others with zero.
+    int ksplit, split_c;
+    float* part;
 };
 
 // KC consecutive channels [c0, c0 + KC) of input pixel (iy, ix) of batch b,
@@ -260,8 +266,13 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
     const int mt0 = wm * C::MT;                        // first m-tile of this wave
     // Logical work item: output-channel block fastest, then pixel tiles in
     // row-major order, then images; each XCD runs a contiguous range of them.
-    const int item = xcd_order(blockIdx.x, a.nwg);
+    // With split K the splits are outermost, so an XCD's range shares one
+    // split's weights.
+    const int item_all = xcd_order(blockIdx.x, a.nwg * a.ksplit);
+    const int split = item_all / a.nwg, item = item_all - split * a.nwg;
     const int ocb = item % a.ocbs, tile = (item / a.ocbs) % a.tiles, b = item / (a.ocbs * a.tiles);
+    const int chunk0 = split * (a.split_c / C::KC);
+    const int chunk1 = a.ksplit > 1 ? min(a.nchunks, chunk0 + a.split_c / C::KC) : a.nchunks;
     const int tx0 = (tile % a.tiles_x) * C::TW, ty0 = (tile / a.tiles_x) * C::TH;
     const int iy0 = ty0 * C::S - a.ph, ix0 = tx0 * C::S - a.pw;
     // First staged input column (8-aligned for the vector path).
@@ -273,7 +284,7 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
     for (int mt = 0; mt < C::MT; ++mt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            const float bv = a.bias[ocb * C::BM + (mt0 + mt) * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)];
+            const float bv = split == 0 ? a.bias[ocb * C::BM + (mt0 + mt) * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3)] : 0.0f;
 #pragma unroll
             for (int nt = 0; nt < C::NT; ++nt) acc[mt][nt][r] = bv;
         }
@@ -492,13 +503,13 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
     };
 
     if constexpr (C::DB) {
-        fetch(0, 0);
+        fetch(chunk0, 0);
         commit(0);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's LDS DMA has landed
         __syncthreads();
-        for (int chunk = 0; chunk < a.nchunks; ++chunk) {
-            const int cur = chunk & 1;
-            const bool more = chunk + 1 < a.nchunks;
+        for (int chunk = chunk0; chunk < chunk1; ++chunk) {
+            const int cur = (chunk - chunk0) & 1;
+            const bool more = chunk + 1 < chunk1;
             // Stage cur^1 was last read before the previous barrier.
             if (more) fetch(chunk + 1, cur ^ 1);
             compute(cur);
@@ -509,11 +520,11 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
             __syncthreads();
         }
     } else {
-        fetch(0, 0);
+        fetch(chunk0, 0);
         commit(0);
         __syncthreads();
-        for (int chunk = 0; chunk < a.nchunks; ++chunk) {
-            const bool more = chunk + 1 < a.nchunks;
+        for (int chunk = chunk0; chunk < chunk1; ++chunk) {
+            const bool more = chunk + 1 < chunk1;
             if (more) fetch(chunk + 1, 0);
             compute(0);
             __syncthreads();
@@ -533,6 +544,27 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
     // straight from registers: two 4-byte pairs per lane, 32 lanes covering
     // 128 contiguous bytes of a row. Plain outputs go through an LDS
     // [channel][pixel] tile and leave as 16-byte rows.
+    if (a.ksplit > 1) {
+        // Split K: the FP32 partial of this split, in the conv's output
+        // geometry (the reduce kernel rounds, applies the epilogue and the
+        // DEPTH_TO_SPACE store). 32 lanes write 32 consecutive pixels.
+        const size_t ohw = static_cast<size_t>(a.oh) * a.ow;
+        float* const pd = a.part + (static_cast<size_t>(split) * (a.nwg / (a.tiles * a.ocbs)) + b) * a.oc * ohw;
+#pragma unroll
+        for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+            for (int nt = 0; nt < C::NT; ++nt) {
+                const int p = wn * C::WN + nt * 32 + (lane & 31);
+                const int oy = ty0 + (p / C::TW), ox = tx0 + (p % C::TW);
+                if (oy >= a.oh || ox >= a.ow) continue;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) {
+                    const int oc = ocb * C::BM + (mt0 + mt) * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+                    if (oc < a.oc) pd[oc * ohw + static_cast<size_t>(oy) * a.ow + ox] = acc[mt][nt][r];
+                }
+            }
+        return;
+    }
     const bool max_form = a.alpha >= 0.0f && a.alpha <= 1.0f;
     if (a.d2s == 2) {
 #pragma unroll

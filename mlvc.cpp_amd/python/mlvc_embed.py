@@ -19,7 +19,7 @@ process loads with global symbol scope before libmlvc_hip.so (or build.py
 links the two objects into libmlvc_hip.so itself when
 MLVC_EMBED_MODEL_ROOT is set).
 
-  python mlvc_embed.py --model-root ROOT --out-dir DIR [--shared libmodels.so]
+  python mlvc_embed.py --model-root ROOT [--profiles profiles.json] --out-dir DIR [--shared libmodels.so]
   python mlvc_embed.py --bundle PROFILE=DIR [--bundle ...] --out-dir DIR
 """
 
@@ -62,9 +62,12 @@ def find_bundle(model_root: pathlib.Path, profile: str) -> pathlib.Path:
     return found[0].parent
 
 
-def pack(bundles: dict[str, pathlib.Path], out_dir: pathlib.Path, check_dir_name: bool = False) -> list[tuple]:
-    """Writes the payload, assembly and index files for `bundles` (profile -> bundle directory) into
-    out_dir and returns the index entries (profile, path, offset, size)."""
+def pack(bundles: dict[str, pathlib.Path], out_dir: pathlib.Path, check_dir_name: bool = False,
+         model_versions: dict[str, str] | None = None) -> list[tuple]:
+    """Writes the payload, assembly and index files for `bundles` (profile -> bundle directory, in index
+    order) into out_dir and returns the index entries (profile, path, offset, size). With
+    model_versions (profile -> registered model_version), each manifest's model_version must equal
+    its profile's."""
     out_dir = pathlib.Path(out_dir)
     out_dir.mkdir(parents=True, exist_ok=True)
     payload = bytearray()
@@ -76,6 +79,8 @@ def pack(bundles: dict[str, pathlib.Path], out_dir: pathlib.Path, check_dir_name
         info = mlvc_hip.bundle_info(d)
         if info["profile"] != profile:
             raise ValueError(f"bundle profile mismatch: {d} describes {info['profile']!r}, expected {profile!r}")
+        if model_versions is not None and info["model_version"] != model_versions[profile]:
+            raise ValueError(f"bundle model version mismatch for {profile}")
         if check_dir_name and d.name != f"{info['width']}x{info['height']}":
             raise ValueError(f"model bundle directory {d.name!r} does not match manifest dimensions "
                              f"'{info['width']}x{info['height']}'")
@@ -127,26 +132,42 @@ def shared_library(out_dir: pathlib.Path, so_path: pathlib.Path) -> pathlib.Path
     return pathlib.Path(so_path)
 
 
-def pack_model_root(model_root: pathlib.Path, out_dir: pathlib.Path) -> list[tuple]:
-    """Every profile directory below model_root, each holding exactly one <WxH>/ bundle."""
+def load_registry(path: pathlib.Path) -> dict[str, str]:
+    """Profile registry in the shape of the reference's models/profiles/profiles.json
+    ({"profiles": {name: {"model_version": ...}, ...}}): profile -> model_version, in file order."""
+    profiles = json.loads(pathlib.Path(path).read_text())["profiles"]
+    return {name: reg["model_version"] for name, reg in profiles.items()}
+
+
+def pack_model_root(model_root: pathlib.Path, out_dir: pathlib.Path, registry: pathlib.Path | None = None) -> list[tuple]:
+    """Bundles below model_root, each profile directory holding exactly one <WxH>/ bundle. With a
+    profile registry (package.py:249-271): exactly the registered profiles, in registry order, each
+    manifest's model_version checked against its registration; other directories are not embedded.
+    Without one: every profile directory, sorted by name."""
     model_root = pathlib.Path(model_root)
-    profiles = sorted(p.name for p in model_root.iterdir() if p.is_dir())
+    versions = load_registry(registry) if registry is not None else None
+    profiles = list(versions) if versions is not None else sorted(p.name for p in model_root.iterdir() if p.is_dir())
     if not profiles:
         raise FileNotFoundError(f"no model profiles below {model_root}")
-    return pack({p: find_bundle(model_root, p) for p in profiles}, out_dir, check_dir_name=True)
+    return pack({p: find_bundle(model_root, p) for p in profiles}, out_dir, check_dir_name=True,
+                model_versions=versions)
 
 
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--model-root", type=pathlib.Path)
+    ap.add_argument("--profiles", type=pathlib.Path,
+                    help="profile registry (profiles.json shape) selecting and ordering the profiles under --model-root")
     ap.add_argument("--bundle", action="append", default=[], metavar="PROFILE=DIR")
     ap.add_argument("--out-dir", type=pathlib.Path, required=True)
     ap.add_argument("--shared", type=pathlib.Path)
     args = ap.parse_args(argv)
     if bool(args.model_root) == bool(args.bundle):
         ap.error("give either --model-root or --bundle")
+    if args.profiles and not args.model_root:
+        ap.error("--profiles selects profiles under --model-root")
     if args.model_root:
-        index = pack_model_root(args.model_root, args.out_dir)
+        index = pack_model_root(args.model_root, args.out_dir, args.profiles)
     else:
         bundles = {}
         for b in args.bundle:

@@ -14,6 +14,7 @@
 //                        1x1 4C->C of unshuffle2(y1) and shuffle2(3x3 C->4C
 //                        of y1); W,b ~ N(0,0.02)
 //   mlvc_s_640x368       MLVC-S-shaped per-frame graph, 8 frames (below)
+//   mlvc_s_320x192       the same graph at 320x192, 12 frames
 //   mlvc_1920x1088       the same topology widened to 1/16, 32 frames
 //   codec_{enc,dec}_*    the MLVCEncoder / MLVCDecoder pair of the buffered
 //                        codec path (build_codec below)
@@ -557,6 +558,7 @@ const std::vector<ConfigEntry>& registry()
         {"dwblock_tiny", [](GraphBuilder& g, Rng& r, SyntheticModel& i) { build_dwblock(g, r, i, 6, 10, 16); }},
         {"mlvc_s_640x368", [](GraphBuilder& g, Rng& r, SyntheticModel& i) { build_mlvc(g, r, i, 368, 640, 3, 6, 8); }},
         {"mlvc_1920x1088", [](GraphBuilder& g, Rng& r, SyntheticModel& i) { build_mlvc(g, r, i, 1088, 1920, 4, 12, 32); }},
+        {"mlvc_s_320x192", [](GraphBuilder& g, Rng& r, SyntheticModel& i) { build_mlvc(g, r, i, 192, 320, 3, 6, 12); }},
         {"mlvc_s_tiny", [](GraphBuilder& g, Rng& r, SyntheticModel& i) { build_mlvc(g, r, i, 32, 64, 3, 2, 4); }},
         {"mlvc_tiny", [](GraphBuilder& g, Rng& r, SyntheticModel& i) { build_mlvc(g, r, i, 64, 128, 4, 2, 4); }},
         {"codec_enc_1920x1088", [](GraphBuilder& g, Rng& r, SyntheticModel& i) { build_codec(g, r, i, 1088, 1920, 12, 32, true); }},

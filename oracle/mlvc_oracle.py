@@ -449,6 +449,21 @@ class Ops:
         return outs  # y_raw, out
 
 
+def mfma_step(a: np.ndarray, b: np.ndarray, c: np.ndarray) -> np.ndarray:
+    """The isa-2 model of one v_mfma_f32_32x32x16_f16 step per case: a, b
+    [n, 16] raw binary16, c [n] float32 -> [n] float32 = c + sum a*b as the
+    matrix core sums it."""
+    lib = oracle_lib()
+    lib.oracle_mfma_step.argtypes = [C.c_void_p] * 4 + [C.c_size_t]
+    a = np.ascontiguousarray(a, np.uint16)
+    b = np.ascontiguousarray(b, np.uint16)
+    c = np.ascontiguousarray(c, np.float32)
+    out = np.zeros(c.shape, np.float32)
+    if lib.oracle_mfma_step(a.ctypes.data, b.ctypes.data, c.ctypes.data, out.ctypes.data, c.size) != 0:
+        raise OracleError(lib.oracle_last_error().decode())
+    return out
+
+
 def parity_stats(got: np.ndarray, want: np.ndarray) -> dict:
     """max|d|/RMS(want) and mean|d|/RMS(want) over FP16 tensors (raw bits)."""
     g = got.view(np.float16).astype(np.float64)

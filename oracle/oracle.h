@@ -69,6 +69,10 @@ int oracle_depth_to_space_nhwc(const uint16_t* in, uint16_t* out, int n, int c, 
 int oracle_space_to_depth_nhwc(const uint16_t* in, uint16_t* out, int n, int c, int h, int w, int block);
 int oracle_nchw_to_nhwc(const uint16_t* in, uint16_t* out, size_t n, size_t c, size_t hw);
 int oracle_nhwc_to_nchw(const uint16_t* in, uint16_t* out, size_t n, size_t hw, size_t c);
+/* isa-2 model of one v_mfma_f32_32x32x16_f16 step for one output:
+ * out[i] = c[i] + sum_k a[16i+k] * b[16i+k] as the matrix core sums it
+ * (FP16 a, b as raw binary16; FP32 c and out), for count cases. */
+int oracle_mfma_step(const uint16_t* a, const uint16_t* b, const float* c, float* out, size_t count);
 /* Codec I/O: I420 frame (w x h) <-> model image [3, mh, mw] FP16.
  * pad5 = {left, right, top, bottom, rotated}. */
 int oracle_yuv420_to_model(const uint8_t* yuv, int w, int h, int mw, int mh, int rotated, float pixel_range,

@@ -220,9 +220,11 @@ def test_fused_conv_pair(tmp_path, monkeypatch, s2d, ica, h, w, acts, n):
 # 1x1 conv -> SLICE [0,G) / [G,2G) -> CLIP(gate) -> MUL(clipped, linear): one
 # launch with the ReGLU epilogue (the reference's pointwise ReGLU fusion),
 # G-channel output; flattened and ragged pixel counts, two images, G = 32,
-# 64 and 96 (several 64-row blocks, a partial last output-channel block).
+# 64 and 96 (several 64-row blocks, a partial last output-channel block);
+# 640 input channels over few pixels run split K (ranges of 128 channels,
+# the ReGLU applied by the kernel that adds the partials).
 @pytest.mark.parametrize("ic,g,h,w,n,lo,hi", [(64, 32, 16, 24, 1, -1.0, 6.0), (48, 64, 7, 13, 2, 0.0, 4.0),
-                                              (32, 96, 12, 20, 1, -2.0, 2.0)])
+                                              (32, 96, 12, 20, 1, -2.0, 2.0), (640, 96, 6, 10, 2, -1.0, 3.0)])
 def test_conv_reglu_epilogue(tmp_path, monkeypatch, ic, g, h, w, n, lo, hi):
     rng = np.random.default_rng(ic + g + h)
     gr = graphs.Graph()
@@ -243,7 +245,8 @@ def test_conv_reglu_epilogue(tmp_path, monkeypatch, ic, g, h, w, n, lo, hi):
     fused = mlvc_hip.Backend(tmp_path, "hip")
     fused.load("m")
     kinds = [l["kind"] for l in fused.launches()]
-    assert len(kinds) == 1 and kinds[0].endswith("+reglu"), kinds
+    assert len(kinds) == 1 and "+reglu" in kinds[0], kinds
+    assert ("+split" in kinds[0]) == (ic == 640), kinds
     got = fused.run(ins)[0]
     fused.close()
     assert_parity(got, want, f"conv+reglu ic={ic} g={g} {n}x{h}x{w}")

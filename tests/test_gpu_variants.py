@@ -51,6 +51,13 @@ CASES = [
     # width (32 or 64): the last pass is partial.
     ("ragged_ic_ws", 1, 80, 12, 32, 128, 3, 1, 1, dict(epilogue="lrelu")),
     ("ragged_ic_ws_d2s", 2, 48, 8, 16, 256, 3, 1, 1, dict(epilogue="lrelu", d2s=2)),
+    # Split K (deep 1x1 convs over few pixels): 8 splits of an unshuffled
+    # 1x1, five splits with a ragged last one (600 = 4 x 128 + 88 channels)
+    # and a residual over two images, a plane of 77 pixels (the reduce
+    # kernel's one-output-per-thread path) with LeakyReLU.
+    ("split_1x1_s2d", 1, 1024, 6, 16, 256, 1, 1, 0, dict(s2d=2)),
+    ("split_residual_n2", 2, 600, 6, 10, 64, 1, 1, 0, dict(epilogue="residual")),
+    ("split_ragged_plane", 1, 768, 7, 11, 96, 1, 1, 0, dict(epilogue="lrelu")),
 ]
 
 # Geometries the weight-streaming 3x3 kernel (conv_ws.hpp) takes: NCHW inputs
@@ -66,7 +73,7 @@ def test_every_variant(tmp_path, monkeypatch, case):
     rng = np.random.default_rng(5)
     ins = [graphs.half(rng.uniform(-1, 1, sh)) for sh in shapes]
     want = mlvc_oracle.OraclePlan(tmp_path, "m").run(ins)[0]
-    first, ran = None, []
+    first, ran, split = None, [], False
     for v in mlvc_hip.conv_variants()[1:]:
         monkeypatch.setenv("MLVC_HIP_CONV_VARIANT", v)
         gpu = mlvc_hip.Backend(tmp_path, "hip")
@@ -75,6 +82,7 @@ def test_every_variant(tmp_path, monkeypatch, case):
         if not any(kd.startswith(v + "+") or kd == v for kd in kinds):
             gpu.close()
             continue  # not eligible for this geometry
+        split = split or any("+split" in kd for kd in kinds)
         got = gpu.run(ins)[0]
         gpu.close()
         assert_parity(got, want, f"{name} with {v}")
@@ -84,5 +92,9 @@ def test_every_variant(tmp_path, monkeypatch, case):
             assert (got == first[1]).all(), f"{name}: {v} differs from {first[0]}"
         ran.append(v)
     assert len(ran) >= 2, ran
-    if name in WS_CASES:  # the weight-streaming kernel is among them
+    if split:  # split K runs on the conv_mfma variants only
+        assert all(v.startswith("mfma_") for v in ran), ran
+    elif name in WS_CASES:  # the weight-streaming kernel is among them
         assert any(v.startswith("ws_") for v in ran), ran
+    if name.startswith("split_"):
+        assert split, name

@@ -1,11 +1,15 @@
-"""How far FP32 summation order alone moves the recurrent MLVC-shaped graph.
+"""How far the GPU's arithmetic, fed back through the recurrent state, moves
+the MLVC-shaped graph from the reference order.
 
-The GPU convs sum K as (16-channel step, tap), each MFMA step adding a group
-of 16 products to the FP32 accumulator; the reference CPU kernels add one
-product per fused multiply-add in (ky, kx, ic) order. The oracle's isa 2 mode
-models the GPU order (every groups == 1 conv summed that way, everything else
-the reference plan). Comparing it with the reference order on the CPU
-measures the drift that order alone produces, with no GPU involved:
+The oracle's isa 2 mode sums every groups == 1 conv as the GPU's matrix
+cores do (16-channel steps outer, taps inner, each v_mfma_f32_32x32x16_f16
+step's two halves added to the FP32 accumulator with the instruction's own
+truncation and rounding, the GPU's split K; pinned instruction by
+instruction by tests/test_oracle_mfma_model.py, and bit for bit against the
+GPU's convs, fused kernels and frames by tests/test_gpu_order_model.py and
+tests/test_gpu_graphs.py); everything else is the reference plan. Run against
+the reference order on the CPU, it measures the difference the GPU shows,
+with no GPU involved:
 
 * teacher-forced (both fed the same state every frame), the per-frame
   difference is flat and within the FP16 parity bar;
@@ -13,16 +17,10 @@ measures the drift that order alone produces, with no GPU involved:
   frames as each side feeds its own roundings back through the state, then
   levels off.
 
-Measured with this model on 8 CPU threads: at 640x368 the free-running recon
-mean |d|/RMS reaches 9.2e-4 by frame 10 of 12 against a flat 5.2e-4
-teacher-forced; at 1920x1088 over 32 frames it levels at 1.33e-3-1.34e-3
-from frame ~12 (max |d|/RMS 1.06e-2) against a flat 6.8e-4 / 4.0e-4 (recon /
-state) teacher-forced, the numbers the GPU shows on that graph frame for
-frame (frame 2: 1.06e-3 both).
-The GPU's free-running bound in test_gpu_graphs.py is derived from those
-1920x1088 figures. By default this file runs 12 frames of the 640x368 graph;
-MLVC_DRIFT_CONFIG=mlvc_1920x1088 MLVC_DRIFT_FRAMES=32 reproduces the
-1920x1088 figures (about a minute per frame on 8 cores).
+By default this file runs the 12 frames of the 320x192 graph;
+MLVC_DRIFT_CONFIG / MLVC_DRIFT_FRAMES select another (mlvc_1920x1088 over 32
+frames takes about two minutes per frame on 8 cores; its free-running curve
+is recorded in tests/golden/mlvc_1920x1088_isa2.json).
 """
 
 import os
@@ -33,7 +31,7 @@ import pytest
 import mlvc_hip
 import mlvc_oracle as O
 
-CONFIG = os.environ.get("MLVC_DRIFT_CONFIG", "mlvc_s_640x368")
+CONFIG = os.environ.get("MLVC_DRIFT_CONFIG", "mlvc_s_320x192")
 FRAMES = int(os.environ.get("MLVC_DRIFT_FRAMES", "12"))
 
 
