@@ -148,6 +148,18 @@ size_t mlvc_hip_conv_bias_len(const mlvc_hip_conv_desc* desc);
  * kernels_scalar.cpp:14-56, and mlvc_oihw_to_krsc_fp16, layout.cu). */
 int mlvc_hip_conv_pack(const mlvc_hip_conv_desc* desc, const uint16_t* w_oihw, void* dst_host);
 int mlvc_hip_conv_launch(const mlvc_hip_conv_desc* desc, mlvc_hip_stream s);
+/* mlvc_hip_conv_launch without a caller workspace, allocating nothing: a
+ * split-K conv keeps its FP32 partials in a static device array of the
+ * library (32 MiB, one per GPU, held until the process ends) instead of
+ * desc->workspace, which is ignored. Every split mlvc_hip_conv_plan chooses
+ * fits (its partials are at most 512 x 128 x 128 FP32 values); a larger one
+ * set by hand fails with an error before anything is launched. Each call
+ * overwrites every partial it reads, so nothing needs clearing between
+ * calls; calls that overlap on one GPU (on different streams) share the
+ * array and race. No counterpart in the reference: for callers that cannot
+ * allocate device memory (code under graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). */
+int mlvc_hip_conv_launch_noalloc(const mlvc_hip_conv_desc* desc, mlvc_hip_stream s);
 
 /* ---- depthwise KxK (groups == C == OC) ----
  * Replaces mlvc_depthwise_conv_fp16{,_pair,_quad} (depthwise_conv.cu:1-173);

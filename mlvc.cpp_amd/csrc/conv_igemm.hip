@@ -6,6 +6,8 @@
 #include "conv_kernel.hpp"
 
 #include <algorithm>
+#include <map>
+#include <mutex>
 #include <vector>
 
 namespace mlvc_hip {
@@ -444,6 +446,39 @@ void launch_conv(const mlvc_hip_conv_desc& d, void* s)
     }
 }
 
+// Scratch of the no-allocation launch: the FP32 partials of a split-K conv.
+// Every split the planner chooses fits: ksplit * items <= 512 and an item
+// covers at most 128 x 128 outputs, so the partials take at most
+// 512 * 128 * 128 * 4 bytes.
+constexpr size_t kScratchBytes = size_t{512} * 128 * 128 * sizeof(float);
+
+}  // namespace
+}  // namespace mlvc_hip
+
+// One copy per device, held until the process ends.
+static __device__ __align__(256) float scratch[mlvc_hip::kScratchBytes / sizeof(float)];
+
+namespace mlvc_hip {
+namespace {
+
+// Device address of `scratch` on the current device, looked up on the first
+// call per device (the array's name is a host-side stand-in that must not
+// reach a kernel).
+void* scratch_ptr()
+{
+    int dev = 0;
+    check(hipGetDevice(&dev), "current device");
+    static std::mutex mutex;
+    static std::map<int, void*> ptrs;
+    std::lock_guard<std::mutex> lock(mutex);
+    if (const auto it = ptrs.find(dev); it != ptrs.end()) return it->second;
+    void* p = nullptr;
+    check(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "no-allocation scratch address");
+    if (!p) throw std::runtime_error("conv: no-allocation scratch has no device address");
+    ptrs.emplace(dev, p);
+    return p;
+}
+
 }  // namespace
 }  // namespace mlvc_hip
 
@@ -454,6 +489,26 @@ int mlvc_hip_conv_launch(const mlvc_hip_conv_desc* desc, mlvc_hip_stream s)
     return guard([&] {
         if (!desc) throw std::runtime_error("conv: null descriptor");
         launch_conv(*desc, s);
+    });
+}
+
+int mlvc_hip_conv_launch_noalloc(const mlvc_hip_conv_desc* desc, mlvc_hip_stream s)
+{
+    return guard([&] {
+        if (!desc) throw std::runtime_error("conv: null descriptor");
+        mlvc_hip_conv_desc d = *desc;
+        d.workspace = nullptr;
+        d.workspace_bytes = 0;
+        if (d.ksplit > 1) {
+            const size_t need = mlvc_hip_conv_workspace_bytes(&d);
+            if (need > kScratchBytes)
+                throw std::runtime_error("conv: split K needs " + std::to_string(need) +
+                                         " bytes of partials; the no-allocation launch holds " +
+                                         std::to_string(kScratchBytes));
+            d.workspace = scratch_ptr();
+            d.workspace_bytes = kScratchBytes;
+        }
+        launch_conv(d, s);
     });
 }
 
