@@ -195,3 +195,28 @@ def test_backend_loads_from_the_image(image):
         out["shape"] = list(res[0].shape)
     """)
     assert out["same"], out
+
+
+def test_profile_registry_selects_orders_and_checks_versions(tmp_path):
+    """With a profile registry (the reference's models/profiles/profiles.json
+    shape), exactly the registered profiles are embedded, in registry order,
+    each manifest's model_version checked (package.py:249-271)."""
+    root, dirs = _root_with(tmp_path, ["codec_enc_tiny", "mlvc_s_tiny", "dwblock_tiny"])
+    names = sorted(dirs)
+    versions = {p: mlvc_hip.bundle_info(d)["model_version"] for p, d in dirs.items()}
+    chosen = [names[2], names[0]]  # reverse of name order; names[1] left out
+    reg = tmp_path / "profiles.json"
+    reg.write_text(json.dumps({"schema_version": 1, "profiles": {p: {"model_version": versions[p]} for p in chosen}}))
+    index = mlvc_embed.pack_model_root(root, tmp_path / "out", reg)
+    order = list(dict.fromkeys(p for p, *_ in index))
+    assert order == chosen
+    # Without a registry every profile directory is embedded, sorted by name.
+    assert list(dict.fromkeys(p for p, *_ in mlvc_embed.pack_model_root(root, tmp_path / "all"))) == names
+    bad = {"profiles": {chosen[0]: {"model_version": versions[chosen[0]] + "-other"}}}
+    reg.write_text(json.dumps(bad))
+    with pytest.raises(ValueError, match=f"bundle model version mismatch for {chosen[0]}"):
+        mlvc_embed.pack_model_root(root, tmp_path / "out2", reg)
+    # A registered profile without a bundle below the root.
+    reg.write_text(json.dumps({"profiles": {"missing-profile": {"model_version": "v"}}}))
+    with pytest.raises(FileNotFoundError, match="missing-profile"):
+        mlvc_embed.pack_model_root(root, tmp_path / "out3", reg)

@@ -106,11 +106,12 @@ def test_fused_concat_load(tmp_path, k, pad):
 # 3x3 s1 p1 with rows of a multiple of 8 pixels runs the 16-byte row kernel:
 # 256x46x80 and 128x92x160 (the residual-block shapes), 8x1x8 (one row, every
 # tap at a border), 24x7x16 (two segments a row).
-@pytest.mark.parametrize("c,h,w,k,s,p", [(16, 13, 17, 3, 1, 1), (256, 46, 80, 3, 1, 1), (12, 9, 10, 3, 1, 1),
-                                         (64, 15, 21, 3, 2, 1), (32, 11, 11, 5, 1, 2), (128, 92, 160, 3, 1, 1),
-                                         (8, 1, 8, 3, 1, 1), (24, 7, 16, 3, 1, 1)])
-def test_depthwise(tmp_path, c, h, w, k, s, p):
-    shapes = graphs.single_conv_graph(tmp_path, "m", 1, c, h, w, c, k, s, p, groups=c, seed=c)
+# Two images (n = 2) cover the row kernel's plane -> channel mapping.
+@pytest.mark.parametrize("n,c,h,w,k,s,p", [(1, 16, 13, 17, 3, 1, 1), (1, 256, 46, 80, 3, 1, 1), (1, 12, 9, 10, 3, 1, 1),
+                                           (1, 64, 15, 21, 3, 2, 1), (1, 32, 11, 11, 5, 1, 2), (1, 128, 92, 160, 3, 1, 1),
+                                           (1, 8, 1, 8, 3, 1, 1), (1, 24, 7, 16, 3, 1, 1), (2, 16, 9, 24, 3, 1, 1)])
+def test_depthwise(tmp_path, n, c, h, w, k, s, p):
+    shapes = graphs.single_conv_graph(tmp_path, "m", n, c, h, w, c, k, s, p, groups=c, seed=c)
     got, want, launches = run_both(tmp_path, "m", shapes)
     assert launches[0]["kind"] == "depthwise"
     st = assert_parity(got[0], want[0], "depthwise")
