@@ -62,6 +62,14 @@ const Variant kTable[] = {
     MLVC_VARIANT_WSP(128, 4, 32, 32, 2, 9),
     MLVC_VARIANT_WSP(128, 4, 48, 32, 2, 9),
     MLVC_VARIANT_WSP(128, 4, 24, 32, 2, 9),
+    // 64 output channels on two waves, more workgroups per CU.
+    MLVC_VARIANT_WSW(64, 2, 32, 64, 4, 2, 9),
+    MLVC_VARIANT_WSW(64, 4, 32, 64, 3, 2, 9),
+    MLVC_VARIANT_WSW(64, 8, 32, 64, 2, 2, 9),
+    // Short, narrow tiles: enough workgroups for deep convs over few pixels
+    // (46x80 and 92x160 planes).
+    MLVC_VARIANT_WSW(64, 2, 16, 64, 4, 2, 9),
+    MLVC_VARIANT_WSR(128, 2, 16, 64, 2, 9),
 };
 }  // namespace
 

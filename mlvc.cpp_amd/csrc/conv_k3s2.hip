@@ -35,6 +35,9 @@ const Variant kTable[] = {
     MLVC_VARIANT_WS2R(256, 2, 32, 64, 2, 8, 9),
     MLVC_VARIANT_WS2R(192, 2, 32, 64, 2, 6, 9),
     MLVC_VARIANT_WS2R(128, 4, 24, 32, 2, 4, 9),
+    // Short, narrow tiles for deep convs onto few pixels (46x80 outputs).
+    MLVC_VARIANT_WS2R(64, 2, 16, 64, 4, 2, 9),
+    MLVC_VARIANT_WS2R(128, 2, 16, 64, 2, 4, 9),
 };
 }  // namespace
 

@@ -374,6 +374,11 @@ void launch_ws(const ConvArgs& a, dim3 grid, hipStream_t s)
 #define MLVC_VARIANT_WSP(BM, TH, TW, SC, OCC, RING)                                                            \
     Variant{"ws_bm" #BM "_" #TH "x" #TW "_k3x3_s1_sc" #SC "_occ" #OCC "_r" #RING "_pipe", BM, TH, TW, 3, 3, 1, 16,     \
             nullptr, &launch_ws<WsCfg<BM, TH, TW, SC, OCC, 1, 4, RING, true>>, nullptr, SC}
+// Stride 1 with WAVES waves (BM = 64 over two waves: 64-channel convs
+// without padded output rows).
+#define MLVC_VARIANT_WSW(BM, TH, TW, SC, OCC, WAVES, RING)                                                     \
+    Variant{"ws_bm" #BM "_" #TH "x" #TW "_k3x3_s1_sc" #SC "_occ" #OCC "_w" #WAVES "_r" #RING, BM, TH, TW, 3, 3, 1, 16, \
+            nullptr, &launch_ws<WsCfg<BM, TH, TW, SC, OCC, 1, WAVES, RING>>, nullptr, SC}
 // Stride 2 with a ring RING k-steps deep.
 #define MLVC_VARIANT_WS2R(BM, TH, TW, SC, OCC, WAVES, RING)                                                    \
     Variant{"ws_bm" #BM "_" #TH "x" #TW "_k3x3_s2_sc" #SC "_occ" #OCC "_w" #WAVES "_r" #RING, BM, TH, TW, 3, 3, 2, 16, \
