@@ -73,8 +73,9 @@ def plan(ic, h, w, oc, k=3, stride=1, pad=1, n=1, epilogue=1):
 # mlvc_hip_conv_plan on deep 1x1 convs over few pixels, and on shallow,
 # wide or 3x3 ones (never split).
 SPLITS = [
-    (1024, 46, 80, 256, 1, 1, 8, 128),     # unshuffled 1x1 4C->C at 46x80, C=256: 58 items
-    (512, 92, 160, 128, 1, 1, 1, 512),     # the same at 92x160, C=128: K = 512 < 576
+    (1024, 23, 40, 256, 1, 1, 8, 128),     # unshuffled 1x1 4C->C at 23x40, C=256: 16 items
+    (1024, 46, 80, 256, 1, 1, 8, 128),     # the same over 4x the pixels: 58 items
+    (512, 46, 80, 128, 1, 1, 1, 512),      # the C=128 workload's, at 46x80: K = 512 < 576
     (576, 46, 80, 128, 1, 1, 5, 128),      # s = min(8, 17, 9) = 8, ranges of 128: 4 + a last 64
     (640, 6, 10, 192, 1, 1, 5, 128),       # s = min(8, 512, 10) = 8: 64 * ceil(640 / 512) = 128
     (1024, 184, 320, 256, 1, 1, 1, 1024),  # 920 items

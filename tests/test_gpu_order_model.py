@@ -67,8 +67,9 @@ CONVS = [
     ("concat_1x1_128_64", 1, 128, 34, 64, 64, 1, 1, 0, dict(concat_ic=64, epilogue="lrelu")),
     ("1x1_256_512", 1, 256, 46, 80, 512, 1, 1, 0, dict(epilogue="lrelu")),
     ("1x1_512_256_residual", 1, 512, 46, 80, 256, 1, 1, 0, dict(epilogue="residual")),
-    # Split K: the residual-block workload's unshuffle(2) -> 1x1 1024->256 at
-    # 46x80 (8 ranges of 128 channels) and a ragged split with a residual.
+    # Split K: an unshuffle(2) -> 1x1 1024->256 (the residual-block
+    # workload's at 23x40, here over 46x80; 8 ranges of 128 channels) and a
+    # ragged split with a residual.
     ("s2d_1x1_1024_256_split", 1, 1024, 46, 80, 256, 1, 1, 0, dict(s2d=2)),
     ("1x1_600_64_split_residual", 2, 600, 6, 10, 64, 1, 1, 0, dict(epilogue="residual")),
 ]
