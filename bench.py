@@ -397,6 +397,153 @@ def realops(reps: int, frames: int) -> dict:
             "frames_per_s": frames / (ms * 1e-3), "kernels_per_frame": n_launch, "kernels": kernels}
 
 
+def ops_kernels(reps: int) -> dict:
+    """The real-model operator kernels of realops_544x960 launched straight
+    through the device C ABI, without the graph, the backend or a hipGraph
+    (so a profiler sees plain kernel dispatches): ReGLU 128->64, ADD, MUL by a
+    [1,32,1,1] row, channel SLICE and both feature-update forms at 544x960;
+    the y0 / y1 quantisation tails at Q=96, 272x480. Random FP16 operands in
+    each kernel's working range; HIP events around `reps` back-to-back
+    launches after 3 warm-up launches. Algorithmic bytes: every operand read
+    and every result written once."""
+    import ctypes as C
+
+    import numpy as np
+
+    import mlvc_hip
+
+    L = mlvc_hip.device_lib()
+    vp, ci, sz, i64p = C.c_void_p, C.c_int, C.c_size_t, C.POINTER(C.c_int64)
+    L.mlvc_hip_malloc.argtypes = [C.POINTER(vp), sz]
+    L.mlvc_hip_free.argtypes = [vp]
+    L.mlvc_hip_memcpy_h2d.argtypes = [vp, vp, sz, vp]
+    L.mlvc_hip_stream_create.argtypes = [C.POINTER(vp)]
+    L.mlvc_hip_stream_destroy.argtypes = [vp]
+    L.mlvc_hip_stream_synchronize.argtypes = [vp]
+    L.mlvc_hip_event_create.argtypes = [C.POINTER(vp)]
+    L.mlvc_hip_event_destroy.argtypes = [vp]
+    L.mlvc_hip_event_record.argtypes = [vp, vp]
+    L.mlvc_hip_event_synchronize.argtypes = [vp]
+    L.mlvc_hip_event_elapsed_ms.argtypes = [vp, vp, C.POINTER(C.c_float)]
+    L.mlvc_hip_binary.argtypes = [vp, i64p, vp, i64p, vp, i64p, ci, vp]
+    L.mlvc_hip_slice.argtypes = [vp, i64p, vp, i64p, i64p, i64p, vp]
+    L.mlvc_hip_reglu.argtypes = [vp, vp, ci, ci, sz, C.c_float, C.c_float, vp]
+    L.mlvc_hip_prepare_tables.argtypes = [vp]
+    L.mlvc_hip_feature_update.argtypes = [vp] * 6 + [ci, ci, sz, vp]
+    L.mlvc_hip_y0_tail.argtypes = [vp, vp]
+    L.mlvc_hip_y1_tail.argtypes = [vp, vp]
+
+    class Y0(C.Structure):
+        _fields_ = [(f, vp) for f in ("latent", "prior", "quant_scale", "update_scale0", "update_scale1", "normalized",
+                                      "clipped", "y_raw", "concat2", "concat3")] + \
+                   [("n", ci), ("q", ci), ("hw", sz), ("clip_min", C.c_float)]
+
+    class Y1(C.Structure):
+        _fields_ = [(f, vp) for f in ("normalized", "prior", "quant_scale", "update_scale0", "update_scale1", "concat2",
+                                      "clipped", "y_raw", "out")] + [("n", ci), ("q", ci), ("hw", sz)]
+
+    def ok(rc):
+        if rc != 0:
+            raise mlvc_hip.MlvcError(L.mlvc_hip_last_error().decode())
+
+    bufs = []
+
+    def alloc(elems):
+        p = vp()
+        ok(L.mlvc_hip_malloc(C.byref(p), max(2 * elems, 16)))
+        bufs.append(p)
+        return p
+
+    rng = np.random.default_rng(5)
+
+    def put(c, hw, lo=-2.0, hi=2.0):
+        a = rng.uniform(lo, hi, c * hw).astype(np.float16).view(np.uint16)
+        p = alloc(a.size)
+        ok(L.mlvc_hip_memcpy_h2d(p, a.ctypes.data, a.nbytes, None))
+        return p
+
+    def dims(*d):
+        return (C.c_int64 * 4)(*d)
+
+    h, w, ch, q = 544, 960, 64, 96
+    hw, hw2 = h * w, (h // 2) * (w // 2)
+    s, e0, e1 = vp(), vp(), vp()
+    ok(L.mlvc_hip_stream_create(C.byref(s)))
+    ok(L.mlvc_hip_event_create(C.byref(e0)))
+    ok(L.mlvc_hip_event_create(C.byref(e1)))
+    rows = []
+    try:
+        ok(L.mlvc_hip_prepare_tables(s))
+        cases = []
+        # ReGLU of the graph's 1x1 conv output: [1,128,hw] -> [1,64,hw].
+        x, y = put(2 * ch, hw, -3, 8), alloc(ch * hw)
+        cases.append(("reglu_c128_544x960", "reglu", 3 * ch * hw * 2,
+                      lambda x=x, y=y: ok(L.mlvc_hip_reglu(x, y, 1, ch, hw, -1.0, 6.0, s))))
+        # The FFN residual ADD and the q-row MUL on 32 channels.
+        a, b, y = put(32, hw), put(32, hw), alloc(32 * hw)
+        dd = dims(1, 32, h, w)
+        cases.append(("add_c32_544x960", "binary", 3 * 32 * hw * 2,
+                      lambda a=a, b=b, y=y, dd=dd: ok(L.mlvc_hip_binary(a, dd, b, dd, y, dd, 0, s))))
+        row, dr = put(32, 1, 0.5, 1.5), dims(1, 32, 1, 1)
+        cases.append(("mul_row_c32_544x960", "binary", 2 * 32 * hw * 2 + 32 * 2,
+                      lambda a=a, row=row, y=y, dd=dd, dr=dr: ok(L.mlvc_hip_binary(a, dd, row, dr, y, dd, 2, s))))
+        # Channels 0..31 of the 64-channel state.
+        st = put(ch, hw)
+        dx, dy, st0, st1 = dims(1, ch, h, w), dims(1, ch // 2, h, w), dims(0, 0, 0, 0), dims(1, 1, 1, 1)
+        cases.append(("slice_c64_to_32_544x960", "slice", 2 * (ch // 2) * hw * 2,
+                      lambda st=st, y=y: ok(L.mlvc_hip_slice(st, dx, y, dy, st0, st1, s))))
+        # Feature update: x [1,3C,hw], history [1,C,hw], scale [C] ->
+        # feature [1,2C,hw] (C = 64), and the deferred form with scaled and
+        # blended also written (C = 32).
+        fx, fh, fs, ff = put(3 * ch, hw, -6, 6), put(ch, hw), put(ch, 1, 0.5, 1.5), alloc(2 * ch * hw)
+        cases.append(("feature_update_c64_544x960", "feature_update", (3 * ch + ch + 2 * ch) * hw * 2 + ch * 2,
+                      lambda: ok(L.mlvc_hip_feature_update(fx, fh, fs, ff, None, None, 1, ch, hw, s))))
+        c2 = ch // 2
+        gx, gh, gs = put(3 * c2, hw, -6, 6), put(c2, hw), put(c2, 1, 0.5, 1.5)
+        gf, gsc, gbl = alloc(2 * c2 * hw), alloc(c2 * hw), alloc(c2 * hw)
+        cases.append(("feature_update_outputs_c32_544x960", "feature_update_outputs",
+                      (3 * c2 + c2 + 4 * c2) * hw * 2 + c2 * 2,
+                      lambda: ok(L.mlvc_hip_feature_update(gx, gh, gs, gf, gsc, gbl, 1, c2, hw, s))))
+        # Quantisation tails at half resolution, Q = 96.
+        y0 = Y0(put(2 * q, hw2, -20, 20).value,
+                put(4 * q, hw2, -0.5, 3).value, put(2 * q, hw2, 0.5, 2).value, put(q, hw2, 0.5, 1.5).value,
+                put(q, hw2, 0.5, 1.5).value, alloc(2 * q * hw2).value, alloc(2 * q * hw2).value,
+                alloc(q * hw2).value, alloc(2 * q * hw2).value, alloc(6 * q * hw2).value, 1, q, hw2, 0.11)
+        cases.append(("y0_tail_q96_272x480", "y0_tail", 23 * q * hw2 * 2,
+                      lambda: ok(L.mlvc_hip_y0_tail(C.byref(y0), s))))
+        y1 = Y1(y0.normalized, put(2 * q, hw2, -4, 4).value, y0.quant_scale, y0.update_scale0, y0.update_scale1,
+                y0.concat2, y0.clipped, alloc(q * hw2).value, alloc(2 * q * hw2).value, 1, q, hw2)
+        cases.append(("y1_tail_q96_272x480", "y1_tail", 15 * q * hw2 * 2,
+                      lambda: ok(L.mlvc_hip_y1_tail(C.byref(y1), s))))
+        ok(L.mlvc_hip_stream_synchronize(None))
+        for name, kind, nbytes, launch in cases:
+            for _ in range(3):
+                launch()
+            ok(L.mlvc_hip_event_record(e0, s))
+            for _ in range(reps):
+                launch()
+            ok(L.mlvc_hip_event_record(e1, s))
+            ok(L.mlvc_hip_event_synchronize(e1))
+            ms = C.c_float()
+            ok(L.mlvc_hip_event_elapsed_ms(e0, e1, C.byref(ms)))
+            us = ms.value * 1e3 / reps
+            rows.append({"name": name, "kind": kind, "us": us, "algorithmic_bytes": nbytes,
+                         "gbs": nbytes / us / 1e3, "hbm_frac": nbytes / us / 1e3 / PEAK_HBM_GBS})
+            log(f"ops {name:36} {nbytes / 1e6:8.2f} MB {us:8.2f} us {nbytes / us / 1e3:7.0f} GB/s "
+                f"{nbytes / us / 1e3 / PEAK_HBM_GBS:.3f} ({reps + 3} launches)")
+    finally:
+        ok(L.mlvc_hip_stream_synchronize(s))
+        for p in bufs:
+            L.mlvc_hip_free(p)
+        L.mlvc_hip_event_destroy(e0)
+        L.mlvc_hip_event_destroy(e1)
+        L.mlvc_hip_stream_destroy(s)
+    return {"workload": "realops_544x960's operator kernels through the device C ABI (no graph): ReGLU, ADD, "
+                        "row MUL, SLICE, feature update (C=64, and C=32 with 3 outputs) at 544x960; y0/y1 tails "
+                        "(Q=96) at 272x480",
+            "kernels": rows}
+
+
 # The smaller workloads, each timed launch by launch beside its summed
 # per-kernel roofline time (min over MFMA and HBM peaks of each launch's
 # algorithmic FLOPs and bytes): (label, synthetic graph, what it is).
@@ -644,6 +791,9 @@ def main() -> int:
     ap.add_argument("--codec-only", action="store_true",
                     help="run only the codec I/O conversion kernels (after the calibration stream kernel, for "
                          "rocprofv3 kernel traces and counter passes); no JSON line")
+    ap.add_argument("--ops-only", action="store_true",
+                    help="run only the real-model operator kernels through the device C ABI, no graph (after the "
+                         "calibration stream kernel, for rocprofv3 kernel traces and counter passes); no JSON line")
     ap.add_argument("--cold-frames", type=int, default=50,
                     help="frames timed with L2 and MALL flushed before each (0: skip)")
     ap.add_argument("--api-frames", type=int, default=30,
@@ -676,6 +826,10 @@ def main() -> int:
         return 0
     if args.small_configs_only:
         small_configs(args.kernel_reps, args.launch_cold_reps, args.small_frames)
+        return 0
+    if args.ops_only:
+        calibration_stream()
+        ops_kernels(args.kernel_reps)
         return 0
     if args.codec_only:
         calibration_stream()
