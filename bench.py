@@ -715,13 +715,21 @@ def measured_traffic(path, launch_names, kind):
     return None
 
 
+def base_kind(kind: str) -> str:
+    """A launch's kernel variant without the activation-layout tags of chained
+    fused blocks (+nhwc_in, +nhwc_out: the same kernel and work, its input or
+    output handed over channel-last)."""
+    return kind.replace("+nhwc_in", "").replace("+nhwc_out", "")
+
+
 def group_launches(rows):
-    """Launches of one kernel variant on one shape (same kind, FLOPs and
-    bytes) merged: mean time per launch, number of launches and their summed
-    time, largest summed time first."""
+    """Launches of one kernel variant on one shape (same kind up to layout
+    tags, FLOPs and bytes) merged: mean time per launch, number of launches
+    and their summed time, largest summed time first."""
     groups = {}
     for r in rows:
-        g = groups.setdefault((r["kind"], r["flops"], r["bytes"]), dict(r, launches=0, total_ms=0.0, names=[]))
+        key = (base_kind(r["kind"]), r["flops"], r["bytes"])
+        g = groups.setdefault(key, dict(r, kind=key[0], launches=0, total_ms=0.0, names=[]))
         g["launches"] += 1
         g["total_ms"] += r["ms"]
         g["names"].append(r["name"])

@@ -176,7 +176,7 @@ int mlvc_hip_depthwise(const void* x, const uint16_t* w, const float* bias, void
  * the 1x1 expand with LeakyReLU epilogue and the 1x1 project with residual
  * epilogue (pointwise_conv.cu / cutlass.cu EVT epilogues) that the
  * reference runs as three launches; rounding points are unchanged.
- * x, y: [n, c, h, w]; dw_w: [c, 1, 3, 3] fp16 (stride 1, pad 1);
+ * x, y: [n, c, h, w] (or channel-last, below); dw_w: [c, 1, 3, 3] fp16 (stride 1, pad 1);
  * w1: W1 [e, c] packed by mlvc_hip_dwblock_pack; w2: W2 [c, e] packed.
  * x, y and dw_w must be 16-byte aligned. */
 typedef struct mlvc_hip_dwblock_desc {
@@ -190,6 +190,12 @@ typedef struct mlvc_hip_dwblock_desc {
     const void* w2;
     const float* b2;
     float alpha;
+    /* Layouts of x and y: 0 = NCHW, 1 = channel-last [n, h, w, c]. The
+     * backend sets them for a block whose output feeds only the next block
+     * (no counterpart in the reference, whose tensors are NCHW at every
+     * node boundary; here the handover between chained blocks is internal).
+     * x and y must not alias. */
+    int in_nhwc, out_nhwc;
 } mlvc_hip_dwblock_desc;
 
 /* 1 when (c, e, h, w) has a fused-block kernel, else 0. */

@@ -55,6 +55,15 @@ bool fusion_enabled()
     return !(env && env[0] == '1' && env[1] == '\0');
 }
 
+// MLVC_HIP_BLOCK_HANDOVER=nchw keeps the activations between chained fused
+// blocks NCHW (default: channel-last); for comparing the two layouts, which
+// give identical results.
+bool block_handover_nhwc()
+{
+    const char* env = std::getenv("MLVC_HIP_BLOCK_HANDOVER");
+    return !(env && std::string(env) == "nchw");
+}
+
 // MLVC_HIP_CONV_VARIANT=<variant name> runs every conv that variant can
 // run with it, untuned (tests sweep the variants this way).
 std::string forced_conv_variant()
@@ -1351,6 +1360,22 @@ private:
             if (L->name.empty()) L->name = desc(L->y).name;
             launches_.push_back(std::move(L));
         }
+        // Chained fused blocks hand over channel-last: a block output whose
+        // only readers are the next block's depthwise conv and residual ADD
+        // (its two consumers) never leaves that pair of launches, so its
+        // layout is theirs to choose.
+        for (auto& P : launches_) {
+            if (!block_handover_nhwc()) break;
+            if (P->kind != Launch::kDwBlock || outputs.count(P->y) || consumers[P->y] != 2) continue;
+            for (auto& Q : launches_)
+                if (Q->kind == Launch::kDwBlock && Q->x == P->y) {
+                    P->blk.out_nhwc = 1;
+                    Q->blk.in_nhwc = 1;
+                }
+        }
+        for (auto& P : launches_)
+            if (P->kind == Launch::kDwBlock)
+                P->kind_name += std::string(P->blk.in_nhwc ? "+nhwc_in" : "") + (P->blk.out_nhwc ? "+nhwc_out" : "");
     }
 
     void require_fp16_activation(TensorId id) const

@@ -32,9 +32,17 @@
 //     select), with the product rounded to FP32 first;
 //   * the project result is rounded into LDS as [channel][pixel] and leaves
 //     as 16-byte rows with the residual added from the staged tile.
-// LDS: x[channel][6 rows][24 columns] (+8 halves per channel),
-// d[pixel][C + 8] (later reused as y[channel][pixel]) and e[pixel][E + 8].
-// Requires W % 8 == 0 (16-byte rows).
+// Chained blocks hand their activations over channel-last: a block whose
+// output feeds only the next block writes it [n][h][w][C] (OUT_NHWC), and
+// that block stages it (IN_NHWC) as 16-byte pieces of 8 channels of one
+// pixel. Its halo is then the 6 x 10 pixels it needs (60 x C x 2 bytes,
+// 240 cache lines at C = 256) instead of 6 rows x 24 columns of every
+// channel (74 KB, about 2.2k cache lines). Arithmetic and rounding are the
+// same in every layout.
+// LDS: x[channel][6 rows][24 columns] (+8 halves per channel) or, channel-
+// last, x[6 rows][10 pixels][C + 8]; d[pixel][C + 8] (later reused as
+// y[channel][pixel], or y[pixel][C + 8] for a channel-last output) and
+// e[pixel][E + 8]. Requires W % 8 == 0 (16-byte rows).
 
 #include "common.hpp"
 #include "mlvc_hip_device.h"
@@ -61,6 +69,7 @@ constexpr int kRing = MLVC_DW_RING;               // weight fragments in flight 
 // 11.8-13.0 us per block).
 constexpr int kEarly = MLVC_DW_EARLY;
 constexpr int kXR = kTH + 2, kXW = kTW + 16;      // staged input rows and columns (x0 - 8 .. x0 + kTW + 7)
+constexpr int kXP = kTW + 2;                      // channel-last staging: pixels x0 - 1 .. x0 + kTW per row
 // Halves per staged channel: 304 bytes, 76 dwords, so 16 lanes reading 16
 // bytes at the same offset of 16 consecutive channels hit distinct banks.
 constexpr int kXCS = kXR * kXW + 8;
@@ -78,6 +87,9 @@ struct BlockCfg {
     static constexpr int ORT = kTH / TPC;                             // depthwise output rows per thread
     static constexpr int RV = C * kTH / T;                            // output rows (16 B) per thread
     static constexpr int DST = C + 8, EST = E + 8;
+    static constexpr int XPS = C + 8;                                 // channel-last staging: halves per pixel
+    static constexpr int XN_PIECES = kXR * kXP * 4;                   // its 16-byte pieces per wave (32 channels)
+    static constexpr int XNU = (XN_PIECES + 63) / 64;                 // per lane
     static constexpr int DS_HALVES = kP * DST > C * kYS ? kP * DST : C * kYS;
     static constexpr int XUNITS = C * kXR * (kXW / 8);                // 16-byte pieces of the staged tile
     static constexpr int XU = (XUNITS + T - 1) / T;                   // per thread
@@ -115,15 +127,17 @@ __device__ __forceinline__ void lds_barrier()
 __device__ __forceinline__ float lo_h(std::uint32_t v) { return h2f(static_cast<std::uint16_t>(v & 0xFFFFu)); }
 __device__ __forceinline__ float hi_h(std::uint32_t v) { return h2f(static_cast<std::uint16_t>(v >> 16)); }
 
-template <int C, int E, int MODE>
+template <int C, int E, int MODE, bool IN_NHWC, bool OUT_NHWC>
 __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArgs a)
 {
     using B = BlockCfg<C, E>;
     constexpr int DST = B::DST, EST = B::EST, MT1 = B::MT1, MT2 = B::MT2, KS1 = B::KS1, KS2 = B::KS2;
-    constexpr int NF1 = B::NF1, NF = B::NF, ORT = B::ORT, RV = B::RV, T = B::T;
+    constexpr int NF1 = B::NF1, NF = B::NF, ORT = B::ORT, RV = B::RV, T = B::T, XPS = B::XPS;
+    constexpr int XS_HALVES = IN_NHWC ? kXR * kXP * XPS : C * kXCS;
     __shared__ __attribute__((aligned(16))) std::uint16_t es[kP * EST];
     __shared__ __attribute__((aligned(16))) std::uint16_t dys[B::DS_HALVES];
-    __shared__ __attribute__((aligned(16))) std::uint16_t xs[C * kXCS];  // x[channel][row][column]
+    // x[channel][row][column], or channel-last x[row][pixel][channel]
+    __shared__ __attribute__((aligned(16))) std::uint16_t xs[XS_HALVES];
     __shared__ __attribute__((aligned(16))) std::uint16_t taps[C * 9];  // depthwise taps [channel][ky][kx]
     std::uint16_t* const ds = dys;  // d[pixel][C + 8]
     std::uint16_t* const ys = dys;  // y[channel][kYS], after the expand stage
@@ -158,14 +172,27 @@ __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArg
     // those channels: thread (c, g), c = 32w + lane % 32, row group
     // g = lane / 32. So the staged tile needs no workgroup barrier before the
     // depthwise stage.
-    u32x4 xp[B::XU];
+    // Channel-last: piece u of wave w is channels 32w + 8 (u % 4) .. + 7 of
+    // staged pixel u / 4 (row-major over 6 rows x 10 pixels, image pixel
+    // (y0 - 1 + row, x0 - 1 + column)), so four lanes read 64 contiguous
+    // bytes of one pixel.
+    constexpr int XU = IN_NHWC ? B::XNU : B::XU;
+    u32x4 xp[XU];
 #pragma unroll
-    for (int i = 0; i < B::XU; ++i) {
-        const int u = wave * 64 * B::XU + lane + 64 * i, k = u % (kXW / 8), r = (u / (kXW / 8)) % kXR,
-                  ch = u / ((kXW / 8) * kXR);
-        const int iy = y0 - 1 + r, ix = x0 - 8 + 8 * k;
-        const bool ok = iy >= 0 && iy < a.h && ix >= 0 && ix < a.w;
-        xp[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? ((ch * a.h + iy) * a.w + ix) * 2 : kOutOfRange, 0, 0);
+    for (int i = 0; i < XU; ++i) {
+        if constexpr (IN_NHWC) {
+            const int u = lane + 64 * i, pix = u >> 2, sub = u & 3, r = pix / kXP, px = pix % kXP;
+            const int iy = y0 - 1 + r, ix = x0 - 1 + px;
+            const bool ok = u < B::XN_PIECES && iy >= 0 && iy < a.h && ix >= 0 && ix < a.w;
+            xp[i] = __builtin_amdgcn_raw_buffer_load_b128(
+                rx, ok ? ((iy * a.w + ix) * C + 32 * wave + 8 * sub) * 2 : kOutOfRange, 0, 0);
+        } else {
+            const int u = wave * 64 * B::XU + lane + 64 * i, k = u % (kXW / 8), r = (u / (kXW / 8)) % kXR,
+                      ch = u / ((kXW / 8) * kXR);
+            const int iy = y0 - 1 + r, ix = x0 - 8 + 8 * k;
+            const bool ok = iy >= 0 && iy < a.h && ix >= 0 && ix < a.w;
+            xp[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, ok ? ((ch * a.h + iy) * a.w + ix) * 2 : kOutOfRange, 0, 0);
+        }
     }
     const int c = 32 * wave + (lane & 31), g = lane >> 5;
     // The taps of this wave's channels as 16-byte pieces, staged with the
@@ -193,10 +220,15 @@ __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArg
     __builtin_amdgcn_sched_barrier(0);
 
 #pragma unroll
-    for (int i = 0; i < B::XU; ++i) {
-        const int u = wave * 64 * B::XU + lane + 64 * i, k = u % (kXW / 8), r = (u / (kXW / 8)) % kXR,
-                  ch = u / ((kXW / 8) * kXR);
-        *reinterpret_cast<u32x4*>(&xs[ch * kXCS + r * kXW + 8 * k]) = xp[i];
+    for (int i = 0; i < XU; ++i) {
+        if constexpr (IN_NHWC) {
+            const int u = lane + 64 * i, pix = u >> 2, sub = u & 3;
+            if (u < B::XN_PIECES) *reinterpret_cast<u32x4*>(&xs[pix * XPS + 32 * wave + 8 * sub]) = xp[i];
+        } else {
+            const int u = wave * 64 * B::XU + lane + 64 * i, k = u % (kXW / 8), r = (u / (kXW / 8)) % kXR,
+                      ch = u / ((kXW / 8) * kXR);
+            *reinterpret_cast<u32x4*>(&xs[ch * kXCS + r * kXW + 8 * k]) = xp[i];
+        }
     }
     if (lane < B::WTAP) *reinterpret_cast<u32x4*>(&taps[(wave * B::WTAP + lane) * 8]) = tp;
     // Lanes read what other lanes of this wave wrote (LDS runs a wave's
@@ -209,15 +241,22 @@ __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArg
     for (int t = 0; t < 9; ++t) wdw[t] = taps[c * 9 + t];
     // This thread's halo rows from the staged tile: per row the dword of
     // columns x0-2, x0-1, the 16 bytes x0 .. x0+7 and the dword x0+8, x0+9.
+    // Channel-last: the 10 pixels of each row, one half each.
     const int row0 = g * ORT;  // staged row of image row y0 + g*ORT - 1
     std::uint32_t xl[ORT + 2], xr[ORT + 2];
     u32x4 xm[ORT + 2];
+    std::uint16_t xn[IN_NHWC ? ORT + 2 : 1][kXP];
 #pragma unroll
     for (int r = 0; r < ORT + 2; ++r) {
-        const std::uint16_t* rowp = &xs[c * kXCS + (row0 + r) * kXW];
-        xl[r] = *reinterpret_cast<const std::uint32_t*>(rowp + 6);
-        xm[r] = *reinterpret_cast<const u32x4*>(rowp + 8);
-        xr[r] = *reinterpret_cast<const std::uint32_t*>(rowp + 16);
+        if constexpr (IN_NHWC) {
+#pragma unroll
+            for (int px = 0; px < kXP; ++px) xn[r][px] = xs[((row0 + r) * kXP + px) * XPS + c];
+        } else {
+            const std::uint16_t* rowp = &xs[c * kXCS + (row0 + r) * kXW];
+            xl[r] = *reinterpret_cast<const std::uint32_t*>(rowp + 6);
+            xm[r] = *reinterpret_cast<const u32x4*>(rowp + 8);
+            xr[r] = *reinterpret_cast<const std::uint32_t*>(rowp + 16);
+        }
     }
 
     {
@@ -254,13 +293,18 @@ __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArg
                 if (iy < 0 || iy >= a.h) continue;
                 const int rr = r + ky;
                 float xv[kTW + 2];
-                xv[0] = hi_h(xl[rr]);
+                if constexpr (IN_NHWC) {
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    xv[1 + 2 * i] = lo_h(xm[rr][i]);
-                    xv[2 + 2 * i] = hi_h(xm[rr][i]);
+                    for (int px = 0; px < kXP; ++px) xv[px] = h2f(xn[rr][px]);
+                } else {
+                    xv[0] = hi_h(xl[rr]);
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        xv[1 + 2 * i] = lo_h(xm[rr][i]);
+                        xv[2 + 2 * i] = hi_h(xm[rr][i]);
+                    }
+                    xv[kTW + 1] = lo_h(xr[rr]);
                 }
-                xv[kTW + 1] = lo_h(xr[rr]);
 #pragma unroll
                 for (int px = 0; px < kTW; ++px)
 #pragma unroll
@@ -347,9 +391,20 @@ __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArg
 #pragma unroll
     for (int m = 0; m < MT2; ++m) {
         const int mt = wave * MT2 + m;
+        if constexpr (OUT_NHWC) {
+            // y[pixel][channel]: the lane's four consecutive channels per j.
+            typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-            ys[(mt * 32 + 8 * (r >> 2) + hsel + (r & 3)) * kYS + pl] = f2h(acc2[m][r]);
+            for (int j = 0; j < 4; ++j) {
+                const std::uint32_t lo = f2h(acc2[m][4 * j]) | (static_cast<std::uint32_t>(f2h(acc2[m][4 * j + 1])) << 16);
+                const std::uint32_t hi = f2h(acc2[m][4 * j + 2]) | (static_cast<std::uint32_t>(f2h(acc2[m][4 * j + 3])) << 16);
+                *reinterpret_cast<u32x2*>(&ys[pl * DST + mt * 32 + 8 * j + hsel]) = u32x2{lo, hi};
+            }
+        } else {
+#pragma unroll
+            for (int r = 0; r < 16; ++r)
+                ys[(mt * 32 + 8 * (r >> 2) + hsel + (r & 3)) * kYS + pl] = f2h(acc2[m][r]);
+        }
     }
     // Each wave writes out the channels it computed, so it waits for its own
     // LDS writes only, not for the other waves (LDS runs a wave's
@@ -361,12 +416,54 @@ __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArg
     // ---- 4. residual add, 16-byte rows out ------------------------------
     static_assert(MT2 * 32 * kTH == 64 * RV, "output rows per lane");
     std::uint16_t* yb = a.y + static_cast<size_t>(b) * C * plane;
+    // The residual x of 8 consecutive halves of the output piece: 8 channels
+    // of one pixel (channel-last output) or 8 pixels of one channel.
+    auto residual = [&](int ch, int row, int px) -> u32x4 {
+        std::uint16_t v[8];
+        if constexpr (IN_NHWC && OUT_NHWC) {
+            return *reinterpret_cast<const u32x4*>(&xs[((row + 1) * kXP + px + 1) * XPS + ch]);
+        } else if constexpr (IN_NHWC) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = xs[((row + 1) * kXP + px + 1 + k) * XPS + ch];
+        } else if constexpr (OUT_NHWC) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = xs[(ch + k) * kXCS + (row + 1) * kXW + 8 + px];
+        } else {
+            return *reinterpret_cast<const u32x4*>(&xs[ch * kXCS + (row + 1) * kXW + 8 + px]);
+        }
+        u32x4 r;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) r[k] = v[2 * k] | (static_cast<std::uint32_t>(v[2 * k + 1]) << 16);
+        return r;
+    };
+    if constexpr (OUT_NHWC) {
+        constexpr int PER = MT2 * 4;         // 16-byte pieces per pixel of this wave's channels
+        constexpr int PV = PER * kP / 64;    // per lane
+        static_assert(PER * kP % 64 == 0, "output pieces per lane");
+#pragma unroll
+        for (int i = 0; i < PV; ++i) {
+            const int v = lane + 64 * i, p = v / PER, ch = wave * MT2 * 32 + 8 * (v % PER);
+            const int row = p / kTW, px = p % kTW, gy = y0 + row;
+            if (gy >= a.h) continue;
+            const u32x4 pv = *reinterpret_cast<const u32x4*>(&ys[p * DST + ch]);
+            const u32x4 rv = residual(ch, row, px);
+            u32x4 o;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                const std::uint32_t lo = f2h(lo_h(pv[k]) + lo_h(rv[k]));
+                const std::uint32_t hi = f2h(hi_h(pv[k]) + hi_h(rv[k]));
+                o[k] = lo | (hi << 16);
+            }
+            *reinterpret_cast<u32x4*>(yb + (static_cast<size_t>(gy) * a.w + x0 + px) * C + ch) = o;
+        }
+        return;
+    }
 #pragma unroll
     for (int i = 0; i < RV; ++i) {
         const int q = lane + 64 * i, ch = wave * MT2 * 32 + q / kTH, row = q % kTH, gy = y0 + row;
         if (gy >= a.h) continue;
         const u32x4 pv = *reinterpret_cast<const u32x4*>(&ys[ch * kYS + row * kTW]);
-        const u32x4 rv = *reinterpret_cast<const u32x4*>(&xs[ch * kXCS + (row + 1) * kXW + 8]);  // residual x
+        const u32x4 rv = residual(ch, row, 0);
         u32x4 o;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -378,14 +475,23 @@ __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArg
     }
 }
 
-template <int C, int E>
-void launch(const DwBlockArgs& a, dim3 grid, hipStream_t s)
+template <int C, int E, bool IN_NHWC, bool OUT_NHWC>
+void launch_layout(const DwBlockArgs& a, dim3 grid, hipStream_t s)
 {
     // LeakyReLU form fixed at compile time (max form for 0 <= alpha <= 1).
     if (epi_mode(1, a.alpha) == 1)
-        hipLaunchKernelGGL((dwblock_kernel<C, E, 1>), grid, dim3(BlockCfg<C, E>::T), 0, s, a);
+        hipLaunchKernelGGL((dwblock_kernel<C, E, 1, IN_NHWC, OUT_NHWC>), grid, dim3(BlockCfg<C, E>::T), 0, s, a);
     else
-        hipLaunchKernelGGL((dwblock_kernel<C, E, 2>), grid, dim3(BlockCfg<C, E>::T), 0, s, a);
+        hipLaunchKernelGGL((dwblock_kernel<C, E, 2, IN_NHWC, OUT_NHWC>), grid, dim3(BlockCfg<C, E>::T), 0, s, a);
+}
+
+template <int C, int E>
+void launch(const DwBlockArgs& a, bool in_nhwc, bool out_nhwc, dim3 grid, hipStream_t s)
+{
+    if (in_nhwc && out_nhwc) launch_layout<C, E, true, true>(a, grid, s);
+    else if (in_nhwc) launch_layout<C, E, true, false>(a, grid, s);
+    else if (out_nhwc) launch_layout<C, E, false, true>(a, grid, s);
+    else launch_layout<C, E, false, false>(a, grid, s);
 }
 
 }  // namespace
@@ -439,9 +545,13 @@ int mlvc_hip_dwblock_launch(const mlvc_hip_dwblock_desc* d, mlvc_hip_stream s)
         if (nwg > 0x7FFFFFFF) throw std::runtime_error("dwblock: grid too large");
         a.nwg = static_cast<int>(nwg);
         const dim3 grid(static_cast<unsigned>(a.nwg));
-        if (d->c == 256 && d->e == 512) launch<256, 512>(a, grid, to_stream(s));
-        else if (d->c == 128 && d->e == 256) launch<128, 256>(a, grid, to_stream(s));
-        else launch<128, 512>(a, grid, to_stream(s));
+        if ((d->in_nhwc != 0 && d->in_nhwc != 1) || (d->out_nhwc != 0 && d->out_nhwc != 1))
+            throw std::runtime_error("dwblock: in_nhwc / out_nhwc must be 0 or 1");
+        if (d->x == d->y) throw std::runtime_error("dwblock: x and y must not alias (workgroups read their neighbours' x)");
+        const bool in = d->in_nhwc != 0, out = d->out_nhwc != 0;
+        if (d->c == 256 && d->e == 512) launch<256, 512>(a, in, out, grid, to_stream(s));
+        else if (d->c == 128 && d->e == 256) launch<128, 256>(a, in, out, grid, to_stream(s));
+        else launch<128, 512>(a, in, out, grid, to_stream(s));
         check(hipGetLastError(), "dwblock launch");
     });
 }

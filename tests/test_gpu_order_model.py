@@ -145,6 +145,70 @@ def test_fused_residual_block_follows_the_order_model(tmp_path):
         _compare(f"{config} output {i}", g, a, b, kinds)
 
 
+def block_chain(directory, c, e, n=2, h=10, w=24, blocks=3, also_output=None, seed=7):
+    """`blocks` depthwise-separable residual blocks in a row on x [n, c, h,
+    w]; block `also_output`'s result is a graph output as well as the next
+    block's input (so it must stay NCHW)."""
+    rng = np.random.default_rng(seed)
+    g = graphs.Graph()
+    x = g.input("x", [n, c, h, w])
+    for k in range(blocks):
+        wd = g.weight_fp16(f"wd{k}", rng.normal(0, 1 / 3, (c, 1, 3, 3)))
+        bd = g.weight_fp16(f"bd{k}", rng.normal(0, 0.01, (c,)))
+        d = g.conv(f"d{k}", x, wd, bd, (1, 1), (1, 1, 1, 1), groups=c)
+        w1 = g.weight_fp16(f"w1_{k}", rng.normal(0, 1 / np.sqrt(c), (e, c, 1, 1)))
+        b1 = g.weight_fp16(f"b1_{k}", rng.normal(0, 0.01, (e,)))
+        t = g.leaky_relu(f"t{k}", g.conv(f"e{k}", d, w1, b1), 0.01)
+        w2 = g.weight_fp16(f"w2_{k}", rng.normal(0, 1 / np.sqrt(e), (c, e, 1, 1)))
+        b2 = g.weight_fp16(f"b2_{k}", rng.normal(0, 0.01, (c,)))
+        x = g.binary("ADD", f"y{k}", g.conv(f"p{k}", t, w2, b2), x)
+        if k == also_output:
+            g.output(x)
+    g.output(x)
+    g.write(directory, "m")
+    return [graphs.half(rng.uniform(-1, 1, (n, c, h, w)))]
+
+
+@pytest.mark.parametrize("c,e", [(256, 512), (128, 256), (128, 512)])
+def test_chained_blocks_hand_over_channel_last(tmp_path, c, e):
+    """Three fused blocks in a row (batch 2, 10x24: a partial last tile row):
+    the first writes channel-last, the second reads and writes it, the third
+    reads it and writes NCHW. Every output carries the order model's bits."""
+    ins = block_chain(tmp_path, c, e)
+    gpu = mlvc_hip.Backend(tmp_path, "hip")
+    gpu.load("m")
+    kinds = [l["kind"] for l in gpu.launches()]
+    got = gpu.run(ins)[0]
+    gpu.close()
+    base = f"dwblock_c{c}_e{e}"
+    assert kinds == [base + "+nhwc_out", base + "+nhwc_in+nhwc_out", base + "+nhwc_in"], kinds
+    m2 = mlvc_oracle.OraclePlan(tmp_path, "m", isa=2).run(ins)[0]
+    m0 = mlvc_oracle.OraclePlan(tmp_path, "m", isa=0).run(ins)[0]
+    _compare(f"block chain c{c} e{e}", got, m2, m0, kinds)
+
+
+def test_block_output_read_elsewhere_stays_nchw(tmp_path, monkeypatch):
+    """A block output that is also a graph output is handed over NCHW; with
+    MLVC_HIP_BLOCK_HANDOVER=nchw every handover is NCHW, with the same
+    bits."""
+    ins = block_chain(tmp_path, 256, 512, blocks=4, also_output=1)
+    outs = {}
+    for mode in ("nhwc", "nchw"):
+        if mode == "nchw":
+            monkeypatch.setenv("MLVC_HIP_BLOCK_HANDOVER", "nchw")
+        gpu = mlvc_hip.Backend(tmp_path, "hip")
+        gpu.load("m")
+        outs[mode] = ([l["kind"] for l in gpu.launches()], gpu.run(ins))
+        gpu.close()
+    base = "dwblock_c256_e512"
+    assert outs["nhwc"][0] == [base + "+nhwc_out", base + "+nhwc_in", base + "+nhwc_out", base + "+nhwc_in"]
+    assert outs["nchw"][0] == [base] * 4
+    m2 = mlvc_oracle.OraclePlan(tmp_path, "m", isa=2).run(ins)
+    for got in (outs["nhwc"][1], outs["nchw"][1]):
+        for g, want in zip(got, m2):
+            assert np.array_equal(g, want)
+
+
 def test_stem_pair_follows_the_order_model(tmp_path):
     """SPACE_TO_DEPTH(2) -> 3x3 12->64 + LeakyReLU -> CONCAT(ref) -> 1x1
     128->64 + LeakyReLU as the fused frame-stem kernel (n5's geometry at
