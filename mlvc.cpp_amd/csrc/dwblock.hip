@@ -59,14 +59,15 @@ constexpr int kYS = kP + 8;                       // y staging row stride (halve
 #endif
 constexpr int kRing = MLVC_DW_RING;               // weight fragments in flight per wave
 #ifndef MLVC_DW_EARLY
-#define MLVC_DW_EARLY 0
+#define MLVC_DW_EARLY 8
 #endif
 // Ring slots filled before the depthwise stage; the rest are requested
 // between its rows. A wave stalls at a load while the memory request queue
 // is full, so fragments requested up front delay the start of its
 // depthwise work; requested between the depthwise rows, they keep the weight
 // stream going while the VALU works (24 slots, none up front: 12.3-14.1 to
-// 11.8-13.0 us per block).
+// 11.8-13.0 us per block with the 74 KB NCHW input tile). With the 30 KB
+// channel-last tile, 8 of them up front: 10.44 -> 10.27 us.
 constexpr int kEarly = MLVC_DW_EARLY;
 constexpr int kXR = kTH + 2, kXW = kTW + 16;      // staged input rows and columns (x0 - 8 .. x0 + kTW + 7)
 constexpr int kXP = kTW + 2;                      // channel-last staging: pixels x0 - 1 .. x0 + kTW per row
@@ -153,11 +154,14 @@ __global__ __launch_bounds__((BlockCfg<C, E>::T)) void dwblock_kernel(DwBlockArg
     const u32x4* w2 = reinterpret_cast<const u32x4*>(a.w2);
     const int koff = (lane >> 5) * 8, pl = lane & 31, hsel = 4 * (lane >> 5);
 
-    // Fragment f of this wave's stream: W1 in (k-step, m-tile) order, then W2.
+    // Fragment f of this wave's stream: W1 in (k-step, m-tile) order, then
+    // W2. The packing puts one k-step's fragments of all m-tiles next to each
+    // other, so the loads in flight across the waves of every CU cover
+    // contiguous bytes rather than one piece every 16 KB.
     auto frag = [&](int f) -> u32x4 {
-        if (f < NF1) return w1[((wave * MT1 + f % MT1) * KS1 + f / MT1) * 64 + lane];
+        if (f < NF1) return w1[((f / MT1) * (E / 32) + wave * MT1 + f % MT1) * 64 + lane];
         f -= NF1;
-        return w2[((wave * MT2 + f % MT2) * KS2 + f / MT2) * 64 + lane];
+        return w2[((f / MT2) * (C / 32) + wave * MT2 + f % MT2) * 64 + lane];
     };
     // ---- 1. input tile into LDS, coalesced --------------------------------
     // Piece u: 8 columns (x0 - 8 + 8k .. + 7) of staged row r (image row
@@ -514,9 +518,9 @@ int mlvc_hip_dwblock_pack(const uint16_t* w_mk, int m, int k, void* dst_host)
         if (m % 32 != 0 || k % 16 != 0) throw std::runtime_error("dwblock: weight shape not tileable");
         auto* out = static_cast<std::uint16_t*>(dst_host);
         size_t o = 0;
-        // [m-tile][k-step][lane][8]: lane l holds W[mt*32 + l%32][ks*16 + 8*(l/32) + j].
-        for (int mt = 0; mt < m / 32; ++mt)
-            for (int ks = 0; ks < k / 16; ++ks)
+        // [k-step][m-tile][lane][8]: lane l holds W[mt*32 + l%32][ks*16 + 8*(l/32) + j].
+        for (int ks = 0; ks < k / 16; ++ks)
+            for (int mt = 0; mt < m / 32; ++mt)
                 for (int lane = 0; lane < 64; ++lane)
                     for (int j = 0; j < 8; ++j)
                         out[o++] = w_mk[static_cast<size_t>(mt * 32 + (lane & 31)) * k + ks * 16 + 8 * (lane >> 5) + j];
