@@ -109,6 +109,13 @@ typedef struct mlvc_hip_conv_desc {
     int ksplit, split_c;               /* split K; set by mlvc_hip_conv_plan (below) */
     void* workspace;                   /* FP32 partials of a split conv, mlvc_hip_conv_workspace_bytes */
     size_t workspace_bytes;
+    /* Channel-last x ([n, ih, iw, ic]) / y ([n, oh, ow, oc]): set by the
+     * backend where a conv hands its activations to or from a fused
+     * residual block (no counterpart in the reference, whose tensors are
+     * NCHW at every node boundary). 3x3 weight-streaming variants only;
+     * channel counts a multiple of 8; in: no concat or space_to_depth
+     * fusion; out: no depth_to_space, LeakyReLU, clamp or no epilogue. */
+    int in_nhwc, out_nhwc;
 } mlvc_hip_conv_desc;
 
 /* Chooses the kernel variant for the geometry by a cost model (sets

@@ -55,9 +55,9 @@ bool fusion_enabled()
     return !(env && env[0] == '1' && env[1] == '\0');
 }
 
-// MLVC_HIP_BLOCK_HANDOVER=nchw keeps the activations between chained fused
-// blocks NCHW (default: channel-last); for comparing the two layouts, which
-// give identical results.
+// MLVC_HIP_BLOCK_HANDOVER=nchw keeps every activation NCHW (default: fused
+// blocks and the 3x3 convs around them hand over channel-last where they
+// can); for comparing the two layouts, which give identical results.
 bool block_handover_nhwc()
 {
     const char* env = std::getenv("MLVC_HIP_BLOCK_HANDOVER");
@@ -1360,22 +1360,82 @@ private:
             if (L->name.empty()) L->name = desc(L->y).name;
             launches_.push_back(std::move(L));
         }
-        // Chained fused blocks hand over channel-last: a block output whose
-        // only readers are the next block's depthwise conv and residual ADD
-        // (its two consumers) never leaves that pair of launches, so its
-        // layout is theirs to choose.
-        for (auto& P : launches_) {
-            if (!block_handover_nhwc()) break;
-            if (P->kind != Launch::kDwBlock || outputs.count(P->y) || consumers[P->y] != 2) continue;
-            for (auto& Q : launches_)
-                if (Q->kind == Launch::kDwBlock && Q->x == P->y) {
-                    P->blk.out_nhwc = 1;
-                    Q->blk.in_nhwc = 1;
-                }
+        if (block_handover_nhwc()) lower_channel_last(outputs);
+    }
+
+    // Channel-last handover: a tensor whose producer and every reader can
+    // take it as [n][h][w][c] is handed over that way. A fused block then
+    // stages a 30 KB halo of whole pixels instead of 74 KB of channel rows,
+    // and a weight-streaming conv stages 16-byte pixel pieces with no
+    // transposes. Readers are fused blocks (their depthwise conv and
+    // residual ADD: two nodes reading the tensor) and 3x3 convs reading it
+    // as their plain input (one node); every node that reads the tensor
+    // must belong to one of them, and no graph output or state is changed.
+    void lower_channel_last(const std::set<TensorId>& outputs)
+    {
+        auto conv_ok = [&](const Launch& L, int in, int out) {
+            if (L.kind != Launch::kConv || L.forced) return false;
+            mlvc_hip_conv_desc d = L.conv;
+            d.in_nhwc = in;
+            d.out_nhwc = out;
+            int count = 0;
+            return mlvc_hip_conv_candidates(&d, nullptr, 0, &count) == 0 && count > 0;
+        };
+        std::set<TensorId> cl;
+        for (const auto& P : launches_) {
+            const TensorId t = P->y;
+            if (!t || outputs.count(t) || state_out_.count(t) || !(P->kind == Launch::kDwBlock || P->kind == Launch::kConv))
+                continue;
+            int node_reads = 0, readers = 0;
+            bool ok = true;
+            for (const auto& Q : launches_) {
+                if (Q->x2 == t || Q->res == t || std::find(Q->ins.begin(), Q->ins.end(), t) != Q->ins.end()) ok = false;
+                if (!ok) break;
+                if (Q->x != t) continue;
+                ++readers;
+                if (Q->kind == Launch::kDwBlock) node_reads += 2;
+                else if (Q->kind == Launch::kConv) node_reads += 1;
+                else ok = false;
+            }
+            if (ok && readers > 0 && node_reads == consumers_[t]) cl.insert(t);
         }
-        for (auto& P : launches_)
-            if (P->kind == Launch::kDwBlock)
-                P->kind_name += std::string(P->blk.in_nhwc ? "+nhwc_in" : "") + (P->blk.out_nhwc ? "+nhwc_out" : "");
+        // A conv needs a variant for the layouts of both its operands; drop
+        // handovers until every conv has one.
+        for (bool changed = true; changed;) {
+            changed = false;
+            for (const auto& Lp : launches_) {
+                if (Lp->kind != Launch::kConv) continue;
+                const int in = cl.count(Lp->x) ? 1 : 0, out = cl.count(Lp->y) ? 1 : 0;
+                if ((in || out) && !conv_ok(*Lp, in, out)) {
+                    cl.erase(out ? Lp->y : Lp->x);
+                    changed = true;
+                }
+            }
+        }
+        for (const auto& Lp : launches_) {
+            Launch& L = *Lp;
+            const int in = cl.count(L.x) ? 1 : 0, out = cl.count(L.y) ? 1 : 0;
+            if (!in && !out) continue;
+            const std::string tag = std::string(in ? "+nhwc_in" : "") + (out ? "+nhwc_out" : "");
+            if (L.kind == Launch::kDwBlock) {
+                L.blk.in_nhwc = in;
+                L.blk.out_nhwc = out;
+                L.kind_name += tag;
+                continue;
+            }
+            // Re-plan among the variants that take the layouts and re-pack
+            // for the one chosen (its weight order can differ).
+            const std::string tags = L.kind_name.substr(std::string(mlvc_hip_conv_variant_name(L.conv.variant)).size());
+            L.conv.in_nhwc = in;
+            L.conv.out_nhwc = out;
+            hip_check(mlvc_hip_conv_plan(&L.conv), "conv planning");
+            L.kind_name = std::string(mlvc_hip_conv_variant_name(L.conv.variant)) + tags + tag;
+            for (void* old : {L.packed.ptr, L.bias.ptr})
+                pending_uploads_.erase(std::remove_if(pending_uploads_.begin(), pending_uploads_.end(),
+                                                      [&](const auto& u) { return u.first == old; }),
+                                       pending_uploads_.end());
+            pack_conv(L, L.packed, L.bias, L.conv);
+        }
     }
 
     void require_fp16_activation(TensorId id) const

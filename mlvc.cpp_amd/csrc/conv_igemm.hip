@@ -168,7 +168,16 @@ void validate(const mlvc_hip_conv_desc& d, bool pointers)
         throw std::runtime_error("conv: invalid depth_to_space fusion");
     if (d.epilogue == MLVC_EPI_REGLU && (d.oc % 64 != 0 || d.out_d2s_block > 1))
         throw std::runtime_error("conv: ReGLU epilogue needs 64-channel gate/linear blocks and no depth_to_space");
+    if ((d.in_nhwc != 0 && d.in_nhwc != 1) || (d.out_nhwc != 0 && d.out_nhwc != 1))
+        throw std::runtime_error("conv: in_nhwc / out_nhwc must be 0 or 1");
+    if (d.in_nhwc && (d.x2 || d.in_s2d_block > 1 || d.ic % 8 != 0))
+        throw std::runtime_error("conv: a channel-last input needs 8-channel groups and no concat or space_to_depth fusion");
+    if (d.out_nhwc && (d.out_d2s_block > 1 || d.oc % 8 != 0 ||
+                       !(d.epilogue == MLVC_EPI_NONE || d.epilogue == MLVC_EPI_LEAKY_RELU || d.epilogue == MLVC_EPI_CLAMP)))
+        throw std::runtime_error("conv: a channel-last output needs 8-channel groups, no depth_to_space and a "
+                                 "LeakyReLU, clamp or no epilogue");
     if (!pointers) return;
+    if (d.out_nhwc && (reinterpret_cast<std::uintptr_t>(d.y) & 15u)) throw std::runtime_error("conv: channel-last y must be 16-byte aligned");
     if (d.epilogue == MLVC_EPI_RESIDUAL_ADD && !d.residual) throw std::runtime_error("conv: residual missing");
     if (!d.x || !d.y || !d.packed_w || !d.bias) throw std::runtime_error("conv: null tensor");
 }
@@ -214,6 +223,10 @@ void split_rule(const mlvc_hip_conv_desc& d, int& ksplit, int& split_c)
 bool eligible(const mlvc_hip_conv_desc& d, const Variant& k)
 {
     if (k.bm == 0 || k.kh != d.kh || k.kw != d.kw || k.s != d.stride_h || k.s != d.stride_w) return false;
+    // Channel-last operands: the weight-streaming kernel (an output only
+    // where its [pixel][channel] tile fits the LDS).
+    if ((d.in_nhwc || d.out_nhwc) && !k.ws_ic) return false;
+    if (d.out_nhwc && !k.nhwc_out) return false;
     // Split K: conv_mfma variants whose chunk divides the split.
     if (d.ksplit > 1 && (k.ws_ic || d.split_c % k.kc != 0)) return false;
     // ReGLU pairs gate and linear rows inside 64-row blocks of one tile.
@@ -385,6 +398,10 @@ void launch_conv(const mlvc_hip_conv_desc& d, void* s)
         a.hi = d.clip_hi;
         a.ksplit = 1;
         a.split_c = d.ic;
+        a.in_nhwc = d.in_nhwc;
+        a.out_nhwc = d.out_nhwc;
+        if ((d.in_nhwc || d.out_nhwc) && (!k.ws_ic || (d.out_nhwc && !k.nhwc_out) || d.ksplit > 1))
+            throw std::runtime_error("conv: channel-last operands need a weight-streaming variant");
         if (d.ksplit > 1) {
             if (k.bm == 0 || k.ws_ic || d.split_c <= 0 || d.split_c % k.kc != 0 ||
                 static_cast<long long>(d.split_c) * (d.ksplit - 1) >= d.ic || static_cast<long long>(d.split_c) * d.ksplit < d.ic)

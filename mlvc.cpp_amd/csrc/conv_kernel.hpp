@@ -64,6 +64,9 @@ struct ConvArgs {
     // seeds its accumulators with the bias, the others with zero.
     int ksplit, split_c;
     float* part;
+    // Channel-last x ([n][ih][iw][ic]) / y ([n][oh][ow][oc]); weight-
+    // streaming kernel only.
+    int in_nhwc, out_nhwc;
 };
 
 // KC consecutive channels [c0, c0 + KC) of input pixel (iy, ix) of batch b,
@@ -716,6 +719,8 @@ struct Variant {
     // Weight-streaming kernel (conv_ws.hpp) staging ws_ic input channels
     // per pass; 0 for conv_mfma_kernel variants.
     int ws_ic = 0;
+    // Its [pixel][channel] output tile fits the LDS (channel-last output).
+    bool nhwc_out = false;
 };
 
 template <class C>

@@ -17,7 +17,12 @@
 //   * every wave covers all BN pixels, reading its B fragments from the
 //     staged halo;
 //   * two workgroups per CU (halo <= 80 KB, 128 accumulator registers), so
-//     one workgroup's staging and epilogue overlap the other's MFMAs.
+//     one workgroup's staging and epilogue overlap the other's MFMAs;
+//   * a channel-last input ([n][h][w][c], from a producer that hands its
+//     output over that way) is staged into the same halo layout as 16-byte
+//     pieces of 8 channels of one pixel, channel groups fastest across the
+//     lanes, with no transposes; a channel-last output leaves through a
+//     [pixel][channel] LDS tile as 16-byte pieces of 8 channels.
 // The conv kernel it competes with stages 16 input channels of weights and
 // input per chunk through registers and LDS with two barriers each; per
 // 128x256 tile that re-reads every weight once per 16 channels for each
@@ -48,6 +53,10 @@ struct WsCfg {
     static constexpr int UNITS = (SC / 8) * IH_T * NSEG;  // 8 channels x 8 columns each
     static constexpr int UNITS_PER_T = (UNITS + kThreads - 1) / kThreads;
     static constexpr int EPI_ROW = BN + 8, EPI_LDS = BM * EPI_ROW;
+    // Channel-last input: 16-byte pieces, 8 channels of one staged pixel
+    // each (as many as the NCHW units' row loads, so the same registers).
+    static constexpr int NPIECE = (SC / 8) * IH_T * IW_S;
+    static constexpr int NP_PER_T = (NPIECE + kThreads - 1) / kThreads;
     // Pipelined passes: two halo buffers; pass p+1 is loaded into registers
     // at the start of pass p and written to the other buffer after its first
     // 16-channel step, so one barrier per pass and no exposed staging after
@@ -63,6 +72,10 @@ struct WsCfg {
     static_assert(S == 1 || S == 2, "stride");
     static_assert(TAPS % RING == 0, "ring slots are static per tap");
     static_assert(LDS * 2 * OCC <= 160 * 1024, "LDS budget");
+    static_assert(NP_PER_T <= UNITS_PER_T * 8, "channel-last staging registers");
+    // Channel-last output: [pixel][BM + 8] tile, where it fits the LDS.
+    static constexpr int EPI_ROW_N = BM + 8;
+    static constexpr bool NHWC_EPI = BN * EPI_ROW_N <= LDS;
     __device__ static constexpr int at(int row, int x) { return row * ROW + x * PST; }
 };
 
@@ -123,7 +136,38 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
             *reinterpret_cast<u32x4*>(&lds[boff + C::at(yi, col) + c8 * 8]) = t;
         }
     };
+    // Channel-last piece q (thread t stages q = t + i * kThreads): channel
+    // group q % (SC/8) of staged pixel q / (SC/8), columns fastest, then
+    // rows; past the image, the pass or IC (a partial last pass) it reads
+    // zeros.
+    auto piece_off = [&](int cb, int q) -> std::uint32_t {
+        const int c8 = q % (C::SC / 8), pix = q / (C::SC / 8), col = pix % C::IW_S, yi = pix / C::IW_S;
+        const int iy = iy0 + yi, ix = xa + col, c = cb + 8 * c8;
+        const bool ok = q < C::NPIECE && iy >= 0 && iy < a.ih && ix >= 0 && ix < a.iw && c < a.ic;
+        return ok ? (static_cast<std::uint32_t>(iy * a.iw + ix) * static_cast<std::uint32_t>(a.ic) + c) * 2u : kOutOfRange;
+    };
+    auto load_piece = [&](std::uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(rx, static_cast<int>(off), 0, 0); };
+    auto piece_put = [&](int q, const u32x4& v, int boff) {
+        if (q >= C::NPIECE) return;
+        const int c8 = q % (C::SC / 8), pix = q / (C::SC / 8), col = pix % C::IW_S, yi = pix / C::IW_S;
+        const int lc = C::S == 1 ? col : (col & 1) * C::HALF + (col >> 1);
+        *reinterpret_cast<u32x4*>(&lds[boff + C::at(yi, lc) + c8 * 8]) = v;
+    };
     auto stage = [&](int cb) {
+        if (a.in_nhwc) {
+            constexpr int PB = 8;  // pieces in flight per thread
+#pragma unroll
+            for (int i0 = 0; i0 < C::NP_PER_T; i0 += PB) {
+                u32x4 v[PB];
+#pragma unroll
+                for (int ii = 0; ii < PB; ++ii)
+                    if (i0 + ii < C::NP_PER_T) v[ii] = load_piece(piece_off(cb, tid + (i0 + ii) * C::kThreads));
+#pragma unroll
+                for (int ii = 0; ii < PB; ++ii)
+                    if (i0 + ii < C::NP_PER_T) piece_put(tid + (i0 + ii) * C::kThreads, v[ii], 0);
+            }
+            return;
+        }
         constexpr int BATCH = C::STAGE_BATCH;  // units in flight per thread (bounds the staging registers)
 #pragma unroll
         for (int i0 = 0; i0 < C::UNITS_PER_T; i0 += BATCH) {
@@ -180,9 +224,10 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
     // LDS offset boff.
     // Pipelined passes: row loads of the next pass, NL per thread, issued
     // inside the K loop (see below).
-    constexpr int NL = C::UNITS_PER_T * 8;
+    constexpr int NL = C::UNITS_PER_T * 8, NLN = C::NP_PER_T;
     u32x4 pv[C::UNITS_PER_T][8];
     std::uint32_t poff[C::UNITS_PER_T];
+    int cb_next = 0;  // channel-last: first channel of the pass being loaded
     auto kstep = [&](int c16, int tap, int coff, int boff, bool pipe_issue) {
         const int s = c16 * C::TAPS + tap;
         const int ky = tap / C::KW, kx = tap % C::KW;
@@ -197,9 +242,15 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
             ring[tap % C::RING][mt] = frag(min(s + C::RING, total - 1), mt);
         }
         if (C::PIPE && pipe_issue) {
+            if (a.in_nhwc) {
 #pragma unroll
-            for (int q = 0; q < NL; ++q)
-                if (q * C::TAPS / NL == tap) pv[q / 8][q % 8] = load_row(poff[q / 8], q % 8);
+                for (int q = 0; q < NLN; ++q)
+                    if (q * C::TAPS / NLN == tap) pv[q / 8][q % 8] = load_piece(piece_off(cb_next, tid + q * C::kThreads));
+            } else {
+#pragma unroll
+                for (int q = 0; q < NL; ++q)
+                    if (q * C::TAPS / NL == tap) pv[q / 8][q % 8] = load_row(poff[q / 8], q % 8);
+            }
         }
         // The refill is issued here, before this tap's MFMAs, and
         // unconditionally (past the last step it re-reads that step):
@@ -227,7 +278,8 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
         int buf = 0;
         for (int cb = 0; cb < nsteps16 * 16; cb += C::SC) {
             const bool next = cb + C::SC < nsteps16 * 16;  // only the last pass can be partial
-            if (next) {
+            cb_next = cb + C::SC;
+            if (next && !a.in_nhwc) {
 #pragma unroll
                 for (int i = 0; i < C::UNITS_PER_T; ++i) poff[i] = unit_off(cb + C::SC, i);
             }
@@ -239,8 +291,13 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
                     for (int tap = 0; tap < C::TAPS; ++tap) kstep(c16, tap, j * 16, buf * C::IN_LDS, j == 0 && next);
                 }
                 if (j == C::SC / 16 - 1 && next) {
+                    if (a.in_nhwc) {
 #pragma unroll
-                    for (int i = 0; i < C::UNITS_PER_T; ++i) put(i, pv[i], (buf ^ 1) * C::IN_LDS);
+                        for (int q = 0; q < NLN; ++q) piece_put(tid + q * C::kThreads, pv[q / 8][q % 8], (buf ^ 1) * C::IN_LDS);
+                    } else {
+#pragma unroll
+                        for (int i = 0; i < C::UNITS_PER_T; ++i) put(i, pv[i], (buf ^ 1) * C::IN_LDS);
+                    }
                 }
             }
             __syncthreads();
@@ -315,6 +372,43 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
             }
         return;
     }
+    if constexpr (C::NHWC_EPI) {
+        if (a.out_nhwc) {
+            // [pixel][channel] tile: the lane's four consecutive channels of
+            // one pixel per (m-tile, n-tile, j), then 16-byte pieces of 8
+            // channels of one pixel out (the host allows no residual here).
+            typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+            __syncthreads();  // every wave is done reading the halo
+#pragma unroll
+            for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < C::NT; ++nt)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int ocl = (mt0 + mt) * 32 + 8 * j + hsel, p = nt * 32 + (lane & 31);
+                        *reinterpret_cast<u32x2*>(&lds[p * C::EPI_ROW_N + ocl]) =
+                            u32x2{pack_f16(acc[mt][nt][4 * j], acc[mt][nt][4 * j + 1]),
+                                  pack_f16(acc[mt][nt][4 * j + 2], acc[mt][nt][4 * j + 3])};
+                    }
+            __syncthreads();
+            constexpr int G8 = C::BM / 8;
+            for (int u = tid; u < C::BN * G8; u += C::kThreads) {
+                const int p = u / G8, oc = ocb * C::BM + 8 * (u % G8);
+                const int oy = ty0 + p / C::TW, ox = tx0 + p % C::TW;
+                if (oc >= a.oc || oy >= a.oh || ox >= a.ow) continue;
+                u32x4 h = *reinterpret_cast<const u32x4*>(&lds[p * C::EPI_ROW_N + 8 * (u % G8)]);
+                if (a.epi == MLVC_EPI_LEAKY_RELU) {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) h[k] = leaky_h2(h[k], a.alpha, max_form);
+                } else if (a.epi == MLVC_EPI_CLAMP) {
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) h[k] = clamp_h2(h[k], a.lo, a.hi);
+                }
+                *reinterpret_cast<u32x4*>(a.y + ((static_cast<size_t>(b) * a.oh + oy) * a.ow + ox) * a.oc + oc) = h;
+            }
+            return;
+        }
+    }
     __syncthreads();  // every wave is done reading the halo
 #pragma unroll
     for (int mt = 0; mt < C::MT; ++mt)
@@ -360,29 +454,29 @@ void launch_ws(const ConvArgs& a, dim3 grid, hipStream_t s)
 // staged SC channels per pass; no scalar or SPACE_TO_DEPTH staging.
 #define MLVC_VARIANT_WS(BM, TH, TW, SC, OCC)                                                                   \
     Variant{"ws_bm" #BM "_" #TH "x" #TW "_k3x3_s1_sc" #SC "_occ" #OCC, BM, TH, TW, 3, 3, 1, 16, nullptr,          \
-            &launch_ws<WsCfg<BM, TH, TW, SC, OCC>>, nullptr, SC}
+            &launch_ws<WsCfg<BM, TH, TW, SC, OCC>>, nullptr, SC, WsCfg<BM, TH, TW, SC, OCC>::NHWC_EPI}
 // A ring RING k-steps deep (3 or 9): with one m-tile per wave, 9 steps of
 // fragments cover the L2 latency that 3 do not.
 #define MLVC_VARIANT_WSR(BM, TH, TW, SC, OCC, RING)                                                            \
     Variant{"ws_bm" #BM "_" #TH "x" #TW "_k3x3_s1_sc" #SC "_occ" #OCC "_r" #RING, BM, TH, TW, 3, 3, 1, 16, nullptr, \
-            &launch_ws<WsCfg<BM, TH, TW, SC, OCC, 1, 4, RING>>, nullptr, SC}
+            &launch_ws<WsCfg<BM, TH, TW, SC, OCC, 1, 4, RING>>, nullptr, SC, WsCfg<BM, TH, TW, SC, OCC, 1, 4, RING>::NHWC_EPI}
 // Stride 2, WAVES waves splitting the BM output channels.
 #define MLVC_VARIANT_WS2(BM, TH, TW, SC, OCC, WAVES)                                                           \
     Variant{"ws_bm" #BM "_" #TH "x" #TW "_k3x3_s2_sc" #SC "_occ" #OCC "_w" #WAVES, BM, TH, TW, 3, 3, 2, 16, nullptr, \
-            &launch_ws<WsCfg<BM, TH, TW, SC, OCC, 2, WAVES>>, nullptr, SC}
+            &launch_ws<WsCfg<BM, TH, TW, SC, OCC, 2, WAVES>>, nullptr, SC, WsCfg<BM, TH, TW, SC, OCC, 2, WAVES>::NHWC_EPI}
 // Pipelined passes (two halo buffers, next pass staged under the current one).
 #define MLVC_VARIANT_WSP(BM, TH, TW, SC, OCC, RING)                                                            \
     Variant{"ws_bm" #BM "_" #TH "x" #TW "_k3x3_s1_sc" #SC "_occ" #OCC "_r" #RING "_pipe", BM, TH, TW, 3, 3, 1, 16,     \
-            nullptr, &launch_ws<WsCfg<BM, TH, TW, SC, OCC, 1, 4, RING, true>>, nullptr, SC}
+            nullptr, &launch_ws<WsCfg<BM, TH, TW, SC, OCC, 1, 4, RING, true>>, nullptr, SC, WsCfg<BM, TH, TW, SC, OCC, 1, 4, RING, true>::NHWC_EPI}
 // Stride 1 with WAVES waves (BM = 64 over two waves: 64-channel convs
 // without padded output rows).
 #define MLVC_VARIANT_WSW(BM, TH, TW, SC, OCC, WAVES, RING)                                                     \
     Variant{"ws_bm" #BM "_" #TH "x" #TW "_k3x3_s1_sc" #SC "_occ" #OCC "_w" #WAVES "_r" #RING, BM, TH, TW, 3, 3, 1, 16, \
-            nullptr, &launch_ws<WsCfg<BM, TH, TW, SC, OCC, 1, WAVES, RING>>, nullptr, SC}
+            nullptr, &launch_ws<WsCfg<BM, TH, TW, SC, OCC, 1, WAVES, RING>>, nullptr, SC, WsCfg<BM, TH, TW, SC, OCC, 1, WAVES, RING>::NHWC_EPI}
 // Stride 2 with a ring RING k-steps deep.
 #define MLVC_VARIANT_WS2R(BM, TH, TW, SC, OCC, WAVES, RING)                                                    \
     Variant{"ws_bm" #BM "_" #TH "x" #TW "_k3x3_s2_sc" #SC "_occ" #OCC "_w" #WAVES "_r" #RING, BM, TH, TW, 3, 3, 2, 16, \
-            nullptr, &launch_ws<WsCfg<BM, TH, TW, SC, OCC, 2, WAVES, RING>>, nullptr, SC}
+            nullptr, &launch_ws<WsCfg<BM, TH, TW, SC, OCC, 2, WAVES, RING>>, nullptr, SC, WsCfg<BM, TH, TW, SC, OCC, 2, WAVES, RING>::NHWC_EPI}
 
 }  // namespace conv
 }  // namespace mlvc_hip

@@ -21,7 +21,8 @@ class ConvDesc(C.Structure):
         ("packed_w", C.c_void_p), ("bias", C.c_void_p), ("epilogue", C.c_int), ("alpha", C.c_float),
         ("clip_lo", C.c_float), ("clip_hi", C.c_float), ("residual", C.c_void_p), ("y", C.c_void_p),
         ("out_d2s_block", C.c_int), ("variant", C.c_int), ("vector_io", C.c_int), ("ksplit", C.c_int),
-        ("split_c", C.c_int), ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t)]
+        ("split_c", C.c_int), ("workspace", C.c_void_p), ("workspace_bytes", C.c_size_t), ("in_nhwc", C.c_int),
+        ("out_nhwc", C.c_int)]
 
 
 def candidates(ic, h, w, oc, k=3, stride=1, pad=1, d2s=0, desc=None):

@@ -262,3 +262,43 @@ def test_mlvc_frame_follows_the_order_model(tmp_path):
           f"max {s2['max_ulp']} ulp mean_rel {s2['mean_rel']:.2e}; reference order identical {s0['identical']:.6f} "
           f"max {s0['max_ulp']} ulp mean_rel {s0['mean_rel']:.2e}", flush=True)
     assert s2["identical"] > s0["identical"] and s2["mean_rel"] < s0["mean_rel"], (s2, s0)
+
+
+def test_convs_and_blocks_hand_over_channel_last(tmp_path):
+    """3x3 s2 64->128 and 128->256 convs, two fused blocks, a 3x3 256->64
+    conv: every activation between them is handed over channel-last (the
+    weight-streaming kernel staging 16-byte pixel pieces and writing a
+    [pixel][channel] tile), with the order model's bits throughout."""
+    rng = np.random.default_rng(9)
+    g = graphs.Graph()
+    x = g.input("x", [1, 64, 40, 64])
+
+    def conv(name, t, ic, oc, stride):
+        w = g.weight_fp16(f"{name}_w", rng.normal(0, 1 / np.sqrt(9 * ic), (oc, ic, 3, 3)))
+        b = g.weight_fp16(f"{name}_b", rng.normal(0, 0.01, (oc,)))
+        return g.leaky_relu(f"{name}_a", g.conv(name, t, w, b, (stride, stride), (1, 1, 1, 1)), 0.01)
+
+    t = conv("c1", conv("c0", x, 64, 128, 2), 128, 256, 2)
+    for k in range(2):
+        wd = g.weight_fp16(f"wd{k}", rng.normal(0, 1 / 3, (256, 1, 3, 3)))
+        bd = g.weight_fp16(f"bd{k}", rng.normal(0, 0.01, (256,)))
+        w1 = g.weight_fp16(f"w1_{k}", rng.normal(0, 1 / 16, (512, 256, 1, 1)))
+        b1 = g.weight_fp16(f"b1_{k}", rng.normal(0, 0.01, (512,)))
+        w2 = g.weight_fp16(f"w2_{k}", rng.normal(0, 1 / np.sqrt(512), (256, 512, 1, 1)))
+        b2 = g.weight_fp16(f"b2_{k}", rng.normal(0, 0.01, (256,)))
+        e = g.leaky_relu(f"t{k}", g.conv(f"e{k}", g.conv(f"d{k}", t, wd, bd, (1, 1), (1, 1, 1, 1), groups=256), w1, b1), 0.01)
+        t = g.binary("ADD", f"y{k}", g.conv(f"p{k}", e, w2, b2), t)
+    g.output(conv("c2", t, 256, 64, 1))
+    g.write(tmp_path, "m")
+    ins = [graphs.half(rng.uniform(-1, 1, (1, 64, 40, 64)))]
+    gpu = mlvc_hip.Backend(tmp_path, "hip")
+    gpu.load("m")
+    kinds = [l["kind"] for l in gpu.launches()]
+    got = gpu.run(ins)[0]
+    gpu.close()
+    tags = [k[k.find("+nhwc"):] if "+nhwc" in k else "" for k in kinds]
+    assert tags == ["+nhwc_out", "+nhwc_in+nhwc_out", "+nhwc_in+nhwc_out", "+nhwc_in+nhwc_out", "+nhwc_in"], kinds
+    assert all(k.startswith("ws_") for k in (kinds[0], kinds[1], kinds[4])), kinds
+    m2 = mlvc_oracle.OraclePlan(tmp_path, "m", isa=2).run(ins)[0]
+    m0 = mlvc_oracle.OraclePlan(tmp_path, "m", isa=0).run(ins)[0]
+    _compare("convs and blocks channel-last", got, m2, m0, kinds)
