@@ -114,7 +114,9 @@ typedef struct mlvc_hip_conv_desc {
      * residual block (no counterpart in the reference, whose tensors are
      * NCHW at every node boundary). 3x3 weight-streaming variants only;
      * channel counts a multiple of 8; in: no concat or space_to_depth
-     * fusion; out: no depth_to_space, LeakyReLU, clamp or no epilogue. */
+     * fusion; out: LeakyReLU, clamp or no epilogue, and with
+     * depth_to_space(2) a multiple of 8 output channels after it
+     * (y: [n, 2 oh, 2 ow, oc / 4]). */
     int in_nhwc, out_nhwc;
 } mlvc_hip_conv_desc;
 

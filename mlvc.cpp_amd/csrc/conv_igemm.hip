@@ -172,10 +172,10 @@ void validate(const mlvc_hip_conv_desc& d, bool pointers)
         throw std::runtime_error("conv: in_nhwc / out_nhwc must be 0 or 1");
     if (d.in_nhwc && (d.x2 || d.in_s2d_block > 1 || d.ic % 8 != 0))
         throw std::runtime_error("conv: a channel-last input needs 8-channel groups and no concat or space_to_depth fusion");
-    if (d.out_nhwc && (d.out_d2s_block > 1 || d.oc % 8 != 0 ||
+    if (d.out_nhwc && (d.out_d2s_block > 2 || d.oc % (d.out_d2s_block == 2 ? 32 : 8) != 0 ||
                        !(d.epilogue == MLVC_EPI_NONE || d.epilogue == MLVC_EPI_LEAKY_RELU || d.epilogue == MLVC_EPI_CLAMP)))
-        throw std::runtime_error("conv: a channel-last output needs 8-channel groups, no depth_to_space and a "
-                                 "LeakyReLU, clamp or no epilogue");
+        throw std::runtime_error("conv: a channel-last output needs 8-channel groups (after depth_to_space(2), if "
+                                 "fused) and a LeakyReLU, clamp or no epilogue");
     if (!pointers) return;
     if (d.out_nhwc && (reinterpret_cast<std::uintptr_t>(d.y) & 15u)) throw std::runtime_error("conv: channel-last y must be 16-byte aligned");
     if (d.epilogue == MLVC_EPI_RESIDUAL_ADD && !d.residual) throw std::runtime_error("conv: residual missing");
@@ -226,7 +226,7 @@ bool eligible(const mlvc_hip_conv_desc& d, const Variant& k)
     // Channel-last operands: the weight-streaming kernel (an output only
     // where its [pixel][channel] tile fits the LDS).
     if ((d.in_nhwc || d.out_nhwc) && !k.ws_ic) return false;
-    if (d.out_nhwc && !k.nhwc_out) return false;
+    if (d.out_nhwc && !(k.nhwc_out & (d.out_d2s_block == 2 ? 2 : 1))) return false;
     // Split K: conv_mfma variants whose chunk divides the split.
     if (d.ksplit > 1 && (k.ws_ic || d.split_c % k.kc != 0)) return false;
     // ReGLU pairs gate and linear rows inside 64-row blocks of one tile.
@@ -400,7 +400,8 @@ void launch_conv(const mlvc_hip_conv_desc& d, void* s)
         a.split_c = d.ic;
         a.in_nhwc = d.in_nhwc;
         a.out_nhwc = d.out_nhwc;
-        if ((d.in_nhwc || d.out_nhwc) && (!k.ws_ic || (d.out_nhwc && !k.nhwc_out) || d.ksplit > 1))
+        if ((d.in_nhwc || d.out_nhwc) && (!k.ws_ic || (d.out_nhwc && !(k.nhwc_out & (d.out_d2s_block == 2 ? 2 : 1))) ||
+                                          d.ksplit > 1))
             throw std::runtime_error("conv: channel-last operands need a weight-streaming variant");
         if (d.ksplit > 1) {
             if (k.bm == 0 || k.ws_ic || d.split_c <= 0 || d.split_c % k.kc != 0 ||

@@ -719,8 +719,9 @@ struct Variant {
     // Weight-streaming kernel (conv_ws.hpp) staging ws_ic input channels
     // per pass; 0 for conv_mfma_kernel variants.
     int ws_ic = 0;
-    // Its [pixel][channel] output tile fits the LDS (channel-last output).
-    bool nhwc_out = false;
+    // Its channel-last output tile fits the LDS: bit 0 plain, bit 1 with
+    // DEPTH_TO_SPACE(2).
+    int nhwc_out = 0;
 };
 
 template <class C>

@@ -73,9 +73,12 @@ struct WsCfg {
     static_assert(TAPS % RING == 0, "ring slots are static per tap");
     static_assert(LDS * 2 * OCC <= 160 * 1024, "LDS budget");
     static_assert(NP_PER_T <= UNITS_PER_T * 8, "channel-last staging registers");
-    // Channel-last output: [pixel][BM + 8] tile, where it fits the LDS.
-    static constexpr int EPI_ROW_N = BM + 8;
-    static constexpr bool NHWC_EPI = BN * EPI_ROW_N <= LDS;
+    // Channel-last output: [pixel][BM + 8] tile, or with DEPTH_TO_SPACE(2)
+    // [subpixel][pixel][BM/4 + 8], where it fits the LDS (bit 0: plain,
+    // bit 1: DEPTH_TO_SPACE).
+    static constexpr int EPI_ROW_N = BM + 8, EPI_ROW_D = BM / 4 + 8;
+    static constexpr bool NHWC_EPI = BN * EPI_ROW_N <= LDS, NHWC_D2S_EPI = 4 * BN * EPI_ROW_D <= LDS;
+    static constexpr int NHWC_OUT = (NHWC_EPI ? 1 : 0) | (NHWC_D2S_EPI ? 2 : 0);
     __device__ static constexpr int at(int row, int x) { return row * ROW + x * PST; }
 };
 
@@ -325,6 +328,54 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
     // 16-byte rows; with DEPTH_TO_SPACE(2) the 4 channels of a lane are the
     // (dy, dx) block of output channel oc0/4, stored as two 4-byte pairs.
     const bool max_form = a.alpha >= 0.0f && a.alpha <= 1.0f;
+    if constexpr (C::NHWC_D2S_EPI) {
+        if (a.d2s == 2 && a.out_nhwc) {
+            // Channel-last DEPTH_TO_SPACE(2): conv channel ocl is output
+            // channel ocl / 4 of subpixel ocl % 4 = (dy, dx). The rounded,
+            // epilogued halves go to a [subpixel][pixel][channel] tile, which
+            // leaves as 16-byte pieces of 8 output channels of one output
+            // pixel (the host allows no residual here).
+            __syncthreads();  // every wave is done reading the halo
+#pragma unroll
+            for (int mt = 0; mt < C::MT; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < C::NT; ++nt)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const int cl = ((mt0 + mt) * 32 + 8 * j + hsel) / 4, p = nt * 32 + (lane & 31);
+                        const float v[4] = {acc[mt][nt][4 * j], acc[mt][nt][4 * j + 1], acc[mt][nt][4 * j + 2],
+                                            acc[mt][nt][4 * j + 3]};
+                        std::uint32_t h01, h23;
+                        if (a.epi == MLVC_EPI_LEAKY_RELU) {
+                            h01 = leaky_pair(v[0], v[1], a.alpha, max_form);
+                            h23 = leaky_pair(v[2], v[3], a.alpha, max_form);
+                        } else {
+                            h01 = pack_f16(v[0], v[1]);
+                            h23 = pack_f16(v[2], v[3]);
+                            if (a.epi == MLVC_EPI_CLAMP) {
+                                h01 = clamp_h2(h01, a.lo, a.hi);
+                                h23 = clamp_h2(h23, a.lo, a.hi);
+                            }
+                        }
+                        const std::uint16_t h[4] = {static_cast<std::uint16_t>(h01), static_cast<std::uint16_t>(h01 >> 16),
+                                                    static_cast<std::uint16_t>(h23), static_cast<std::uint16_t>(h23 >> 16)};
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) lds[(r * C::BN + p) * C::EPI_ROW_D + cl] = h[r];
+                    }
+            __syncthreads();
+            constexpr int G8 = C::BM / 32;  // 8-channel pieces per output pixel of this block
+            const int occ = a.oc / 4, OW2 = a.ow * 2, OH2 = a.oh * 2;
+            for (int u = tid; u < 4 * C::BN * G8; u += C::kThreads) {
+                const int g = u % G8, rp = u / G8, r = rp / C::BN, p = rp % C::BN;
+                const int oy = ty0 + p / C::TW, ox = tx0 + p % C::TW, c = ocb * (C::BM / 4) + 8 * g;
+                if (c >= occ || oy >= a.oh || ox >= a.ow) continue;
+                const u32x4 h = *reinterpret_cast<const u32x4*>(&lds[rp * C::EPI_ROW_D + 8 * g]);
+                const int Y = 2 * oy + (r >> 1), X = 2 * ox + (r & 1);
+                *reinterpret_cast<u32x4*>(a.y + ((static_cast<size_t>(b) * OH2 + Y) * OW2 + X) * occ + c) = h;
+            }
+            return;
+        }
+    }
     if (a.d2s == 2) {
         // Straight from the accumulators, no LDS and no barrier: each wave
         // writes as soon as its own K loop ends. Lanes 0-31 and 32-63 each
@@ -454,29 +505,29 @@ void launch_ws(const ConvArgs& a, dim3 grid, hipStream_t s)
 // staged SC channels per pass; no scalar or SPACE_TO_DEPTH staging.
 #define MLVC_VARIANT_WS(BM, TH, TW, SC, OCC)                                                                   \
     Variant{"ws_bm" #BM "_" #TH "x" #TW "_k3x3_s1_sc" #SC "_occ" #OCC, BM, TH, TW, 3, 3, 1, 16, nullptr,          \
-            &launch_ws<WsCfg<BM, TH, TW, SC, OCC>>, nullptr, SC, WsCfg<BM, TH, TW, SC, OCC>::NHWC_EPI}
+            &launch_ws<WsCfg<BM, TH, TW, SC, OCC>>, nullptr, SC, WsCfg<BM, TH, TW, SC, OCC>::NHWC_OUT}
 // A ring RING k-steps deep (3 or 9): with one m-tile per wave, 9 steps of
 // fragments cover the L2 latency that 3 do not.
 #define MLVC_VARIANT_WSR(BM, TH, TW, SC, OCC, RING)                                                            \
     Variant{"ws_bm" #BM "_" #TH "x" #TW "_k3x3_s1_sc" #SC "_occ" #OCC "_r" #RING, BM, TH, TW, 3, 3, 1, 16, nullptr, \
-            &launch_ws<WsCfg<BM, TH, TW, SC, OCC, 1, 4, RING>>, nullptr, SC, WsCfg<BM, TH, TW, SC, OCC, 1, 4, RING>::NHWC_EPI}
+            &launch_ws<WsCfg<BM, TH, TW, SC, OCC, 1, 4, RING>>, nullptr, SC, WsCfg<BM, TH, TW, SC, OCC, 1, 4, RING>::NHWC_OUT}
 // Stride 2, WAVES waves splitting the BM output channels.
 #define MLVC_VARIANT_WS2(BM, TH, TW, SC, OCC, WAVES)                                                           \
     Variant{"ws_bm" #BM "_" #TH "x" #TW "_k3x3_s2_sc" #SC "_occ" #OCC "_w" #WAVES, BM, TH, TW, 3, 3, 2, 16, nullptr, \
-            &launch_ws<WsCfg<BM, TH, TW, SC, OCC, 2, WAVES>>, nullptr, SC, WsCfg<BM, TH, TW, SC, OCC, 2, WAVES>::NHWC_EPI}
+            &launch_ws<WsCfg<BM, TH, TW, SC, OCC, 2, WAVES>>, nullptr, SC, WsCfg<BM, TH, TW, SC, OCC, 2, WAVES>::NHWC_OUT}
 // Pipelined passes (two halo buffers, next pass staged under the current one).
 #define MLVC_VARIANT_WSP(BM, TH, TW, SC, OCC, RING)                                                            \
     Variant{"ws_bm" #BM "_" #TH "x" #TW "_k3x3_s1_sc" #SC "_occ" #OCC "_r" #RING "_pipe", BM, TH, TW, 3, 3, 1, 16,     \
-            nullptr, &launch_ws<WsCfg<BM, TH, TW, SC, OCC, 1, 4, RING, true>>, nullptr, SC, WsCfg<BM, TH, TW, SC, OCC, 1, 4, RING, true>::NHWC_EPI}
+            nullptr, &launch_ws<WsCfg<BM, TH, TW, SC, OCC, 1, 4, RING, true>>, nullptr, SC, WsCfg<BM, TH, TW, SC, OCC, 1, 4, RING, true>::NHWC_OUT}
 // Stride 1 with WAVES waves (BM = 64 over two waves: 64-channel convs
 // without padded output rows).
 #define MLVC_VARIANT_WSW(BM, TH, TW, SC, OCC, WAVES, RING)                                                     \
     Variant{"ws_bm" #BM "_" #TH "x" #TW "_k3x3_s1_sc" #SC "_occ" #OCC "_w" #WAVES "_r" #RING, BM, TH, TW, 3, 3, 1, 16, \
-            nullptr, &launch_ws<WsCfg<BM, TH, TW, SC, OCC, 1, WAVES, RING>>, nullptr, SC, WsCfg<BM, TH, TW, SC, OCC, 1, WAVES, RING>::NHWC_EPI}
+            nullptr, &launch_ws<WsCfg<BM, TH, TW, SC, OCC, 1, WAVES, RING>>, nullptr, SC, WsCfg<BM, TH, TW, SC, OCC, 1, WAVES, RING>::NHWC_OUT}
 // Stride 2 with a ring RING k-steps deep.
 #define MLVC_VARIANT_WS2R(BM, TH, TW, SC, OCC, WAVES, RING)                                                    \
     Variant{"ws_bm" #BM "_" #TH "x" #TW "_k3x3_s2_sc" #SC "_occ" #OCC "_w" #WAVES "_r" #RING, BM, TH, TW, 3, 3, 2, 16, \
-            nullptr, &launch_ws<WsCfg<BM, TH, TW, SC, OCC, 2, WAVES, RING>>, nullptr, SC, WsCfg<BM, TH, TW, SC, OCC, 2, WAVES, RING>::NHWC_EPI}
+            nullptr, &launch_ws<WsCfg<BM, TH, TW, SC, OCC, 2, WAVES, RING>>, nullptr, SC, WsCfg<BM, TH, TW, SC, OCC, 2, WAVES, RING>::NHWC_OUT}
 
 }  // namespace conv
 }  // namespace mlvc_hip

@@ -302,3 +302,30 @@ def test_convs_and_blocks_hand_over_channel_last(tmp_path):
     m2 = mlvc_oracle.OraclePlan(tmp_path, "m", isa=2).run(ins)[0]
     m0 = mlvc_oracle.OraclePlan(tmp_path, "m", isa=0).run(ins)[0]
     _compare("convs and blocks channel-last", got, m2, m0, kinds)
+
+
+def test_depth_to_space_chain_hands_over_channel_last(tmp_path):
+    """3x3 256->768, 192->512 and 128->256 convs, each + LeakyReLU +
+    DEPTH_TO_SPACE(2) (n72 -> n75 -> n78 at reduced size): the first two
+    write their shuffled outputs channel-last, the second and third stage
+    them as pixel pieces; the last output (a graph output) stays NCHW."""
+    rng = np.random.default_rng(12)
+    g = graphs.Graph()
+    t = g.input("x", [1, 256, 12, 24])
+    for k, (ic, oc) in enumerate([(256, 768), (192, 512), (128, 256)]):
+        w = g.weight_fp16(f"w{k}", rng.normal(0, 1 / np.sqrt(9 * ic), (oc, ic, 3, 3)))
+        b = g.weight_fp16(f"b{k}", rng.normal(0, 0.01, (oc,)))
+        t = g.pixel("DEPTH_TO_SPACE", f"s{k}", g.leaky_relu(f"a{k}", g.conv(f"c{k}", t, w, b, (1, 1), (1, 1, 1, 1)), 0.01), 2)
+    g.output(t)
+    g.write(tmp_path, "m")
+    ins = [graphs.half(rng.uniform(-1, 1, (1, 256, 12, 24)))]
+    gpu = mlvc_hip.Backend(tmp_path, "hip")
+    gpu.load("m")
+    kinds = [l["kind"] for l in gpu.launches()]
+    got = gpu.run(ins)[0]
+    gpu.close()
+    assert [k[k.find("+nhwc"):] if "+nhwc" in k else "" for k in kinds] == ["+nhwc_out", "+nhwc_in+nhwc_out", "+nhwc_in"], kinds
+    assert all(k.startswith("ws_") and "+d2s" in k for k in kinds), kinds
+    m2 = mlvc_oracle.OraclePlan(tmp_path, "m", isa=2).run(ins)[0]
+    m0 = mlvc_oracle.OraclePlan(tmp_path, "m", isa=0).run(ins)[0]
+    _compare("depth_to_space chain channel-last", got, m2, m0, kinds)
