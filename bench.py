@@ -708,7 +708,7 @@ def measured_traffic(path, launch_names, kind):
     try:
         for line in pathlib.Path(path).read_text().splitlines():
             f = line.split()
-            if len(f) == 5 and f[0] == "traffic:" and f[1] in launch_names and f[2] == kind:
+            if len(f) == 5 and f[0] == "traffic:" and f[1] in launch_names and base_kind(f[2]) == base_kind(kind):
                 return float(f[3]) + float(f[4])
     except OSError:
         pass
