@@ -38,6 +38,12 @@ const Variant kTable[] = {
     // Short, narrow tiles for deep convs onto few pixels (46x80 outputs).
     MLVC_VARIANT_WS2R(64, 2, 16, 64, 4, 2, 9),
     MLVC_VARIANT_WS2R(128, 2, 16, 64, 2, 4, 9),
+    // All 192 output channels in one block over tiles dividing 136x240 (no
+    // padded rows or columns), and one 32-pixel tile of all 256 channels per
+    // CU at 68x120 (255 workgroups).
+    MLVC_VARIANT_WS2R(192, 4, 24, 64, 2, 6, 9),
+    MLVC_VARIANT_WS2R(192, 2, 48, 64, 2, 6, 9),
+    MLVC_VARIANT_WS2R(256, 4, 8, 64, 2, 8, 9),
 };
 }  // namespace
 
