@@ -44,6 +44,9 @@ const Variant kTable[] = {
     MLVC_VARIANT_WS2R(192, 4, 24, 64, 2, 6, 9),
     MLVC_VARIANT_WS2R(192, 2, 48, 64, 2, 6, 9),
     MLVC_VARIANT_WS2R(256, 4, 8, 64, 2, 8, 9),
+    // Four workgroups per CU (128 registers, 29 KB of LDS each): the
+    // stride-2 convs wait on memory, and more waves keep more loads in flight.
+    MLVC_VARIANT_WS2(128, 2, 32, 32, 4, 4),
 };
 }  // namespace
 
