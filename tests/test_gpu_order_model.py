@@ -264,14 +264,17 @@ def test_mlvc_frame_follows_the_order_model(tmp_path):
     assert s2["identical"] > s0["identical"] and s2["mean_rel"] < s0["mean_rel"], (s2, s0)
 
 
-def test_convs_and_blocks_hand_over_channel_last(tmp_path):
+@pytest.mark.parametrize("n,h", [(1, 40), (2, 44)])
+def test_convs_and_blocks_hand_over_channel_last(tmp_path, n, h):
     """3x3 s2 64->128 and 128->256 convs, two fused blocks, a 3x3 256->64
     conv: every activation between them is handed over channel-last (the
     weight-streaming kernel staging 16-byte pixel pieces and writing a
-    [pixel][channel] tile), with the order model's bits throughout."""
+    [pixel][channel] tile), with the order model's bits throughout; one
+    image, and a batch of two whose 11-row block input leaves partial
+    tiles."""
     rng = np.random.default_rng(9)
     g = graphs.Graph()
-    x = g.input("x", [1, 64, 40, 64])
+    x = g.input("x", [n, 64, h, 64])
 
     def conv(name, t, ic, oc, stride):
         w = g.weight_fp16(f"{name}_w", rng.normal(0, 1 / np.sqrt(9 * ic), (oc, ic, 3, 3)))
@@ -290,7 +293,7 @@ def test_convs_and_blocks_hand_over_channel_last(tmp_path):
         t = g.binary("ADD", f"y{k}", g.conv(f"p{k}", e, w2, b2), t)
     g.output(conv("c2", t, 256, 64, 1))
     g.write(tmp_path, "m")
-    ins = [graphs.half(rng.uniform(-1, 1, (1, 64, 40, 64)))]
+    ins = [graphs.half(rng.uniform(-1, 1, (n, 64, h, 64)))]
     gpu = mlvc_hip.Backend(tmp_path, "hip")
     gpu.load("m")
     kinds = [l["kind"] for l in gpu.launches()]
@@ -301,24 +304,25 @@ def test_convs_and_blocks_hand_over_channel_last(tmp_path):
     assert all(k.startswith("ws_") for k in (kinds[0], kinds[1], kinds[4])), kinds
     m2 = mlvc_oracle.OraclePlan(tmp_path, "m", isa=2).run(ins)[0]
     m0 = mlvc_oracle.OraclePlan(tmp_path, "m", isa=0).run(ins)[0]
-    _compare("convs and blocks channel-last", got, m2, m0, kinds)
+    _compare(f"convs and blocks channel-last n{n} h{h}", got, m2, m0, kinds)
 
 
 def test_depth_to_space_chain_hands_over_channel_last(tmp_path):
     """3x3 256->768, 192->512 and 128->256 convs, each + LeakyReLU +
-    DEPTH_TO_SPACE(2) (n72 -> n75 -> n78 at reduced size): the first two
-    write their shuffled outputs channel-last, the second and third stage
-    them as pixel pieces; the last output (a graph output) stays NCHW."""
+    DEPTH_TO_SPACE(2) (n72 -> n75 -> n78 at reduced size, batch 2, 10 rows:
+    partial tiles): the first two write their shuffled outputs channel-last,
+    the second and third stage them as pixel pieces; the last output (a
+    graph output) stays NCHW."""
     rng = np.random.default_rng(12)
     g = graphs.Graph()
-    t = g.input("x", [1, 256, 12, 24])
+    t = g.input("x", [2, 256, 10, 24])
     for k, (ic, oc) in enumerate([(256, 768), (192, 512), (128, 256)]):
         w = g.weight_fp16(f"w{k}", rng.normal(0, 1 / np.sqrt(9 * ic), (oc, ic, 3, 3)))
         b = g.weight_fp16(f"b{k}", rng.normal(0, 0.01, (oc,)))
         t = g.pixel("DEPTH_TO_SPACE", f"s{k}", g.leaky_relu(f"a{k}", g.conv(f"c{k}", t, w, b, (1, 1), (1, 1, 1, 1)), 0.01), 2)
     g.output(t)
     g.write(tmp_path, "m")
-    ins = [graphs.half(rng.uniform(-1, 1, (1, 256, 12, 24)))]
+    ins = [graphs.half(rng.uniform(-1, 1, (2, 256, 10, 24)))]
     gpu = mlvc_hip.Backend(tmp_path, "hip")
     gpu.load("m")
     kinds = [l["kind"] for l in gpu.launches()]
