@@ -856,6 +856,19 @@ def main() -> int:
         gpu.upload_inputs([mlvc_hip.synth_input(CONFIG, 0, 0, shape)])
         gpu.reset_state()
         gpu.time_frames(args.warmup)
+        # Right after load() the GPU is still raising its clocks (per-frame
+        # times settle after about 30 frames), so the other measurements come
+        # first: cold frames (a 512 MiB device copy before each frame,
+        # outside its events, evicts L2, 4 MB per XCD, and the 256 MB MALL;
+        # the clock ramp can only make them read slower), the per-launch
+        # table and the per-frame spread (events around every frame of a
+        # back-to-back run). Then the state is reset and the W warm-up frames
+        # run again right before the K timed ones.
+        cold = gpu.time_frames_each(args.cold_frames, COLD_FLUSH_BYTES) if args.cold_frames > 0 else None
+        rows = kernel_table(gpu, args.kernel_reps, args.launch_cold_reps)
+        each = gpu.time_frames_each(args.steps)
+        gpu.reset_state()
+        gpu.time_frames(args.warmup)
         # Timed region: K frames replayed back to back; the call synchronises
         # on an event recorded after the last frame.
         t0 = time.perf_counter()
@@ -865,17 +878,11 @@ def main() -> int:
         launches = gpu.launches()
         conv_flops = sum(l["flops"] for l in launches)
         frame_bytes = sum(l["bytes"] for l in launches)
-        # Per-frame spread (events around every frame of a back-to-back run),
-        # then cold frames: a 512 MiB device copy before each frame, outside
-        # its events, evicts L2 (4 MB per XCD) and the 256 MB MALL.
-        each = gpu.time_frames_each(args.steps)
-        cold = gpu.time_frames_each(args.cold_frames, COLD_FLUSH_BYTES) if args.cold_frames > 0 else None
         frame_ms = spread(each)
         cold_ms = dict(spread(cold), flush_bytes=COLD_FLUSH_BYTES) if cold is not None else None
         log(f"per frame: median {frame_ms['median']:.3f} ms (p10 {frame_ms['p10']:.3f}, p90 {frame_ms['p90']:.3f})"
             + (f"; cold (L2 + MALL flushed) median {cold_ms['median']:.3f} ms (p10 {cold_ms['p10']:.3f}, "
                f"p90 {cold_ms['p90']:.3f})" if cold_ms else ""))
-        rows = kernel_table(gpu, args.kernel_reps, args.launch_cold_reps)
         # The dominant kernel is the one with the largest share of the frame:
         # launches of one kernel variant on one shape (the 12 fused residual
         # blocks) count together. The longest single launch goes beside it.
