@@ -1,7 +1,7 @@
 """Packs model bundles into an embedded model image (include/mlvc_embedded_models.h).
 
 Replaces the reference's `package.py embed` step (tools/python/mlvc_tools/
-package.py:207-306) for this build. For every profile, the bundle directory
+package.py:207-306) for this library. For every profile, the bundle directory
 is checked first (every artifact of model_bundle.pb present with its size
 and SHA-256, through the runtime's own check; the manifest's profile equal to
 the profile name; with a model root, the directory named

@@ -6,7 +6,7 @@
 // reference's runtime/include/mlvc/runtime/aot_graph.hpp:16-125 (the operator
 // contract that backends consume). decode_graph_binary applies the same
 // validation rules as the reference's runtime/src/aot_graph.cpp:110-284 but
-// parses the protobuf wire format with this build's own codec (wire.hpp), so
+// parses the protobuf wire format with this library's own codec (wire.hpp), so
 // no protobuf library is needed.
 
 #include "mlvc/core/assets.hpp"
