@@ -47,6 +47,12 @@ const Variant kTable[] = {
     // Four workgroups per CU (128 registers, 29 KB of LDS each): the
     // stride-2 convs wait on memory, and more waves keep more loads in flight.
     MLVC_VARIANT_WS2(128, 2, 32, 32, 4, 4),
+    // One 8x16 tile of all 192 output channels per CU at 136x240 (255
+    // workgroups of six waves, 109 KB of LDS for two halo buffers): each CU
+    // streams the 442 KB weight set of a 128 -> 192 conv once, where the
+    // 128-channel 2x32 tiles stream 1.25 MB per CU (4.25 workgroups of
+    // 295 KB each).
+    MLVC_VARIANT_WS2P(192, 8, 16, 32, 1, 6, 9),
 };
 }  // namespace
 

@@ -528,6 +528,11 @@ void launch_ws(const ConvArgs& a, dim3 grid, hipStream_t s)
 #define MLVC_VARIANT_WS2R(BM, TH, TW, SC, OCC, WAVES, RING)                                                    \
     Variant{"ws_bm" #BM "_" #TH "x" #TW "_k3x3_s2_sc" #SC "_occ" #OCC "_w" #WAVES "_r" #RING, BM, TH, TW, 3, 3, 2, 16, \
             nullptr, &launch_ws<WsCfg<BM, TH, TW, SC, OCC, 2, WAVES, RING>>, nullptr, SC, WsCfg<BM, TH, TW, SC, OCC, 2, WAVES, RING>::NHWC_OUT}
+// Stride 2 with a ring RING k-steps deep and pipelined passes.
+#define MLVC_VARIANT_WS2P(BM, TH, TW, SC, OCC, WAVES, RING)                                                    \
+    Variant{"ws_bm" #BM "_" #TH "x" #TW "_k3x3_s2_sc" #SC "_occ" #OCC "_w" #WAVES "_r" #RING "_pipe", BM, TH, TW, 3, 3, 2, \
+            16, nullptr, &launch_ws<WsCfg<BM, TH, TW, SC, OCC, 2, WAVES, RING, true>>, nullptr, SC,                     \
+            WsCfg<BM, TH, TW, SC, OCC, 2, WAVES, RING, true>::NHWC_OUT}
 
 }  // namespace conv
 }  // namespace mlvc_hip

@@ -307,6 +307,44 @@ def test_convs_and_blocks_hand_over_channel_last(tmp_path, n, h):
     _compare(f"convs and blocks channel-last n{n} h{h}", got, m2, m0, kinds)
 
 
+def test_stride2_chain_on_one_tile_per_cu_variant(tmp_path, monkeypatch):
+    """3x3 stride-2 convs 64->128->192->256 (n6 -> n8 -> n10 at reduced
+    size, batch 2, partial 8x16 tiles), all three on the pipelined 8x16
+    tile of 192 output channels, named by a tuning file: channel-last
+    output, input and output, input; 64 and 128 padded output rows in the
+    first and last conv's blocks. Bits of the order model."""
+    variant = "ws_bm192_8x16_k3x3_s2_sc32_occ1_w6_r9_pipe"
+    assert variant in mlvc_hip.conv_variants()
+    rng = np.random.default_rng(13)
+    g = graphs.Graph()
+    t = g.input("x", [2, 64, 44, 128])
+    for k, (ic, oc) in enumerate([(64, 128), (128, 192), (192, 256)]):
+        w = g.weight_fp16(f"w{k}", rng.normal(0, 1 / np.sqrt(9 * ic), (oc, ic, 3, 3)))
+        b = g.weight_fp16(f"b{k}", rng.normal(0, 0.01, (oc,)))
+        t = g.leaky_relu(f"a{k}", g.conv(f"c{k}", t, w, b, (2, 2), (1, 1, 1, 1)), 0.01)
+    g.output(t)
+    g.write(tmp_path, "m")
+    ins = [graphs.half(rng.uniform(-1, 1, (2, 64, 44, 128)))]
+    gpu = mlvc_hip.Backend(tmp_path, "hip")
+    gpu.load("m")
+    names = [l["name"] for l in gpu.launches()]
+    gpu.close()
+    tune = tmp_path / "tune.txt"
+    tune.write_text("".join(f"m:{n} {variant}\n" for n in names))
+    monkeypatch.setenv("MLVC_HIP_TUNE_FILE", str(tune))
+    gpu = mlvc_hip.Backend(tmp_path, "hip")
+    gpu.load("m")
+    kinds = [l["kind"] for l in gpu.launches()]
+    got = gpu.run(ins)[0]
+    gpu.close()
+    assert len(kinds) == 3 and all(k.startswith(variant + "+") for k in kinds), kinds
+    tags = [k[k.find("+nhwc"):] if "+nhwc" in k else "" for k in kinds]
+    assert tags == ["+nhwc_out", "+nhwc_in+nhwc_out", "+nhwc_in"], kinds
+    m2 = mlvc_oracle.OraclePlan(tmp_path, "m", isa=2).run(ins)[0]
+    m0 = mlvc_oracle.OraclePlan(tmp_path, "m", isa=0).run(ins)[0]
+    _compare("stride-2 chain on the 8x16 tile of 192 channels", got, m2, m0, kinds)
+
+
 def test_depth_to_space_chain_hands_over_channel_last(tmp_path):
     """3x3 256->768, 192->512 and 128->256 convs, each + LeakyReLU +
     DEPTH_TO_SPACE(2) (n72 -> n75 -> n78 at reduced size, batch 2, 10 rows:
