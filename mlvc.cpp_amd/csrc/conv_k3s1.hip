@@ -70,6 +70,11 @@ const Variant kTable[] = {
     // (46x80 and 92x160 planes).
     MLVC_VARIANT_WSW(64, 2, 16, 64, 4, 2, 9),
     MLVC_VARIANT_WSR(128, 2, 16, 64, 2, 9),
+    // 512 output channels at 136x240 in one round of two workgroups per CU:
+    // 255 8x16 tiles x 2 channel blocks = 510 workgroups, where the 4x48
+    // tiles' 680 take two rounds of 512 slots with the second a third full.
+    // LDS for the channel-last DEPTH_TO_SPACE(2) output tile (72 KB).
+    MLVC_VARIANT_WSPD(256, 8, 16, 32, 2, 3),
 };
 }  // namespace
 

@@ -35,7 +35,8 @@
 namespace mlvc_hip {
 namespace conv {
 
-template <int BM_, int TH_, int TW_, int SC_, int OCC_ = 2, int S_ = 1, int WAVES_ = 4, int RING_ = 3, bool PIPE_ = false>
+template <int BM_, int TH_, int TW_, int SC_, int OCC_ = 2, int S_ = 1, int WAVES_ = 4, int RING_ = 3, bool PIPE_ = false,
+          bool CL_D2S_ = false>
 struct WsCfg {
     static constexpr int BM = BM_, TH = TH_, TW = TW_, SC = SC_, OCC = OCC_, S = S_;
     static constexpr int KH = 3, KW = 3, TAPS = 9;
@@ -63,7 +64,12 @@ struct WsCfg {
     // the first pass.
     static constexpr bool PIPE = PIPE_;
     static constexpr int NBUF = PIPE ? 2 : 1;
-    static constexpr int LDS = NBUF * IN_LDS > EPI_LDS ? NBUF * IN_LDS : EPI_LDS;  // the plain epilogue's tile aliases the halo
+    // Channel-last output: [pixel][BM + 8] tile, or with DEPTH_TO_SPACE(2)
+    // [subpixel][pixel][BM/4 + 8], where it fits the LDS (bit 0: plain,
+    // bit 1: DEPTH_TO_SPACE). CL_D2S sizes the LDS for the second one.
+    static constexpr int EPI_ROW_N = BM + 8, EPI_ROW_D = BM / 4 + 8;
+    static constexpr int LDS_HALO = NBUF * IN_LDS > EPI_LDS ? NBUF * IN_LDS : EPI_LDS;  // the plain epilogue's tile aliases the halo
+    static constexpr int LDS = CL_D2S_ && 4 * BN * EPI_ROW_D > LDS_HALO ? 4 * BN * EPI_ROW_D : LDS_HALO;
     static constexpr int RING = RING_;               // A-fragment prefetch distance in k-steps
     // Staging units in flight per thread: 2, or 1 where the accumulators and
     // the ring leave no room for a second unit's 32 registers.
@@ -73,10 +79,6 @@ struct WsCfg {
     static_assert(TAPS % RING == 0, "ring slots are static per tap");
     static_assert(LDS * 2 * OCC <= 160 * 1024, "LDS budget");
     static_assert(NP_PER_T <= UNITS_PER_T * 8, "channel-last staging registers");
-    // Channel-last output: [pixel][BM + 8] tile, or with DEPTH_TO_SPACE(2)
-    // [subpixel][pixel][BM/4 + 8], where it fits the LDS (bit 0: plain,
-    // bit 1: DEPTH_TO_SPACE).
-    static constexpr int EPI_ROW_N = BM + 8, EPI_ROW_D = BM / 4 + 8;
     static constexpr bool NHWC_EPI = BN * EPI_ROW_N <= LDS, NHWC_D2S_EPI = 4 * BN * EPI_ROW_D <= LDS;
     static constexpr int NHWC_OUT = (NHWC_EPI ? 1 : 0) | (NHWC_D2S_EPI ? 2 : 0);
     __device__ static constexpr int at(int row, int x) { return row * ROW + x * PST; }
@@ -528,6 +530,12 @@ void launch_ws(const ConvArgs& a, dim3 grid, hipStream_t s)
 #define MLVC_VARIANT_WS2R(BM, TH, TW, SC, OCC, WAVES, RING)                                                    \
     Variant{"ws_bm" #BM "_" #TH "x" #TW "_k3x3_s2_sc" #SC "_occ" #OCC "_w" #WAVES "_r" #RING, BM, TH, TW, 3, 3, 2, 16, \
             nullptr, &launch_ws<WsCfg<BM, TH, TW, SC, OCC, 2, WAVES, RING>>, nullptr, SC, WsCfg<BM, TH, TW, SC, OCC, 2, WAVES, RING>::NHWC_OUT}
+// Pipelined passes, with the LDS sized for the channel-last
+// DEPTH_TO_SPACE(2) output tile.
+#define MLVC_VARIANT_WSPD(BM, TH, TW, SC, OCC, RING)                                                           \
+    Variant{"ws_bm" #BM "_" #TH "x" #TW "_k3x3_s1_sc" #SC "_occ" #OCC "_r" #RING "_pipe", BM, TH, TW, 3, 3, 1, 16,     \
+            nullptr, &launch_ws<WsCfg<BM, TH, TW, SC, OCC, 1, 4, RING, true, true>>, nullptr, SC,                     \
+            WsCfg<BM, TH, TW, SC, OCC, 1, 4, RING, true, true>::NHWC_OUT}
 // Stride 2 with a ring RING k-steps deep and pipelined passes.
 #define MLVC_VARIANT_WS2P(BM, TH, TW, SC, OCC, WAVES, RING)                                                    \
     Variant{"ws_bm" #BM "_" #TH "x" #TW "_k3x3_s2_sc" #SC "_occ" #OCC "_w" #WAVES "_r" #RING "_pipe", BM, TH, TW, 3, 3, 2, \

@@ -345,12 +345,15 @@ def test_stride2_chain_on_one_tile_per_cu_variant(tmp_path, monkeypatch):
     _compare("stride-2 chain on the 8x16 tile of 192 channels", got, m2, m0, kinds)
 
 
-def test_depth_to_space_chain_hands_over_channel_last(tmp_path):
+@pytest.mark.parametrize("variant", [None, "ws_bm256_8x16_k3x3_s1_sc32_occ2_r3_pipe"])
+def test_depth_to_space_chain_hands_over_channel_last(tmp_path, monkeypatch, variant):
     """3x3 256->768, 192->512 and 128->256 convs, each + LeakyReLU +
     DEPTH_TO_SPACE(2) (n72 -> n75 -> n78 at reduced size, batch 2, 10 rows:
     partial tiles): the first two write their shuffled outputs channel-last,
     the second and third stage them as pixel pieces; the last output (a
-    graph output) stays NCHW."""
+    graph output) stays NCHW. Once as tuned, once with all three on the
+    8x16 tile of 256 channels whose LDS holds the channel-last
+    DEPTH_TO_SPACE tile (named by a tuning file)."""
     rng = np.random.default_rng(12)
     g = graphs.Graph()
     t = g.input("x", [2, 256, 10, 24])
@@ -361,6 +364,15 @@ def test_depth_to_space_chain_hands_over_channel_last(tmp_path):
     g.output(t)
     g.write(tmp_path, "m")
     ins = [graphs.half(rng.uniform(-1, 1, (2, 256, 10, 24)))]
+    if variant is not None:
+        assert variant in mlvc_hip.conv_variants()
+        gpu = mlvc_hip.Backend(tmp_path, "hip")
+        gpu.load("m")
+        names = [l["name"] for l in gpu.launches()]
+        gpu.close()
+        tune = tmp_path / "tune.txt"
+        tune.write_text("".join(f"m:{n} {variant}\n" for n in names))
+        monkeypatch.setenv("MLVC_HIP_TUNE_FILE", str(tune))
     gpu = mlvc_hip.Backend(tmp_path, "hip")
     gpu.load("m")
     kinds = [l["kind"] for l in gpu.launches()]
@@ -368,6 +380,8 @@ def test_depth_to_space_chain_hands_over_channel_last(tmp_path):
     gpu.close()
     assert [k[k.find("+nhwc"):] if "+nhwc" in k else "" for k in kinds] == ["+nhwc_out", "+nhwc_in+nhwc_out", "+nhwc_in"], kinds
     assert all(k.startswith("ws_") and "+d2s" in k for k in kinds), kinds
+    if variant is not None:
+        assert all(k.startswith(variant + "+") for k in kinds), kinds
     m2 = mlvc_oracle.OraclePlan(tmp_path, "m", isa=2).run(ins)[0]
     m0 = mlvc_oracle.OraclePlan(tmp_path, "m", isa=0).run(ins)[0]
-    _compare("depth_to_space chain channel-last", got, m2, m0, kinds)
+    _compare(f"depth_to_space chain channel-last ({variant or 'tuned'})", got, m2, m0, kinds)
