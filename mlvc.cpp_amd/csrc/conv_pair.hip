@@ -502,19 +502,35 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void c
             }
         const int ix0 = t.tx0 - 1, col_off = ix0 - (ix0 - (((ix0 % 8) + 8) % 8));
         const int pxi = (lane & 31) + col_off;
+        // The operands of tap t + 1 are read from LDS during tap t (after its
+        // loads, before its MFMAs), so each tap's MFMAs find theirs in
+        // registers: with the scheduling barriers that keep the loads one per
+        // tap, reads issued at their own tap left the LDS latency in front of
+        // every pair of MFMAs (phase A 3.45k -> 2.9k cycles per tile).
+        auto bfrag = [&](int tap) { return *reinterpret_cast<const half8*>(&in_s[C::at(wave + tap / 3, pxi + tap % 3) + koff]); };
+        auto afrag = [&](int tap, int mt) { return *reinterpret_cast<const half8*>(&wa_s[((tap * C::MTA + mt) * 64 + lane) * 8]); };
+        half8 bcur = bfrag(0), acur[C::MTA];
+#pragma unroll
+        for (int mt = 0; mt < C::MTA; ++mt) acur[mt] = afrag(0, mt);
 #pragma unroll
         for (int tap = 0; tap < 9; ++tap) {
-            const int ky = tap / 3, kx = tap % 3;
             if (tap < 8) {
                 fetch_k(tn, more, tap);
                 __builtin_amdgcn_sched_barrier(0);
             }
-            const half8 bv = *reinterpret_cast<const half8*>(&in_s[C::at(wave + ky, pxi + kx) + koff]);
+            half8 bnext = bcur, anext[C::MTA];
 #pragma unroll
-            for (int mt = 0; mt < C::MTA; ++mt) {
-                const half8 av = *reinterpret_cast<const half8*>(&wa_s[((tap * C::MTA + mt) * 64 + lane) * 8]);
-                acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, acc[mt], 0, 0, 0);
+            for (int mt = 0; mt < C::MTA; ++mt) anext[mt] = acur[mt];
+            if (tap < 8) {
+                bnext = bfrag(tap + 1);
+#pragma unroll
+                for (int mt = 0; mt < C::MTA; ++mt) anext[mt] = afrag(tap + 1, mt);
             }
+#pragma unroll
+            for (int mt = 0; mt < C::MTA; ++mt) acc[mt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(acur[mt], bcur, acc[mt], 0, 0, 0);
+            bcur = bnext;
+#pragma unroll
+            for (int mt = 0; mt < C::MTA; ++mt) acur[mt] = anext[mt];
         }
 
         // ---- t into this wave's P rows: rounded, activated, 4 channels per write ----
