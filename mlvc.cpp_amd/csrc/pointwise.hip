@@ -115,6 +115,21 @@ __global__ __launch_bounds__(kBlock) void depthwise3x3_row8_kernel(const std::ui
 #pragma unroll
     for (int r = 0; r < NR; ++r) asm volatile("" : "+v"(lft[r]), "+v"(rgt[r]));
     const float b = bias[ch];
+    const bool left_in = x0 > 0, right_in = x0 + 8 < wd;
+    // Each staged row converted to FP32 once and kept opaque, so the taps are
+    // plain FP32 multiply-adds rather than mixed-precision ones that convert
+    // the same pixel again for each of its taps.
+    float pxr[NR][10];  // input columns x0 - 1 .. x0 + 8 of each staged row
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        pxr[r][0] = keep(h2f(static_cast<std::uint16_t>(lft[r])));
+        pxr[r][9] = keep(h2f(static_cast<std::uint16_t>(rgt[r])));
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            pxr[r][1 + 2 * k] = keep(h2f(static_cast<std::uint16_t>(v[r][k] & 0xFFFFu)));
+            pxr[r][2 + 2 * k] = keep(h2f(static_cast<std::uint16_t>(v[r][k] >> 16)));
+        }
+    }
     // All rows are computed before the first store: loads and stores share
     // one in-order counter, so a store issued between two waits for loads
     // would make the second wait also wait for the store's write.
@@ -128,26 +143,23 @@ __global__ __launch_bounds__(kBlock) void depthwise3x3_row8_kernel(const std::ui
 #pragma unroll
         for (int ky = 0; ky < 3; ++ky) {
             const int r = orow + ky;
-            const bool row_in = oy - 1 + ky >= 0 && oy - 1 + ky < h;
-            // Converted once and kept opaque, so the taps are plain FP32
-            // multiply-adds rather than mixed-precision ones that convert
-            // the same pixel again for each of its three taps.
-            float px[10];  // input columns x0 - 1 .. x0 + 8
-            px[0] = keep(h2f(static_cast<std::uint16_t>(lft[r])));
-            px[9] = keep(h2f(static_cast<std::uint16_t>(rgt[r])));
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                px[1 + 2 * k] = keep(h2f(static_cast<std::uint16_t>(v[r][k] & 0xFFFFu)));
-                px[2 + 2 * k] = keep(h2f(static_cast<std::uint16_t>(v[r][k] >> 16)));
-            }
+            // Rows outside the image are skipped as a whole; within a row only
+            // the two edge taps (column x0 - 1 at the left border, x0 + 8 at
+            // the right one, x0 being a multiple of 8) can fall outside, so
+            // every other tap is an unconditional multiply-add.
+            if (oy - 1 + ky < 0 || oy - 1 + ky >= h) continue;
+            const float* px = pxr[r];
 #pragma unroll
             for (int kx = 0; kx < 3; ++kx) {
                 const float wv = keep(h2f(static_cast<std::uint16_t>(tap[ky * 3 + kx])));
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    const int ix = x0 + j - 1 + kx;
-                    const bool in = row_in && ix >= 0 && ix < wd;
-                    acc[j] = in ? fmaf(px[j + kx], wv, acc[j]) : acc[j];
+                    if (j == 0 && kx == 0)
+                        acc[j] = left_in ? fmaf(px[j + kx], wv, acc[j]) : acc[j];
+                    else if (j == 7 && kx == 2)
+                        acc[j] = right_in ? fmaf(px[j + kx], wv, acc[j]) : acc[j];
+                    else
+                        acc[j] = fmaf(px[j + kx], wv, acc[j]);
                 }
             }
         }
