@@ -152,6 +152,43 @@ def test_mlvc_1920x1088_free_running(tmp_path):
     gpu.close()
 
 
+# A second tiling of every tuned conv of the 1920x1088 graph, forced through a
+# tuning file: earlier recorded choices and a fresh re-tune's picks (other
+# tile shapes, pass widths, occupancies and kernels than the recorded file's),
+# each taking the same channel-last or NCHW operands. A tile changes the
+# timing, never the bits, so the frames hash as the golden file's.
+SECOND_TILING_1920 = {
+    "n6_conv3x3": "ws_bm128_2x32_k3x3_s2_sc32_occ4_w4",
+    "n8_conv3x3": "ws_bm128_2x32_k3x3_s2_sc64_occ2_w4",
+    "n10_conv3x3": "ws_bm256_2x32_k3x3_s2_sc64_occ2_w8_r9",
+    "n72_conv3x3": "ws_bm128_4x24_k3x3_s1_sc64_occ2_r9",
+    "n75_conv3x3": "ws_bm128_4x48_k3x3_s1_sc32_occ2_r9_pipe",
+    "n78_conv3x3": "ws_bm128_8x32_k3x3_s1_sc64_occ2",
+    "n81_conv3x3": "mfma_bm32_4x64_k3x3_s1_kc16_occ4",
+}
+
+
+def test_mlvc_1920x1088_second_tiling_same_frames(tmp_path, monkeypatch):
+    golden = json.loads(GOLDEN_1920.read_text())["frames"]
+    config = "mlvc_1920x1088"
+    tiles = tmp_path / "second_tiling.txt"
+    tiles.write_text("".join(f"{config}:{k} {v}\n" for k, v in SECOND_TILING_1920.items()))
+    monkeypatch.setenv("MLVC_HIP_TUNE_FILE", str(tiles))
+    monkeypatch.delenv("MLVC_HIP_TUNE_WRITE", raising=False)
+    bindings, _ = _write(tmp_path, config)
+    gpu = mlvc_hip.Backend(tmp_path, "hip")
+    gpu.load(config, bindings)
+    kinds = {l["name"]: l["kind"] for l in gpu.launches()}
+    for name, variant in SECOND_TILING_1920.items():
+        assert kinds[name].startswith(variant + "+"), (name, kinds[name])
+    gpu.reset_state()
+    for f, g in enumerate(golden):
+        got = gpu.run([mlvc_hip.synth_input(config, 0, f, gpu.in_shapes[0])])[0]
+        print(f"{config} second tiling frame {f}: {_sha(got)[:16]}", flush=True)
+        assert _sha(got) == g["sha256"], f"{config} frame {f}: not the isa-2 oracle's frame"
+    gpu.close()
+
+
 def test_device_resident_replay_matches_run(tmp_path):
     """Frames replayed from HBM (the bench path) produce the same outputs as
     run() on the same inputs."""
