@@ -187,6 +187,34 @@ def test_buffered_encoder_then_decoder(pair, frame_wh):
         b.close()
 
 
+def test_codec_graphs_are_the_oracle_gpu_arithmetic(pair):
+    """Encoder then decoder over 4 frames, each backend carrying its own
+    recurrent state: every output of both graphs equals the isa-2 oracle
+    plan's (the matrix core's summation order) bit for bit, so their
+    difference from the reference order (held to the FP16 bar above) is
+    summation order alone."""
+    d, bindings = pair
+    rng = np.random.default_rng(5)
+    q = np.array([3], np.int32)
+    enc, dec = backend(d, "MLVCEncoder", bindings), backend(d, "MLVCDecoder", bindings)
+    model_enc = O.OraclePlan(d, "MLVCEncoder", bindings, isa=2)
+    model_dec = O.OraclePlan(d, "MLVCDecoder", bindings, isa=2)
+    for b in (enc, dec, model_enc, model_dec):
+        b.reset_state()
+    for i in range(4):
+        f = rng.integers(0, 256, O.yuv_frame_bytes(MW, MH), dtype=np.uint8)
+        x = O.yuv_to_model(f, MW, MH, MW, MH, 0, 1.0).reshape(1, 3, MH, MW)
+        got, want = enc.run([x, q]), model_enc.run([x, q])
+        for k, (g, w) in enumerate(zip(got, want)):
+            assert np.array_equal(g, w), f"encoder frame {i} output {k}: {np.count_nonzero(g != w)} of {g.size} differ"
+        ys = got[0].reshape(1, 256, MH // 16, MW // 16)
+        got, want = dec.run([ys, q]), model_dec.run([ys, q])
+        for k, (g, w) in enumerate(zip(got, want)):
+            assert np.array_equal(g, w), f"decoder frame {i} output {k}: {np.count_nonzero(g != w)} of {g.size} differ"
+    enc.close()
+    dec.close()
+
+
 def test_buffered_contract(pair):
     d, bindings = pair
     enc = backend(d, "MLVCEncoder", bindings)
