@@ -408,6 +408,34 @@ def test_realops_recurrent(tmp_path, cfg):
             _check_realops(got, want, f"{cfg} frame {f}")
 
 
+@pytest.mark.parametrize("cfg,max_frames", [("realops_tiny", 3), ("realops_odd_tiny", 2), ("realops_544x960", 2)])
+def test_realops_are_the_oracle_gpu_arithmetic(tmp_path, cfg, max_frames):
+    """The realops graphs, each side carrying its own recurrent state,
+    against the isa-2 oracle plan (its convs summed in the matrix core's
+    order, everything else as the reference plan): every output of every
+    frame bit for bit, those downstream of ROUND included, so the tolerances
+    against the reference order above are summation order alone."""
+    mlvc_hip.synth_write(cfg, tmp_path, 0)
+    bindings, frames = mlvc_hip.synth_bindings(cfg)
+    frames = min(frames, max_frames)
+    model = O.OraclePlan(tmp_path, cfg, bindings, isa=2)
+    with mlvc_hip.Backend(tmp_path, "hip") as gpu:
+        gpu.load(cfg, bindings)
+        gpu.reset_state()
+        model.reset_state()
+        rng = np.random.default_rng(9)
+        bad = []
+        for f in range(frames):
+            ins = _inputs(gpu.in_shapes, rng, f)
+            got, want = gpu.run(ins), model.run(ins)
+            for i, (g, w) in enumerate(zip(got, want)):
+                n = int(np.count_nonzero(g != w))
+                print(f"{cfg} frame {f} output {i}: {n} of {g.size} differ from the isa-2 oracle", flush=True)
+                if n:
+                    bad.append((f, i, n))
+        assert not bad, bad
+
+
 def test_realops_fused_and_unfused_bit_identical(tmp_path, monkeypatch):
     cfg = "realops_tiny"
     mlvc_hip.synth_write(cfg, tmp_path, 0)
