@@ -36,6 +36,9 @@ def test_feedforward_configs(tmp_path, config):
     assert len(got) == len(want)
     for i, (g, w) in enumerate(zip(got, want)):
         assert_parity(g, w, f"{config} output {i}")
+    # Against the oracle's model of the matrix-core summation order: bit for bit.
+    for i, (g, w) in enumerate(zip(got, mlvc_oracle.OraclePlan(tmp_path, config, isa=2).run(ins))):
+        assert np.array_equal(g, w), f"{config} output {i}: {np.count_nonzero(g != w)} of {g.size} differ from isa 2"
     if config == "conv3x3_184x320":
         assert len(gpu.launches()) == 1  # conv + bias + LeakyReLU in one kernel
     gpu.close()
@@ -47,16 +50,19 @@ def test_recurrent_free_running(tmp_path, config, frames):
     gpu = mlvc_hip.Backend(tmp_path, "hip")
     gpu.load(config, bindings)
     ref = mlvc_oracle.OraclePlan(tmp_path, config, bindings)
+    model = mlvc_oracle.OraclePlan(tmp_path, config, bindings, isa=2)
     with pytest.raises(mlvc_hip.MlvcError, match="reset_state"):
         gpu.run([mlvc_hip.synth_input(config, 0, 0, gpu.in_shapes[0])])
     gpu.reset_state()
     ref.reset_state()
+    model.reset_state()
     first = None
     for f in range(frames):
         x = mlvc_hip.synth_input(config, 0, f, gpu.in_shapes[0])
         got, want = gpu.run([x]), ref.run([x])
         assert len(got) == 1  # the state output is bound, only recon is returned
         assert_parity(got[0], want[0], f"{config} frame {f}")
+        assert np.array_equal(got[0], model.run([x])[0]), f"{config} frame {f}: not the isa-2 oracle's frame"
         if f == 0:
             first = got[0].copy()
     # reset_state restores frame 0 exactly.
