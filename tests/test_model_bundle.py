@@ -246,8 +246,8 @@ def test_unparseable_files(tmp_path):
 
 
 def test_embedded_locations(tmp_path):
-    """model_assets.cpp: 'embedded:<profile>' selects the embedded reader, which this build does not link;
-    a malformed profile is rejected before that."""
+    """model_assets.cpp: 'embedded:<profile>' selects the embedded reader; a library linked without a model
+    image reports it with the reference's message, and a malformed profile is rejected before that."""
     assert "embedded models are disabled in this build (embedded:mlvc-psnr-v1)" in _error(
         mlvc_hip.model_config, "embedded:mlvc-psnr-v1")
     # A profile is one path component (model_assets.cpp:35-47).
