@@ -2,7 +2,7 @@
 reference CPU kernels built from source (oracle/_ref/libmlvc_ref_kernels.so).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
-bench.py's cpu_baseline leg, as the checker and the CPU baseline. The
+bench.py's cpu_baseline leg, as the parity reference and the CPU baseline. The
 product never imports this module.
 """
 
