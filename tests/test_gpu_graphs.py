@@ -174,19 +174,25 @@ SECOND_TILING_1920 = {
 }
 
 
-def test_mlvc_1920x1088_second_tiling_same_frames(tmp_path, monkeypatch):
+# With MLVC_HIP_BLOCK_HANDOVER=nchw every activation between launches stays
+# NCHW (no channel-last handover): the same bits again.
+@pytest.mark.parametrize("handover", ["channel_last", "nchw"])
+def test_mlvc_1920x1088_second_tiling_same_frames(tmp_path, monkeypatch, handover):
     golden = json.loads(GOLDEN_1920.read_text())["frames"]
     config = "mlvc_1920x1088"
     tiles = tmp_path / "second_tiling.txt"
     tiles.write_text("".join(f"{config}:{k} {v}\n" for k, v in SECOND_TILING_1920.items()))
     monkeypatch.setenv("MLVC_HIP_TUNE_FILE", str(tiles))
     monkeypatch.delenv("MLVC_HIP_TUNE_WRITE", raising=False)
+    if handover == "nchw":
+        monkeypatch.setenv("MLVC_HIP_BLOCK_HANDOVER", "nchw")
     bindings, _ = _write(tmp_path, config)
     gpu = mlvc_hip.Backend(tmp_path, "hip")
     gpu.load(config, bindings)
     kinds = {l["name"]: l["kind"] for l in gpu.launches()}
     for name, variant in SECOND_TILING_1920.items():
         assert kinds[name].startswith(variant + "+"), (name, kinds[name])
+    assert any("nhwc" in k for k in kinds.values()) == (handover == "channel_last"), kinds
     gpu.reset_state()
     for f, g in enumerate(golden):
         got = gpu.run([mlvc_hip.synth_input(config, 0, f, gpu.in_shapes[0])])[0]
