@@ -201,6 +201,26 @@ def test_mlvc_1920x1088_second_tiling_same_frames(tmp_path, monkeypatch, handove
     gpu.close()
 
 
+def test_mlvc_1920x1088_unfused_schedule_same_frames(tmp_path, monkeypatch):
+    """The 1920x1088 graph with every fusion off (one launch per node: the
+    unshuffle, concat, LeakyReLU, depthwise, 1x1, ADD and shuffle kernels of
+    their own) over the first 8 frames: the golden file's hashes again."""
+    golden = json.loads(GOLDEN_1920.read_text())["frames"][:8]
+    config = "mlvc_1920x1088"
+    monkeypatch.setenv("MLVC_HIP_DISABLE_FUSION", "1")
+    bindings, _ = _write(tmp_path, config)
+    gpu = mlvc_hip.Backend(tmp_path, "hip")
+    gpu.load(config, bindings)
+    kinds = " ".join(l["kind"] for l in gpu.launches())
+    assert "dwblock" not in kinds and "convpair" not in kinds, kinds
+    gpu.reset_state()
+    for f, g in enumerate(golden):
+        got = gpu.run([mlvc_hip.synth_input(config, 0, f, gpu.in_shapes[0])])[0]
+        print(f"{config} unfused frame {f}: {_sha(got)[:16]}", flush=True)
+        assert _sha(got) == g["sha256"], f"{config} frame {f}: not the isa-2 oracle's frame"
+    gpu.close()
+
+
 def test_device_resident_replay_matches_run(tmp_path):
     """Frames replayed from HBM (the bench path) produce the same outputs as
     run() on the same inputs."""
