@@ -164,10 +164,10 @@ def test_mlvc_1920x1088_free_running(tmp_path):
 # each taking the same channel-last or NCHW operands. A tile changes the
 # timing, never the bits, so the frames hash as the golden file's.
 SECOND_TILING_1920 = {
-    "n6_conv3x3": "ws_bm128_2x32_k3x3_s2_sc32_occ4_w4",
+    "n6_conv3x3": "ws_bm128_2x32_k3x3_s2_sc32_occ2_w4",
     "n8_conv3x3": "ws_bm128_2x32_k3x3_s2_sc64_occ2_w4",
     "n10_conv3x3": "ws_bm256_2x32_k3x3_s2_sc64_occ2_w8_r9",
-    "n72_conv3x3": "ws_bm128_4x24_k3x3_s1_sc64_occ2_r9",
+    "n72_conv3x3": "ws_bm128_4x24_k3x3_s1_sc32_occ2_r9_pipe",
     "n75_conv3x3": "ws_bm128_4x48_k3x3_s1_sc32_occ2_r9_pipe",
     "n78_conv3x3": "ws_bm128_8x32_k3x3_s1_sc64_occ2",
     "n81_conv3x3": "mfma_bm32_4x64_k3x3_s1_kc16_occ4",
