@@ -10,6 +10,7 @@ tuning-file choice keyed by launch name (not resolution) could name one.
 """
 
 import ctypes as C
+import pathlib
 
 import mlvc_hip
 
@@ -101,3 +102,31 @@ def test_split_rule():
     # plain one); a batch with enough work items is not split.
     assert plan(1024, 46, 80, 256, 1, 1, pad=0, epilogue=3)[0].ksplit == 8
     assert plan(1024, 46, 80, 256, 1, 1, pad=0, n=16)[0].ksplit <= 1
+
+
+# The tuned convs of the 1920x1088 graph: (launch, ic, h, w, oc, stride,
+# DEPTH_TO_SPACE block, channel-last input, channel-last output).
+TUNED_1920 = [
+    ("n6_conv3x3", 64, 544, 960, 128, 2, 0, 0, 1),
+    ("n8_conv3x3", 128, 272, 480, 192, 2, 0, 1, 1),
+    ("n10_conv3x3", 192, 136, 240, 256, 2, 0, 1, 1),
+    ("n72_conv3x3", 256, 68, 120, 768, 1, 2, 1, 1),
+    ("n75_conv3x3", 192, 136, 240, 512, 1, 2, 1, 1),
+    ("n78_conv3x3", 128, 272, 480, 256, 1, 2, 1, 0),
+    ("n81_conv3x3", 64, 544, 960, 12, 1, 2, 0, 0),
+]
+
+
+def test_recorded_tuning_names_candidates_of_each_launch():
+    """Every choice the recorded tuning file makes for the 1920x1088 graph is
+    a variant that can run that launch's geometry and operand layouts, so the
+    benchmark and the profiles run exactly the recorded tiles (a name that
+    could not would send the tuner back to timing the candidates)."""
+    path = pathlib.Path(__file__).resolve().parents[1] / "mlvc.cpp_amd" / "tuning" / "mi355x.txt"
+    chosen = dict(line.split() for line in path.read_text().splitlines() if line.strip())
+    for name, ic, h, w, oc, stride, d2s, cl_in, cl_out in TUNED_1920:
+        oh, ow = (h - 1) // stride + 1, (w - 1) // stride + 1
+        d = ConvDesc(n=1, ic=ic, ih=h, iw=w, oc=oc, oh=oh, ow=ow, kh=3, kw=3, stride_h=stride, stride_w=stride,
+                     pad_h=1, pad_w=1, epilogue=1, alpha=0.01, out_d2s_block=d2s, in_nhwc=cl_in, out_nhwc=cl_out)
+        names = candidates(ic, h, w, oc, stride=stride, d2s=d2s, desc=d)
+        assert chosen[f"mlvc_1920x1088:{name}"] in names, (name, chosen[f"mlvc_1920x1088:{name}"], names)
